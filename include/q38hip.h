@@ -1,0 +1,112 @@
+/* libq38hip: MI355X (gfx950) kernels for the Qwen3.8 decode hot path.
+ *
+ * C ABI only: plain pointers and sizes.  Two families of entry points:
+ *
+ *  1. Drop-in replacements for the reference kernel ABI
+ *     (include/qwen38/qwen38_quant.h:20-49 of shyringo/qwen3.8-27b-in-c):
+ *     same names, same argument meaning, same 1/0 return convention.  They
+ *     take HOST pointers, stage them through HBM and run the HIP kernels.
+ *
+ *  2. Device-resident variants (q38hip_*): every pointer, including
+ *     tensor->data, is a device pointer; work is enqueued on `stream`
+ *     (a hipStream_t; NULL means the legacy default stream) and the call
+ *     returns without synchronising.  Return 1 on success, 0 on an argument
+ *     error (message via q38hip_last_error()).
+ *
+ * Results are bit-identical to the reference's x86 AVX2 CPU kernels on the
+ * same inputs: integer block sums exactly, fp32 outputs in the reference's
+ * lane order.
+ */
+#ifndef Q38HIP_H
+#define Q38HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Layout-compatible with Q38Q8KBlock (include/qwen38/qwen38_quant.h:14-18). */
+#define Q38_Q8_K_BLOCK_SIZE 256
+typedef struct {
+    float scale;
+    int8_t quants[Q38_Q8_K_BLOCK_SIZE];
+    int16_t sums[Q38_Q8_K_BLOCK_SIZE / 16];
+} Q38Q8KBlock;
+
+/* Layout-compatible with Q38GGUFString / Q38GGUFTensor
+ * (include/qwen38/qwen38_gguf.h:57-77).  shape[0] = input width,
+ * shape[1] = output rows, type = GGML type id (Q4_K 12, Q6_K 14, IQ1_M 29). */
+typedef struct {
+    const char *data;
+    uint64_t length;
+} Q38GGUFString;
+
+typedef struct {
+    Q38GGUFString name;
+    uint32_t n_dims;
+    uint64_t shape[8];
+    uint32_t type;
+    uint64_t offset;
+    uint64_t nbytes;
+    const uint8_t *data;
+    void *iq1_s_repack;
+} Q38GGUFTensor;
+
+/* ---- 1. reference kernel ABI, host pointers ------------------------------ */
+
+/* replaces q38_f16_to_f32, include/qwen38/qwen38_quant.h:20 */
+float q38_f16_to_f32(uint16_t value);
+
+/* replaces q38_quantize_q8_k, include/qwen38/qwen38_quant.h:24-25 */
+int q38_quantize_q8_k(Q38Q8KBlock *output, const float *input,
+                      uint64_t length);
+
+/* replaces q38_tensor_gemv_q8_k, include/qwen38/qwen38_quant.h:38-40
+ * (Q4_K, Q6_K and IQ1_M tensors) */
+int q38_tensor_gemv_q8_k(float *output, const Q38Q8KBlock *input,
+                         uint64_t input_length,
+                         const Q38GGUFTensor *tensor);
+
+/* replaces q38_tensor_gemm_q8_k, include/qwen38/qwen38_quant.h:48-50;
+ * output is batch-major, output[token * rows + row] */
+int q38_tensor_gemm_q8_k(float *output, const Q38Q8KBlock *input,
+                         uint32_t batch_size, uint64_t input_length,
+                         const Q38GGUFTensor *tensor);
+
+/* ---- 2. device-resident variants ---------------------------------------- */
+
+/* Device form of q38_quantize_q8_k (src/qwen38/qwen38_quant.c:50-88):
+ * `rows` independent fp32 rows of `length` elements each. */
+int q38hip_quantize_q8_k(Q38Q8KBlock *output, const float *input,
+                         uint64_t length, uint32_t rows, void *stream);
+
+/* Device form of q38_tensor_gemm_q8_k (src/qwen38/qwen38_quant.c:2950-3169);
+ * batch_size = 1 is q38_tensor_gemv_q8_k (:2833-2922).  batch_size <= 8. */
+int q38hip_gemm_q8_k(float *output, const Q38Q8KBlock *input,
+                     uint32_t batch_size, uint64_t input_length,
+                     const Q38GGUFTensor *tensor, void *stream);
+
+/* Row-wise first-maximum index (q38_argmax, src/qwen38/qwen38_model.c:
+ * 1228-1239) of `rows` rows of `count` floats; index_out[rows]. */
+int q38hip_argmax(uint32_t *index_out, const float *values, uint32_t count,
+                  uint32_t rows, void *stream);
+
+/* Greedy acceptance of a verify batch (src/qwen38/qwen38_model.c:1662-1702):
+ * targets[rows] are the per-row argmaxes, drafts[rows] the draft ids.
+ * result[0] = consumed, result[1] = matched, result[2] = next,
+ * result[3 .. 3+consumed) = accepted tokens.  result needs rows + 3 words. */
+int q38hip_accept(uint32_t *result, const uint32_t *targets,
+                  const uint32_t *drafts, uint32_t rows, void *stream);
+
+/* Last argument error of the calling thread ("" when none). */
+const char *q38hip_last_error(void);
+
+/* Synchronise the device; returns 1 when no HIP error is pending. */
+int q38hip_synchronize(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

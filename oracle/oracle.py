@@ -1,0 +1,200 @@
+"""ctypes front end for the CPU checkers -- TEST INFRASTRUCTURE ONLY.
+
+* ``Oracle``  wraps oracle/liboracle.so, our C restatement of the reference
+  kernels (q38_oracle.c, each function citing the reference lines it follows).
+* ``Reference`` wraps oracle/_ref/libq38ref.so, the reference's own C sources
+  compiled where they lie (oracle/Makefile), when that library was built.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module.  The product library never does.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libq38ref.so")
+
+Q4_K, Q6_K, IQ1_M = 12, 14, 29
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, IQ1_M: 56}
+
+# Q38Q8KBlock (include/qwen38/qwen38_quant.h:14-18): 292 bytes, no padding.
+Q8K_DTYPE = np.dtype([("scale", "<f4"), ("quants", "i1", (256,)), ("sums", "<i2", (16,))])
+assert Q8K_DTYPE.itemsize == 292
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+
+
+def _ptr(array):
+    return ctypes.c_void_p(array.ctypes.data)
+
+
+class GGUFString(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_char_p), ("length", ctypes.c_uint64)]
+
+
+class GGUFTensor(ctypes.Structure):
+    """Q38GGUFTensor (include/qwen38/qwen38_gguf.h:68-77)."""
+    _fields_ = [("name", GGUFString), ("n_dims", ctypes.c_uint32),
+                ("shape", ctypes.c_uint64 * 8), ("type", ctypes.c_uint32),
+                ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64),
+                ("data", ctypes.c_void_p), ("iq1_s_repack", ctypes.c_void_p)]
+
+
+def make_tensor(data, qtype, width, rows):
+    tensor = GGUFTensor()
+    tensor.n_dims = 2
+    tensor.shape[0] = width
+    tensor.shape[1] = rows
+    tensor.type = qtype
+    tensor.nbytes = data.nbytes
+    tensor.data = data.ctypes.data
+    return tensor
+
+
+class Oracle:
+    def __init__(self, path=ORACLE_SO):
+        if not os.path.exists(path):
+            raise RuntimeError("oracle library missing: run make -C oracle")
+        lib = ctypes.CDLL(path)
+        lib.orc_f16_to_f32.restype = ctypes.c_float
+        lib.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        lib.orc_nearest_int.restype = ctypes.c_int
+        lib.orc_nearest_int.argtypes = [ctypes.c_float]
+        lib.orc_quantize_q8_k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64]
+        lib.orc_block_ints.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        lib.orc_gemv_q8_k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                                      ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint64]
+        lib.orc_gemm_q8_k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64,
+                                      ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint64]
+        lib.orc_row_f32.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p,
+                                    ctypes.c_uint64, ctypes.c_uint64]
+        lib.orc_argmax.restype = ctypes.c_uint32
+        lib.orc_argmax.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
+        lib.orc_accept.restype = ctypes.c_uint32
+        lib.orc_accept.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
+                                   _u32p, _u32p, ctypes.c_void_p]
+        lib.orc_iq1m_grid_entry.argtypes = [ctypes.c_uint32, ctypes.c_void_p]
+        lib.orc_attention_decode.argtypes = [ctypes.c_void_p] * 8 + [ctypes.c_uint32]
+        self.lib = lib
+
+    def f16_to_f32(self, bits):
+        return self.lib.orc_f16_to_f32(int(bits))
+
+    def quantize(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros(x.size // 256, dtype=Q8K_DTYPE)
+        if not self.lib.orc_quantize_q8_k(_ptr(out), _ptr(x), x.size):
+            raise ValueError("length must be a multiple of 256")
+        return out
+
+    def block_ints(self, qtype, block, q8k_block):
+        ints = np.zeros(12, dtype=np.int32)
+        n = self.lib.orc_block_ints(qtype, _ptr(block), _ptr(q8k_block), _ptr(ints))
+        return ints[:n]
+
+    def gemv(self, qtype, data, rows, q8k):
+        out = np.zeros(rows, dtype=np.float32)
+        if not self.lib.orc_gemv_q8_k(_ptr(out), _ptr(q8k), q8k.size * 256, qtype, _ptr(data), rows):
+            raise ValueError("bad GEMV arguments")
+        return out
+
+    def gemm(self, qtype, data, rows, q8k, batch):
+        out = np.zeros(batch * rows, dtype=np.float32)
+        width = q8k.size // batch * 256
+        if not self.lib.orc_gemm_q8_k(_ptr(out), _ptr(q8k), batch, width, qtype, _ptr(data), rows):
+            raise ValueError("bad GEMM arguments")
+        return out.reshape(batch, rows)
+
+    def row_f32(self, qtype, data, width, row):
+        out = np.zeros(width, dtype=np.float32)
+        if not self.lib.orc_row_f32(_ptr(out), qtype, _ptr(data), width, row):
+            raise ValueError("unsupported row type")
+        return out
+
+    def argmax(self, values):
+        values = np.ascontiguousarray(values, dtype=np.float32)
+        return int(self.lib.orc_argmax(_ptr(values), values.size))
+
+    def accept(self, batch_logits, drafts):
+        batch_logits = np.ascontiguousarray(batch_logits, dtype=np.float32)
+        drafts = np.ascontiguousarray(drafts, dtype=np.uint32)
+        rows, count = batch_logits.shape
+        matched, nxt = ctypes.c_uint32(), ctypes.c_uint32()
+        accepted = np.zeros(rows, dtype=np.uint32)
+        consumed = self.lib.orc_accept(_ptr(batch_logits), rows, count, _ptr(drafts),
+                                       ctypes.byref(matched), ctypes.byref(nxt), _ptr(accepted))
+        return int(consumed), int(matched.value), int(nxt.value), accepted[:consumed].copy()
+
+    def grid_entry(self, index):
+        out = np.zeros(8, dtype=np.int8)
+        self.lib.orc_iq1m_grid_entry(index, _ptr(out))
+        return out
+
+    def attention_decode(self, q_and_gate, key, value, key_cache, value_cache, q_norm, k_norm, position):
+        """Returns the gated attention output [6144]; updates the caches in place."""
+        out = np.zeros(6144, dtype=np.float32)
+        args = [np.ascontiguousarray(a, dtype=np.float32) for a in (q_and_gate, key, value, q_norm, k_norm)]
+        assert key_cache.dtype == np.float32 and value_cache.dtype == np.float32
+        self.lib.orc_attention_decode(_ptr(out), _ptr(args[0]), _ptr(args[1]), _ptr(args[2]),
+                                      _ptr(key_cache), _ptr(value_cache), _ptr(args[3]), _ptr(args[4]),
+                                      position)
+        return out
+
+
+class Reference:
+    """The reference's compiled C kernels (oracle/_ref), when present."""
+
+    def __init__(self, path=REF_SO):
+        if not os.path.exists(path):
+            raise RuntimeError("reference library not built (oracle/_ref)")
+        lib = ctypes.CDLL(path)
+        lib.q38_f16_to_f32.restype = ctypes.c_float
+        lib.q38_f16_to_f32.argtypes = [ctypes.c_uint16]
+        lib.q38_quantize_q8_k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64]
+        lib.q38_tensor_gemv_q8_k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                                             ctypes.POINTER(GGUFTensor)]
+        lib.q38_tensor_gemm_q8_k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
+                                             ctypes.c_uint64, ctypes.POINTER(GGUFTensor)]
+        lib.q38_tensor_row_f32.argtypes = [ctypes.c_void_p, ctypes.POINTER(GGUFTensor), ctypes.c_uint64]
+        self.lib = lib
+
+    @staticmethod
+    def available(path=REF_SO):
+        return os.path.exists(path)
+
+    def f16_to_f32(self, bits):
+        return self.lib.q38_f16_to_f32(int(bits))
+
+    def quantize(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros(x.size // 256, dtype=Q8K_DTYPE)
+        if not self.lib.q38_quantize_q8_k(_ptr(out), _ptr(x), x.size):
+            raise ValueError("length must be a multiple of 256")
+        return out
+
+    def gemv(self, qtype, data, rows, q8k):
+        width = q8k.size * 256
+        tensor = make_tensor(data, qtype, width, rows)
+        out = np.zeros(rows, dtype=np.float32)
+        if not self.lib.q38_tensor_gemv_q8_k(_ptr(out), _ptr(q8k), width, ctypes.byref(tensor)):
+            raise ValueError("bad GEMV arguments")
+        return out
+
+    def gemm(self, qtype, data, rows, q8k, batch):
+        width = q8k.size // batch * 256
+        tensor = make_tensor(data, qtype, width, rows)
+        out = np.zeros(batch * rows, dtype=np.float32)
+        if not self.lib.q38_tensor_gemm_q8_k(_ptr(out), _ptr(q8k), batch, width, ctypes.byref(tensor)):
+            raise ValueError("bad GEMM arguments")
+        return out.reshape(batch, rows)
+
+    def row_f32(self, qtype, data, width, row, rows):
+        tensor = make_tensor(data, qtype, width, rows)
+        out = np.zeros(width, dtype=np.float32)
+        if not self.lib.q38_tensor_row_f32(_ptr(out), ctypes.byref(tensor), row):
+            raise ValueError("row decode failed")
+        return out

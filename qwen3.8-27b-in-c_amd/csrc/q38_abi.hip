@@ -1,0 +1,262 @@
+/* C ABI of libq38hip (declared in include/q38hip.h). */
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "q38hip.h"
+#include "q38_device.h"
+#include "q38_iq1m_grid.inc"
+
+namespace q38 {
+bool launch_gemm(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows,
+                 uint32_t nblk, const uint32_t *grid, hipStream_t stream);
+void launch_quantize(const float *x, uint8_t *out, uint32_t nblocks, hipStream_t stream);
+uint32_t argmax_chunks(uint32_t count);
+void launch_argmax(const float *values, uint32_t count, uint32_t rows, float *pv, uint32_t *pi,
+                   uint32_t *out, hipStream_t stream);
+void launch_accept(uint32_t *result, const uint32_t *targets, const uint32_t *drafts, uint32_t rows,
+                   hipStream_t stream);
+}  // namespace q38
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(const char *message)
+{
+    g_error = message;
+    return 0;
+}
+
+/* Per-device constant state: the IQ1_M codebook in the nibble-pair form the
+ * GEMM kernel stages into LDS, and a growable argmax partials buffer. */
+struct DeviceState {
+    uint32_t *grid = nullptr;
+    float *argmax_values = nullptr;
+    uint32_t *argmax_index = nullptr;
+    size_t argmax_capacity = 0;
+};
+
+std::mutex g_mutex;
+std::vector<DeviceState> g_devices;
+
+DeviceState *device_state()
+{
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if ((int)g_devices.size() <= device) g_devices.resize(device + 1);
+    DeviceState &s = g_devices[device];
+    if (!s.grid) {
+        uint32_t host[2048];
+        for (int e = 0; e < 2048; ++e) {
+            const uint32_t code = q38_iq1m_grid_codes[e];
+            uint32_t word = 0;
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lo = (code >> (2 * i)) & 3u;        /* element i, value + 1 */
+                const uint32_t hi = (code >> (2 * (4 + i))) & 3u;  /* element 4 + i */
+                word |= (lo | hi << 4) << (8 * i);
+            }
+            host[e] = word;
+        }
+        if (hipMalloc(&s.grid, sizeof(host)) != hipSuccess) return nullptr;
+        if (hipMemcpy(s.grid, host, sizeof(host), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+    }
+    return &s;
+}
+
+bool supported_type(uint32_t type)
+{
+    return type == q38::kQ4K || type == q38::kQ6K || type == q38::kIQ1M;
+}
+
+uint64_t block_bytes(uint32_t type)
+{
+    switch (type) {
+    case q38::kQ4K: return 144;
+    case q38::kQ6K: return 210;
+    case q38::kIQ1M: return 56;
+    default: return 0;
+    }
+}
+
+/* Argument checks of q38_tensor_gemm_q8_k (src/qwen38/qwen38_quant.c:2950-2974). */
+int check_gemm(const void *output, const void *input, uint32_t batch, uint64_t input_length,
+               const Q38GGUFTensor *tensor)
+{
+    if (!output || !input || !batch || !tensor) return fail("null argument");
+    if (tensor->n_dims != 2) return fail("tensor must be 2-D");
+    if (tensor->shape[0] != input_length) return fail("tensor width differs from input length");
+    if (input_length % Q38_Q8_K_BLOCK_SIZE) return fail("input length is not a multiple of 256");
+    if (!supported_type(tensor->type)) return fail("tensor type is not Q4_K, Q6_K or IQ1_M");
+    if (!tensor->data) return fail("tensor has no data");
+    if (batch > 8) return fail("batch_size above 8");
+    if (tensor->shape[1] == 0 || tensor->shape[1] > 0xffffffffull) return fail("bad row count");
+    if (input_length / 256 > 0xffffffffull) return fail("input too long");
+    return 1;
+}
+
+struct DeviceBuffer {
+    void *ptr = nullptr;
+    explicit DeviceBuffer(size_t bytes)
+    {
+        if (bytes && hipMalloc(&ptr, bytes) != hipSuccess) ptr = nullptr;
+    }
+    ~DeviceBuffer()
+    {
+        if (ptr) (void)hipFree(ptr);
+    }
+    DeviceBuffer(const DeviceBuffer &) = delete;
+    DeviceBuffer &operator=(const DeviceBuffer &) = delete;
+};
+
+}  // namespace
+
+extern "C" {
+
+const char *q38hip_last_error(void) { return g_error.c_str(); }
+
+int q38hip_synchronize(void)
+{
+    const hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return fail(hipGetErrorString(e));
+    return 1;
+}
+
+float q38_f16_to_f32(uint16_t value)
+{
+    const uint32_t sign = (uint32_t)(value & 0x8000u) << 16;
+    const uint32_t exponent = (value >> 10) & 31u;
+    uint32_t mantissa = value & 1023u;
+    uint32_t bits;
+    if (exponent == 0) {
+        if (mantissa == 0) {
+            bits = sign;
+        } else {
+            uint32_t e = 113;
+            while (!(mantissa & 0x400u)) { mantissa <<= 1; --e; }
+            bits = sign | e << 23 | (mantissa & 0x3ffu) << 13;
+        }
+    } else if (exponent == 31) {
+        bits = sign | 0x7f800000u | mantissa << 13;
+    } else {
+        bits = sign | (exponent + 112u) << 23 | mantissa << 13;
+    }
+    float out;
+    std::memcpy(&out, &bits, 4);
+    return out;
+}
+
+int q38hip_quantize_q8_k(Q38Q8KBlock *output, const float *input, uint64_t length, uint32_t rows,
+                         void *stream)
+{
+    if (!output || !input) return fail("null argument");
+    if (length % Q38_Q8_K_BLOCK_SIZE) return fail("length is not a multiple of 256");
+    const uint64_t blocks = length / Q38_Q8_K_BLOCK_SIZE * rows;
+    if (blocks == 0) return 1;
+    if (blocks > 0xffffffffull / 4) return fail("input too long");
+    q38::launch_quantize(input, reinterpret_cast<uint8_t *>(output), (uint32_t)blocks,
+                         static_cast<hipStream_t>(stream));
+    return 1;
+}
+
+int q38hip_gemm_q8_k(float *output, const Q38Q8KBlock *input, uint32_t batch_size, uint64_t input_length,
+                     const Q38GGUFTensor *tensor, void *stream)
+{
+    if (!check_gemm(output, input, batch_size, input_length, tensor)) return 0;
+    DeviceState *state = device_state();
+    if (!state) return fail("device initialisation failed");
+    const bool ok = q38::launch_gemm((int)tensor->type, (int)batch_size, tensor->data,
+                                     reinterpret_cast<const uint8_t *>(input), output,
+                                     (uint32_t)tensor->shape[1], (uint32_t)(input_length / 256),
+                                     state->grid, static_cast<hipStream_t>(stream));
+    return ok ? 1 : fail("unsupported GEMM configuration");
+}
+
+int q38hip_argmax(uint32_t *index_out, const float *values, uint32_t count, uint32_t rows, void *stream)
+{
+    if (!index_out || !values || !count || !rows) return fail("bad argmax arguments");
+    DeviceState *state = device_state();
+    if (!state) return fail("device initialisation failed");
+    const size_t need = (size_t)q38::argmax_chunks(count) * rows;
+    {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        if (state->argmax_capacity < need) {
+            if (state->argmax_values) (void)hipFree(state->argmax_values);
+            if (state->argmax_index) (void)hipFree(state->argmax_index);
+            state->argmax_values = nullptr;
+            state->argmax_index = nullptr;
+            state->argmax_capacity = 0;
+            if (hipMalloc(&state->argmax_values, need * sizeof(float)) != hipSuccess ||
+                hipMalloc(&state->argmax_index, need * sizeof(uint32_t)) != hipSuccess)
+                return fail("argmax scratch allocation failed");
+            state->argmax_capacity = need;
+        }
+    }
+    q38::launch_argmax(values, count, rows, state->argmax_values, state->argmax_index, index_out,
+                       static_cast<hipStream_t>(stream));
+    return 1;
+}
+
+int q38hip_accept(uint32_t *result, const uint32_t *targets, const uint32_t *drafts, uint32_t rows,
+                  void *stream)
+{
+    if (!result || !targets || !drafts || !rows) return fail("bad acceptance arguments");
+    q38::launch_accept(result, targets, drafts, rows, static_cast<hipStream_t>(stream));
+    return 1;
+}
+
+/* ---- host-pointer drop-ins for the reference kernel ABI ------------------ */
+
+int q38_quantize_q8_k(Q38Q8KBlock *output, const float *input, uint64_t length)
+{
+    if (!output || !input || length % Q38_Q8_K_BLOCK_SIZE) return fail("bad quantize arguments");
+    if (length == 0) return 1;
+    const uint64_t blocks = length / Q38_Q8_K_BLOCK_SIZE;
+    DeviceBuffer din(length * sizeof(float)), dout(blocks * sizeof(Q38Q8KBlock));
+    if (!din.ptr || !dout.ptr) return fail("device allocation failed");
+    if (hipMemcpy(din.ptr, input, length * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+        return fail("copy to device failed");
+    if (!q38hip_quantize_q8_k(static_cast<Q38Q8KBlock *>(dout.ptr), static_cast<const float *>(din.ptr),
+                              length, 1, nullptr))
+        return 0;
+    if (hipMemcpy(output, dout.ptr, blocks * sizeof(Q38Q8KBlock), hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("copy from device failed");
+    return 1;
+}
+
+int q38_tensor_gemm_q8_k(float *output, const Q38Q8KBlock *input, uint32_t batch_size,
+                         uint64_t input_length, const Q38GGUFTensor *tensor)
+{
+    if (!check_gemm(output, input, batch_size, input_length, tensor)) return 0;
+    const uint64_t rows = tensor->shape[1];
+    const uint64_t blocks = input_length / 256;
+    const uint64_t wbytes = rows * blocks * block_bytes(tensor->type);
+    const uint64_t xbytes = (uint64_t)batch_size * blocks * sizeof(Q38Q8KBlock);
+    const uint64_t ybytes = (uint64_t)batch_size * rows * sizeof(float);
+    DeviceBuffer dw(wbytes), dx(xbytes), dy(ybytes);
+    if (!dw.ptr || !dx.ptr || !dy.ptr) return fail("device allocation failed");
+    if (hipMemcpy(dw.ptr, tensor->data, wbytes, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(dx.ptr, input, xbytes, hipMemcpyHostToDevice) != hipSuccess)
+        return fail("copy to device failed");
+    Q38GGUFTensor dev = *tensor;
+    dev.data = static_cast<const uint8_t *>(dw.ptr);
+    if (!q38hip_gemm_q8_k(static_cast<float *>(dy.ptr), static_cast<const Q38Q8KBlock *>(dx.ptr), batch_size,
+                          input_length, &dev, nullptr))
+        return 0;
+    if (hipMemcpy(output, dy.ptr, ybytes, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("copy from device failed");
+    return 1;
+}
+
+int q38_tensor_gemv_q8_k(float *output, const Q38Q8KBlock *input, uint64_t input_length,
+                         const Q38GGUFTensor *tensor)
+{
+    return q38_tensor_gemm_q8_k(output, input, 1, input_length, tensor);
+}
+
+}  // extern "C"

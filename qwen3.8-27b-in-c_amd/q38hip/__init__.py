@@ -1,0 +1,179 @@
+"""Python host binding of libq38hip (the gfx950 decode hot path).
+
+Thin ctypes layer over the C ABI in include/q38hip.h.  Device memory and
+streams come from PyTorch (ROCm build); every computation runs in the HIP
+kernels of libq38hip.so.  There is no CPU fallback: importing this module
+without the built library raises.
+
+Names mirror the reference kernel ABI (include/qwen38/qwen38_quant.h of
+shyringo/qwen3.8-27b-in-c): quantize_q8_k, tensor_gemv_q8_k,
+tensor_gemm_q8_k, plus device-resident forms that take torch tensors.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+PACKAGE_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PACKAGE_DIR, "libq38hip.so")
+
+Q4_K, Q6_K, IQ1_M = 12, 14, 29
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, IQ1_M: 56}
+Q8K_BYTES = 292
+Q8K_DTYPE = np.dtype([("scale", "<f4"), ("quants", "i1", (256,)), ("sums", "<i2", (16,))])
+
+
+class GGUFString(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_char_p), ("length", ctypes.c_uint64)]
+
+
+class GGUFTensor(ctypes.Structure):
+    """Q38GGUFTensor: shape[0] = input width, shape[1] = rows."""
+    _fields_ = [("name", GGUFString), ("n_dims", ctypes.c_uint32),
+                ("shape", ctypes.c_uint64 * 8), ("type", ctypes.c_uint32),
+                ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64),
+                ("data", ctypes.c_void_p), ("iq1_s_repack", ctypes.c_void_p)]
+
+
+def make_tensor(data_ptr, qtype, width, rows, nbytes=0):
+    tensor = GGUFTensor()
+    tensor.n_dims = 2
+    tensor.shape[0] = width
+    tensor.shape[1] = rows
+    tensor.type = qtype
+    tensor.nbytes = nbytes
+    tensor.data = data_ptr
+    return tensor
+
+
+# Every symbol the C header declares (tests check the library exports them).
+EXPORTS = ("q38_f16_to_f32", "q38_quantize_q8_k", "q38_tensor_gemv_q8_k", "q38_tensor_gemm_q8_k",
+           "q38hip_quantize_q8_k", "q38hip_gemm_q8_k", "q38hip_argmax", "q38hip_accept",
+           "q38hip_last_error", "q38hip_synchronize")
+
+
+def load_library(path=LIB_PATH):
+    if not os.path.exists(path):
+        raise RuntimeError("libq38hip.so is not built (run __graft_entry__.build() or "
+                           "make -C qwen3.8-27b-in-c_amd)")
+    lib = ctypes.CDLL(path)
+    vp, u32, u64 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64
+    lib.q38_f16_to_f32.restype = ctypes.c_float
+    lib.q38_f16_to_f32.argtypes = [ctypes.c_uint16]
+    lib.q38_quantize_q8_k.argtypes = [vp, vp, u64]
+    lib.q38_tensor_gemv_q8_k.argtypes = [vp, vp, u64, ctypes.POINTER(GGUFTensor)]
+    lib.q38_tensor_gemm_q8_k.argtypes = [vp, vp, u32, u64, ctypes.POINTER(GGUFTensor)]
+    lib.q38hip_quantize_q8_k.argtypes = [vp, vp, u64, u32, vp]
+    lib.q38hip_gemm_q8_k.argtypes = [vp, vp, u32, u64, ctypes.POINTER(GGUFTensor), vp]
+    lib.q38hip_argmax.argtypes = [vp, vp, u32, u32, vp]
+    lib.q38hip_accept.argtypes = [vp, vp, vp, u32, vp]
+    lib.q38hip_last_error.restype = ctypes.c_char_p
+    lib.q38hip_last_error.argtypes = []
+    lib.q38hip_synchronize.argtypes = []
+    return lib
+
+
+_LIB = None
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        _LIB = load_library()
+    return _LIB
+
+
+def last_error():
+    return lib().q38hip_last_error().decode()
+
+
+def _check(ok, what):
+    if not ok:
+        raise RuntimeError("%s failed: %s" % (what, last_error()))
+
+
+def _stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev_ptr(tensor):
+    if not tensor.is_cuda:
+        raise ValueError("expected a device tensor")
+    if not tensor.is_contiguous():
+        raise ValueError("expected a contiguous tensor")
+    return ctypes.c_void_p(tensor.data_ptr())
+
+
+# ---- device-resident API (torch tensors on the GPU) --------------------------
+
+def quantize_q8_k(x):
+    """x: float32 [rows, length] (or [length]) on the GPU -> uint8 Q8_K blocks."""
+    import torch
+    if x.dtype != torch.float32:
+        raise ValueError("expected float32 input")
+    rows = x.shape[0] if x.dim() == 2 else 1
+    length = x.shape[-1]
+    out = torch.empty(rows * (length // 256) * Q8K_BYTES, dtype=torch.uint8, device=x.device)
+    _check(lib().q38hip_quantize_q8_k(_dev_ptr(out), _dev_ptr(x), length, rows, _stream()),
+           "q38hip_quantize_q8_k")
+    return out
+
+
+def gemm_q8_k(weights, qtype, width, rows, xq, batch, out=None):
+    """weights: uint8 GGUF rows on the GPU; xq: batch * width/256 Q8_K blocks.
+    Returns float32 [batch, rows] (batch-major, as the reference GEMM)."""
+    import torch
+    if out is None:
+        out = torch.empty((batch, rows), dtype=torch.float32, device=weights.device)
+    tensor = make_tensor(weights.data_ptr(), qtype, width, rows, weights.numel())
+    _check(lib().q38hip_gemm_q8_k(_dev_ptr(out), _dev_ptr(xq), batch, width, ctypes.byref(tensor),
+                                  _stream()), "q38hip_gemm_q8_k")
+    return out
+
+
+def argmax(values):
+    """values: float32 [rows, count] on the GPU -> int32 [rows] first-max indices."""
+    import torch
+    values2 = values if values.dim() == 2 else values.reshape(1, -1)
+    out = torch.empty(values2.shape[0], dtype=torch.int32, device=values.device)
+    _check(lib().q38hip_argmax(_dev_ptr(out), _dev_ptr(values2), values2.shape[1], values2.shape[0],
+                               _stream()), "q38hip_argmax")
+    return out
+
+
+def accept(targets, drafts):
+    """targets, drafts: int32 [rows] on the GPU -> int32 [rows + 3] result words."""
+    import torch
+    rows = targets.numel()
+    out = torch.zeros(rows + 3, dtype=torch.int32, device=targets.device)
+    _check(lib().q38hip_accept(_dev_ptr(out), _dev_ptr(targets), _dev_ptr(drafts), rows, _stream()),
+           "q38hip_accept")
+    return out
+
+
+# ---- host-pointer drop-ins (numpy arrays) ------------------------------------
+
+def host_quantize_q8_k(x):
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.zeros(x.size // 256, dtype=Q8K_DTYPE)
+    _check(lib().q38_quantize_q8_k(out.ctypes.data, x.ctypes.data, x.size), "q38_quantize_q8_k")
+    return out
+
+
+def host_tensor_gemm_q8_k(qtype, data, rows, q8k, batch):
+    width = q8k.size // batch * 256
+    tensor = make_tensor(data.ctypes.data, qtype, width, rows, data.nbytes)
+    out = np.zeros(batch * rows, dtype=np.float32)
+    _check(lib().q38_tensor_gemm_q8_k(out.ctypes.data, q8k.ctypes.data, batch, width, ctypes.byref(tensor)),
+           "q38_tensor_gemm_q8_k")
+    return out.reshape(batch, rows)
+
+
+def host_tensor_gemv_q8_k(qtype, data, rows, q8k):
+    width = q8k.size * 256
+    tensor = make_tensor(data.ctypes.data, qtype, width, rows, data.nbytes)
+    out = np.zeros(rows, dtype=np.float32)
+    _check(lib().q38_tensor_gemv_q8_k(out.ctypes.data, q8k.ctypes.data, width, ctypes.byref(tensor)),
+           "q38_tensor_gemv_q8_k")
+    return out

@@ -1,0 +1,153 @@
+"""GPU parity of the HIP kernels against the CPU oracle (bit-exact).
+
+Every test calls libq38hip through its C ABI (q38hip ctypes binding) and
+compares with oracle/ on the same seeded inputs: integer/index results and
+fp32 outputs must be identical bit for bit (the reference's AVX2 lane order).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import known_blocks as kb
+from oracle import IQ1_M, Q4_K, Q6_K
+from q38hip import synth
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def hip(device):
+    import q38hip
+    q38hip.lib()
+    return q38hip
+
+
+def to_dev(array, device):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(array)).to(device)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def test_quantize_matches_oracle(hip, oracle, device):
+    rng = np.random.default_rng(1)
+    x = rng.normal(size=(3, 17408)).astype(np.float32)
+    x[0, :256] = 0.0                                   # zero block
+    x[1, 256:512] = 0.0
+    x[1, 300], x[1, 400] = -2.5, 2.5                   # |max| tie: first wins
+    x[2, 512:768] = np.float32(-127.0)                 # half-way rounding block
+    x[2, 513:517] = [0.5, 1.5, 2.5, -3.5]
+    x[2, 768:1024] *= np.float32(1e-30)                # tiny values
+    got = hip.quantize_q8_k(to_dev(x, device)).cpu().numpy()
+    want = oracle.quantize(x.reshape(-1)).view(np.uint8)
+    assert got.tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, IQ1_M, Q6_K])
+@pytest.mark.parametrize("rows,width", [(17408, 5120), (5120, 17408)])
+def test_gemv_full_shape_bit_exact(hip, oracle, device, qtype, rows, width):
+    """cfg1/cfg2 shapes: 17408x5120 and 5120x17408, one activation row."""
+    w = synth.matrix(qtype, rows, width, seed=7 * qtype + rows)
+    x = synth.activations(width, seed=rows + 3)
+    q = oracle.quantize(x.reshape(-1))
+    want = oracle.gemv(qtype, w, rows, q)
+    xq = hip.quantize_q8_k(to_dev(x, device))
+    assert xq.cpu().numpy().tobytes() == q.view(np.uint8).tobytes()
+    got = hip.gemm_q8_k(to_dev(w, device), qtype, width, rows, xq, 1).cpu().numpy()[0]
+    assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, IQ1_M, Q6_K])
+@pytest.mark.parametrize("rows,width", [(1024, 5120), (96, 17408), (48, 5120), (77, 6144)])
+def test_gemm_rows_bit_exact(hip, oracle, device, qtype, rows, width):
+    """Verify-batch GEMM, M = 1..5 rows, against the per-token oracle GEMV."""
+    w = synth.matrix(qtype, rows, width, seed=11 * qtype + rows)
+    x = synth.activations(width, seed=width + rows, count=5)
+    q = oracle.quantize(x.reshape(-1))
+    wd = to_dev(w, device)
+    xq = hip.quantize_q8_k(to_dev(x, device))
+    nb = width // 256
+    for m in range(1, 6):
+        want = oracle.gemm(qtype, w, rows, q[:m * nb], m)
+        got = hip.gemm_q8_k(wd, qtype, width, rows, xq[:m * nb * 292], m).cpu().numpy()
+        assert np.array_equal(bits(got), bits(want)), "M=%d" % m
+
+
+@pytest.mark.parametrize("name", sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz")))
+def test_gpu_matches_reference_golden(hip, device, name):
+    g = np.load(os.path.join(GOLDEN, name))
+    qtype, rows, width, tokens = (int(v) for v in g["meta"])
+    xq = hip.quantize_q8_k(to_dev(g["x"].reshape(tokens, width), device))
+    assert xq.cpu().numpy().tobytes() == g["q8k"].tobytes()
+    got = hip.gemm_q8_k(to_dev(g["w"], device), qtype, width, rows, xq, tokens).cpu().numpy()
+    assert np.array_equal(bits(got), bits(g["y"]))
+
+
+def test_host_dropins_known_answers(hip):
+    """The reference kernel ABI (host pointers) on the reference's known blocks."""
+    ones = hip.host_quantize_q8_k(np.ones(256, np.float32))
+    assert abs(hip.host_tensor_gemv_q8_k(Q4_K, kb.q4k_known_block(), 1, ones)[0] - 64.0) <= 64e-5
+    assert abs(hip.host_tensor_gemv_q8_k(IQ1_M, kb.iq1m_known_block(), 1, ones)[0] + 224.0) <= 224e-5
+    assert abs(hip.host_tensor_gemv_q8_k(Q6_K, kb.q6k_known_block(), 1, ones)[0] + 8192.0) <= 8192e-5
+    w = np.concatenate([kb.q4k_known_block(), kb.q4k_known_block()])
+    x = hip.host_quantize_q8_k(np.concatenate([np.ones(256, np.float32), np.full(256, 2.0, np.float32)]))
+    out = hip.host_tensor_gemm_q8_k(Q4_K, w, 2, x, 2).reshape(-1)
+    assert np.allclose(out, [64.0, 64.0, 128.0, 128.0], rtol=1e-5)
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K, IQ1_M])
+def test_host_dropins_batch_exact(hip, oracle, qtype):
+    """test_integer_batch_exact inputs: GEMM = GEMV bit-exact, and equal to the oracle."""
+    from oracle import BLOCK_BYTES
+    w, act, width, rows, tokens = kb.batch_exact_case(qtype, BLOCK_BYTES[qtype])
+    q = hip.host_quantize_q8_k(act)
+    assert q.tobytes() == oracle.quantize(act).tobytes()
+    nb = width // 256
+    for m in range(1, tokens + 1):
+        batch = hip.host_tensor_gemm_q8_k(qtype, w, rows, q[:m * nb], m)
+        assert np.array_equal(bits(batch), bits(oracle.gemm(qtype, w, rows, q[:m * nb], m)))
+        for t in range(m):
+            single = hip.host_tensor_gemv_q8_k(qtype, w, rows, q[t * nb:(t + 1) * nb])
+            assert batch[t].tobytes() == single.tobytes()
+
+
+def test_iq1m_randomized_trials_gpu(hip, oracle):
+    for data, act in kb.random_iq_trials(IQ1_M, 56, trials=50):
+        q = hip.host_quantize_q8_k(act)
+        got = hip.host_tensor_gemv_q8_k(IQ1_M, data, 1, q)
+        assert bits(got).tobytes() == bits(oracle.gemv(IQ1_M, data, 1, q)).tobytes()
+
+
+def test_argmax_matches_oracle(hip, oracle, device):
+    rng = np.random.default_rng(4)
+    v = rng.normal(size=(5, 248320)).astype(np.float32)
+    v[1, 1000] = v[1, 200000] = 50.0          # tie: lower index wins
+    v[2, 0] = np.nan                           # NaN at 0 keeps index 0
+    v[3, 17] = np.nan
+    v[3, 99] = 60.0                            # NaN elsewhere never wins
+    v[4, :] = -np.inf
+    got = hip.argmax(to_dev(v, device)).cpu().numpy()
+    want = [oracle.argmax(row) for row in v]
+    assert list(got) == want
+
+
+def test_accept_matches_oracle(hip, oracle, device):
+    import torch
+    rng = np.random.default_rng(8)
+    count = 1000
+    for pattern in range(16):
+        logits = rng.normal(size=(4, count)).astype(np.float32)
+        targets = logits.argmax(1).astype(np.int32)
+        drafts = np.array([targets[i] if pattern >> i & 1 else (targets[i] + 3) % count for i in range(4)],
+                          np.int32)
+        for rows in (1, 2, 3, 4):
+            res = hip.accept(to_dev(targets[:rows], device), to_dev(drafts[:rows], device)).cpu().numpy()
+            consumed, matched, nxt, accepted = oracle.accept(logits[:rows], drafts[:rows].astype(np.uint32))
+            assert (res[0], res[1], res[2]) == (consumed, matched, nxt)
+            assert list(res[3:3 + consumed]) == list(accepted)
+    torch.cuda.synchronize()
