@@ -108,16 +108,17 @@ def main():
         q38hip.gemm_q8_k(weights[i % copies], qtype, width, rows, xq, 1, out=out)
     torch.cuda.synchronize()
 
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    start.record(stream)
     for i in range(args.steps):
-        starts[i].record(stream)
         q38hip.gemm_q8_k(weights[i % copies], qtype, width, rows, xq, 1, out=out)
-        ends[i].record(stream)
+    end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per_launch_ms = float(np.mean([s.elapsed_time(e) for s, e in zip(starts, ends)]))
+    # back-to-back launches on one stream: the event span / K is the average
+    # launch duration including the inter-kernel gaps
+    per_launch_ms = start.elapsed_time(end) / args.steps
     achieved = nbytes / (per_launch_ms * 1e-3) / 1e9
 
     result = {

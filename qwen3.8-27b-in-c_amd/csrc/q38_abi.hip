@@ -13,7 +13,7 @@
 
 namespace q38 {
 bool launch_gemm(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows,
-                 uint32_t nblk, const uint32_t *grid, hipStream_t stream);
+                 uint32_t nblk, const void *grid, hipStream_t stream);
 void launch_quantize(const float *x, uint8_t *out, uint32_t nblocks, hipStream_t stream);
 uint32_t argmax_chunks(uint32_t count);
 void launch_argmax(const float *values, uint32_t count, uint32_t rows, float *pv, uint32_t *pi,
@@ -32,10 +32,11 @@ int fail(const char *message)
     return 0;
 }
 
-/* Per-device constant state: the IQ1_M codebook in the nibble-pair form the
- * GEMM kernel stages into LDS, and a growable argmax partials buffer. */
+/* Per-device constant state: the IQ1_M codebook as 2048 x 8 int8 values
+ * (the form the GEMM kernel stages into LDS), and a growable argmax
+ * partials buffer. */
 struct DeviceState {
-    uint32_t *grid = nullptr;
+    int8_t *grid = nullptr;
     float *argmax_values = nullptr;
     uint32_t *argmax_index = nullptr;
     size_t argmax_capacity = 0;
@@ -52,16 +53,10 @@ DeviceState *device_state()
     if ((int)g_devices.size() <= device) g_devices.resize(device + 1);
     DeviceState &s = g_devices[device];
     if (!s.grid) {
-        uint32_t host[2048];
+        int8_t host[2048 * 8];
         for (int e = 0; e < 2048; ++e) {
             const uint32_t code = q38_iq1m_grid_codes[e];
-            uint32_t word = 0;
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t lo = (code >> (2 * i)) & 3u;        /* element i, value + 1 */
-                const uint32_t hi = (code >> (2 * (4 + i))) & 3u;  /* element 4 + i */
-                word |= (lo | hi << 4) << (8 * i);
-            }
-            host[e] = word;
+            for (int k = 0; k < 8; ++k) host[8 * e + k] = (int8_t)(((code >> (2 * k)) & 3u) - 1);
         }
         if (hipMalloc(&s.grid, sizeof(host)) != hipSuccess) return nullptr;
         if (hipMemcpy(s.grid, host, sizeof(host), hipMemcpyHostToDevice) != hipSuccess) return nullptr;

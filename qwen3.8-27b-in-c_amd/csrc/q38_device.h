@@ -26,14 +26,28 @@ __device__ __forceinline__ int dot4(int a, int b, int c)
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
-/* Lane exchanges inside a quad (DPP quad_perm). */
+/* Same with a zero accumulator, as the three-operand VOP3P encoding with an
+ * inline 0 (the builtin form is otherwise lowered to v_dot4c plus a v_mov
+ * to clear the tied accumulator). */
+__device__ __forceinline__ int dot4z(int a, int b)
+{
+    return __builtin_amdgcn_sdot4(a, b, 0, false);
+}
+
+/* 24-bit signed multiply / multiply-add (full-rate v_mul_i32_i24 /
+ * v_mad_i32_i24); operands must fit in 24 bits. */
+__device__ __forceinline__ int mul24(int a, int b) { return __mul24(a, b); }
+__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+
+/* Lane exchanges inside a quad (DPP quad_perm); every lane of the quad is
+ * active wherever these are used, so bound_ctrl never applies. */
 __device__ __forceinline__ int quad_xor1(int v)
 {
-    return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true);
 }
 __device__ __forceinline__ int quad_xor2(int v)
 {
-    return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true);
 }
 __device__ __forceinline__ int quad_sum(int v)
 {
