@@ -8,13 +8,22 @@ of the 27B model), quantised activations resident in HBM, weights rotated over
 
 Prints one JSON line (see the fields below).  `roofline.achieved` is the
 algorithmic bytes of one launch divided by its average duration measured
-with HIP events on the stream the kernels run on.  `cpu_baseline` times the
-reference's own AVX2 kernels (oracle/_ref, compiled from its sources) on
-this host's cores over a bounded sample.
+with HIP events on the stream the kernels run on.  `roofline.traffic` is the
+HBM bytes per launch read from the committed counter summary
+profiles/<kernel>.<workload>.pmc.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated
+against a plain device copy), or null when there is none.  `cpu_baseline`
+times the reference's own AVX2 kernels (oracle/_ref, compiled from its
+sources) on this host's cores over a bounded sample whose weights rotate over
+more distinct copies than the host caches hold.
+
+`--workload copy` times a plain device-to-device copy of 64 MiB buffers; it
+is the calibration run for the memory counters, not a bench line.
 """
 import argparse
+import glob
 import json
 import os
+import re
 import sys
 import time
 
@@ -25,18 +34,6 @@ sys.path.insert(0, os.path.join(ROOT, "qwen3.8-27b-in-c_amd"))
 
 PEAK_HBM_GBS = 8000.0
 
-
-def parse():
-    p = argparse.ArgumentParser()
-    p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--workload", default="q4k_gemv",
-                   choices=["q4k_gemv", "q4k_gemv_t", "iq1m_gemv", "iq1m_gemv_t", "q6k_gemv"])
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    return p.parse_args()
-
-
 WORKLOADS = {
     # name: (type, rows, width, label)
     "q4k_gemv": (12, 17408, 5120, "Q4_K GEMV 17408x5120"),
@@ -46,6 +43,19 @@ WORKLOADS = {
     "q6k_gemv": (14, 17408, 5120, "Q6_K GEMV 17408x5120"),
 }
 BLOCK = {12: 144, 14: 210, 29: 56}
+TYPE_NAME = {12: "Q4_K", 14: "Q6_K", 29: "IQ1_M"}
+COPY_BYTES = 64 << 20
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--workload", default="q4k_gemv", choices=sorted(WORKLOADS) + ["copy"])
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
+    return p.parse_args()
 
 
 def algorithmic_bytes(qtype, rows, width):
@@ -53,33 +63,78 @@ def algorithmic_bytes(qtype, rows, width):
     return rows * (width // 256) * BLOCK[qtype] + (width // 256) * 292 + rows * 4
 
 
-def cpu_baseline(qtype, rows, width, budget_s=12.0):
-    """The reference's AVX2 GEMV (oracle/_ref) on the host cores, bounded sample."""
+def committed_traffic(workload):
+    """HBM bytes per launch from profiles/<kernel>.<workload>.pmc.txt, or None."""
+    paths = glob.glob(os.path.join(ROOT, "profiles", "*.%s.pmc.txt" % workload))
+    if len(paths) != 1:
+        return None
+    with open(paths[0]) as f:
+        m = re.search(r"^hbm_bytes_per_launch:\s*([0-9.]+)", f.read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(qtype, rows, width, budget_s):
+    """The reference's AVX2 GEMV (oracle/_ref) on the host cores, bounded sample.
+
+    The weights rotate over enough distinct copies (>= 512 MB) that each GEMV
+    streams its matrix from DRAM as the GPU launches stream theirs from HBM."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Reference
     if not Reference.available():
         return None
     from q38hip import synth
     ref = Reference()
-    w = synth.matrix(qtype, rows, width, seed=1)
+    base = synth.matrix(qtype, rows, width, seed=1)
+    copies = max(2, -(-(512 << 20) // base.nbytes))
+    weights = [base] + [base.copy() for _ in range(copies - 1)]
     x = synth.activations(width, seed=2)
     q = ref.quantize(x.reshape(-1))
-    ref.gemv(qtype, w, rows, q)  # warm-up
-    times = []
+    ref.gemv(qtype, weights[0], rows, q)  # warm-up (thread pool start)
+    count = 0
     start = time.perf_counter()
-    while time.perf_counter() - start < budget_s and len(times) < 400:
-        t0 = time.perf_counter()
-        ref.gemv(qtype, w, rows, q)
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    while True:
+        ref.gemv(qtype, weights[count % copies], rows, q)
+        count += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= budget_s:
+            break
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(algorithmic_bytes(qtype, rows, width) / med / 1e9, 3), "unit": "GB/s",
-            "cores": threads, "kind": "reference",
-            "sample": "median of %d single-row GEMVs (%s) over %.1f s, OpenMP threads=%d" % (
-                len(times), WORKLOADS_LABEL[(qtype, rows, width)], time.perf_counter() - start, threads)}
+    return {"value": round(algorithmic_bytes(qtype, rows, width) * count / elapsed / 1e9, 3),
+            "unit": "GB/s", "cores": threads, "kind": "reference",
+            "sample": "%d single-token %s x Q8_K GEMVs %dx%d (q38_tensor_gemv_q8_k, AVX2 build), "
+                      "weights rotated over %d copies (%d MB), %.1f s, OpenMP threads=%d" % (
+                          count, TYPE_NAME[qtype], rows, width, copies, copies * base.nbytes >> 20,
+                          elapsed, threads)}
 
 
-WORKLOADS_LABEL = {(v[0], v[1], v[2]): v[3] for v in WORKLOADS.values()}
+def timed(torch, stream, steps, launch):
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(steps):
+        launch(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # back-to-back launches on one stream: the event span / K is the average
+    # launch duration including the inter-kernel gaps
+    return start.elapsed_time(end) / steps, wall
+
+
+def run_copy(torch, args):
+    dev = torch.device("cuda:0")
+    n = COPY_BYTES // 4
+    bufs = [torch.empty(n, dtype=torch.float32, device=dev).fill_(i) for i in range(32)]
+    stream = torch.cuda.current_stream()
+    launch = lambda i: bufs[(2 * i + 1) % 32].copy_(bufs[(2 * i) % 32])  # noqa: E731
+    for i in range(args.warmup):
+        launch(i)
+    per_ms, wall = timed(torch, stream, args.steps, launch)
+    print(json.dumps({"metric": "device copy GB/s (counter calibration)", "value":
+                      round(2 * COPY_BYTES / (per_ms * 1e-3) / 1e9, 2), "unit": "GB/s",
+                      "bytes_read_per_launch": COPY_BYTES, "bytes_written_per_launch": COPY_BYTES,
+                      "steps": args.steps, "ms_per_step": round(wall * 1e3 / args.steps, 5)}))
 
 
 def main():
@@ -89,6 +144,9 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     import torch
+    if args.workload == "copy":
+        run_copy(torch, args)
+        return
     import q38hip
     from q38hip import synth
 
@@ -104,25 +162,17 @@ def main():
     out = torch.empty((1, rows), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream()
 
-    for i in range(args.warmup):
+    def launch(i):
         q38hip.gemm_q8_k(weights[i % copies], qtype, width, rows, xq, 1, out=out)
-    torch.cuda.synchronize()
 
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    start.record(stream)
-    for i in range(args.steps):
-        q38hip.gemm_q8_k(weights[i % copies], qtype, width, rows, xq, 1, out=out)
-    end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    # back-to-back launches on one stream: the event span / K is the average
-    # launch duration including the inter-kernel gaps
-    per_launch_ms = start.elapsed_time(end) / args.steps
+    for i in range(args.warmup):
+        launch(i)
+    per_launch_ms, wall = timed(torch, stream, args.steps, launch)
     achieved = nbytes / (per_launch_ms * 1e-3) / 1e9
+    traffic = committed_traffic(args.workload)
 
     result = {
-        "metric": "quant-GEMV HBM GB/s (Q4_K x Q8_K decode GEMV)",
+        "metric": "quant-GEMV HBM GB/s (%s x Q8_K decode GEMV)" % TYPE_NAME[qtype],
         "value": round(achieved, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -132,13 +182,15 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8xuint4->int32, fp32",
+        "dtype": "i8x%s->i32, f32" % TYPE_NAME[qtype],
         "data": "synthetic (seeded GGUF blocks, N(0,1) activations)",
         "config": {"workload": label, "weight_copies_rotated": copies,
-                   "rotated_bytes": copies * wbytes, "bytes_per_launch": nbytes},
+                   "rotated_bytes": copies * wbytes, "bytes_per_launch": nbytes,
+                   "launch_us": round(per_launch_ms * 1e3, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None},
-        "cpu_baseline": None if args.no_cpu else cpu_baseline(qtype, rows, width),
+                     "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": None if traffic is None else int(traffic)},
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(qtype, rows, width, args.cpu_seconds),
     }
     print(json.dumps(result))
 
