@@ -1,0 +1,63 @@
+/* libq38hip model ABI: the reference engine's model API on one MI355X.
+ *
+ * Same names, signatures, argument meaning, ownership and 1/0 (NULL) return
+ * convention as include/qwen38/qwen38_model.h:10-50 of
+ * shyringo/qwen3.8-27b-in-c, so the reference's CLI, server and probes link
+ * against libq38hip.so unchanged.  The GGUF weights are uploaded to HBM at
+ * open; every call runs on one HIP stream owned by the model and returns
+ * after its results are on the host.  Returned logits pointers are owned by
+ * the model (pinned host memory) and are overwritten by the next call, as in
+ * the reference.  Not reentrant: one caller thread per model.
+ *
+ * Supported checkpoints: the Qwen3.8-27B "qwen35" contract
+ * (src/qwen38/qwen38_model.c:196-319) with Q4_K, Q6_K or IQ1_M matrices, a
+ * Q4_K token embedding and F32 norm / conv / ssm vectors.  Other matrix types
+ * are rejected at open with a message.
+ */
+#ifndef Q38MODEL_H
+#define Q38MODEL_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct Q38Model Q38Model;
+
+/* qwen38_model.h:12 (open + upload to HBM; NULL on failure) */
+Q38Model *q38_model_open_gguf(const char *path, uint32_t context_length);
+/* qwen38_model.h:13 */
+int q38_model_attach_mtp_gguf(Q38Model *model, const char *path);
+/* qwen38_model.h:14-15 */
+void q38_model_close(Q38Model *model);
+void q38_model_reset(Q38Model *model);
+
+/* qwen38_model.h:19-20: one token through the model; *logits = 248320 floats */
+int q38_model_forward_token(Q38Model *model, uint32_t token_id, const float **logits);
+
+/* qwen38_model.h:24-25: layer-major prompt evaluation, logits of the last token */
+int q38_model_prefill(Q38Model *model, const uint32_t *tokens, uint32_t token_count, const float **logits);
+
+/* qwen38_model.h:29-31: MTP head (enable before the first target token) */
+int q38_model_enable_mtp(Q38Model *model);
+int q38_model_mtp_forward(Q38Model *model, uint32_t token_id, const float **logits);
+
+/* qwen38_model.h:37-41: draft up to draft_count MTP tokens, verify them in
+ * one batch, greedy acceptance; accepted_tokens needs draft_count entries */
+int q38_model_speculative_greedy(Q38Model *model, uint32_t token_id, uint32_t stop_token, uint32_t draft_count,
+                                 uint32_t *accepted_tokens, uint32_t *accepted_count, const float **next_logits);
+
+/* qwen38_model.h:45-46: hidden state after the first layer_count blocks */
+int q38_model_forward_token_layers(Q38Model *model, uint32_t token_id, uint32_t layer_count, float *hidden_out);
+
+/* qwen38_model.h:48-50 */
+uint32_t q38_model_vocab_size(const Q38Model *model);
+uint32_t q38_model_position(const Q38Model *model);
+uint32_t q38_model_context_length(const Q38Model *model);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

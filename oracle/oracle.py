@@ -198,3 +198,97 @@ class Reference:
         if not self.lib.q38_tensor_row_f32(_ptr(out), ctypes.byref(tensor), row):
             raise ValueError("row decode failed")
         return out
+
+
+class ModelAPI:
+    """The engine ABI of include/qwen38/qwen38_model.h:10-50 over any library
+    that exports it (the compiled reference in oracle/_ref, or libq38hip)."""
+
+    VOCAB = 248320
+    HIDDEN = 5120
+
+    def __init__(self, lib):
+        lib.q38_model_open_gguf.restype = ctypes.c_void_p
+        lib.q38_model_open_gguf.argtypes = [ctypes.c_char_p, ctypes.c_uint32]
+        lib.q38_model_attach_mtp_gguf.argtypes = [ctypes.c_void_p, ctypes.c_char_p]
+        lib.q38_model_close.argtypes = [ctypes.c_void_p]
+        lib.q38_model_reset.argtypes = [ctypes.c_void_p]
+        lib.q38_model_forward_token.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(_f32p)]
+        lib.q38_model_prefill.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(_f32p)]
+        lib.q38_model_enable_mtp.argtypes = [ctypes.c_void_p]
+        lib.q38_model_mtp_forward.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(_f32p)]
+        lib.q38_model_speculative_greedy.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                                     ctypes.c_uint32, ctypes.c_void_p, _u32p,
+                                                     ctypes.POINTER(_f32p)]
+        lib.q38_model_forward_token_layers.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                                       ctypes.c_void_p]
+        for name in ("q38_model_vocab_size", "q38_model_position", "q38_model_context_length"):
+            getattr(lib, name).restype = ctypes.c_uint32
+            getattr(lib, name).argtypes = [ctypes.c_void_p]
+        self.lib = lib
+        self.handle = None
+
+    def open(self, path, context_length):
+        self.handle = self.lib.q38_model_open_gguf(path.encode(), context_length)
+        if not self.handle:
+            raise RuntimeError("q38_model_open_gguf failed for %s" % path)
+        return self
+
+    def close(self):
+        if self.handle:
+            self.lib.q38_model_close(self.handle)
+            self.handle = None
+
+    def _logits(self, pointer):
+        return np.ctypeslib.as_array(pointer, shape=(self.VOCAB,)).copy()
+
+    def reset(self):
+        self.lib.q38_model_reset(self.handle)
+
+    def enable_mtp(self):
+        if not self.lib.q38_model_enable_mtp(self.handle):
+            raise RuntimeError("q38_model_enable_mtp failed")
+
+    def forward_token(self, token):
+        p = _f32p()
+        if not self.lib.q38_model_forward_token(self.handle, token, ctypes.byref(p)):
+            raise RuntimeError("q38_model_forward_token failed")
+        return self._logits(p)
+
+    def prefill(self, tokens):
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        p = _f32p()
+        if not self.lib.q38_model_prefill(self.handle, _ptr(tokens), tokens.size, ctypes.byref(p)):
+            raise RuntimeError("q38_model_prefill failed")
+        return self._logits(p)
+
+    def mtp_forward(self, token):
+        p = _f32p()
+        if not self.lib.q38_model_mtp_forward(self.handle, token, ctypes.byref(p)):
+            raise RuntimeError("q38_model_mtp_forward failed")
+        return self._logits(p)
+
+    def speculative_greedy(self, token, stop_token, draft_count):
+        accepted = np.zeros(max(draft_count, 1), dtype=np.uint32)
+        count = ctypes.c_uint32(0)
+        p = _f32p()
+        if not self.lib.q38_model_speculative_greedy(self.handle, token, stop_token, draft_count,
+                                                     _ptr(accepted), ctypes.byref(count), ctypes.byref(p)):
+            raise RuntimeError("q38_model_speculative_greedy failed")
+        return accepted[:count.value].copy(), self._logits(p)
+
+    def forward_token_layers(self, token, layers):
+        hidden = np.zeros(self.HIDDEN, dtype=np.float32)
+        if not self.lib.q38_model_forward_token_layers(self.handle, token, layers, _ptr(hidden)):
+            raise RuntimeError("q38_model_forward_token_layers failed")
+        return hidden
+
+    def position(self):
+        return self.lib.q38_model_position(self.handle)
+
+
+def reference_model(path=REF_SO):
+    """ModelAPI over the compiled reference (oracle/_ref/libq38ref.so)."""
+    if not os.path.exists(path):
+        raise RuntimeError("reference library not built (oracle/_ref)")
+    return ModelAPI(ctypes.CDLL(path))

@@ -111,6 +111,15 @@ struct DeviceBuffer {
 
 }  // namespace
 
+namespace q38 {
+/* device IQ1_M codebook of the current device (uploaded on first use) */
+const void *iq1m_grid_for_current_device()
+{
+    DeviceState *s = device_state();
+    return s ? s->grid : nullptr;
+}
+}  // namespace q38
+
 extern "C" {
 
 const char *q38hip_last_error(void) { return g_error.c_str(); }

@@ -55,6 +55,14 @@ __device__ __forceinline__ int quad_sum(int v)
     return v + quad_xor2(v);
 }
 
+/* IEEE correctly rounded fp32 division and square root.  In this toolchain
+ * __fdiv_rn is plain '/', and __fsqrt_rn is the approximate native square
+ * root unless OCML_BASIC_ROUNDED_OPERATIONS is defined, so neither is used;
+ * '/' and __builtin_sqrtf are correctly rounded under
+ * -fhip-fp32-correctly-rounded-divide-sqrt (set in the Makefile). */
+__device__ __forceinline__ float div_rn(float a, float b) { return a / b; }
+__device__ __forceinline__ float sqrt_rn(float a) { return __builtin_sqrtf(a); }
+
 __device__ __forceinline__ float fmul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float fadd_rn(float a, float b) { return __fadd_rn(a, b); }
 

@@ -1,0 +1,1056 @@
+/* Qwen3.8-27B decode engine on one MI355X: GGUF reader, HBM-resident weights
+ * and state, and the model ABI of include/q38model.h.
+ *
+ * The control flow restates src/qwen38/qwen38_model.c (forward_token
+ * :1494-1517, prefill :1519-1560, MTP :1562-1612, speculative greedy
+ * :1614-1714, batch evaluation :1121-1294); every arithmetic step runs in the
+ * HIP kernels of q38_gemm.hip, q38_misc.hip and q38_model.hip on the model's
+ * stream.  Rows of a batch are independent in every GEMM, and the recurrent /
+ * KV-cache cores run row by row in token order, so a batch of M rows gives
+ * the same bits as M single-token steps (the reference's own invariant).
+ */
+#include <hip/hip_runtime.h>
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "q38_kernels.h"
+#include "q38model.h"
+
+namespace q38 {
+const void *iq1m_grid_for_current_device();
+}
+
+namespace {
+
+constexpr uint32_t kHidden = 5120, kFFN = 17408, kLayers = 64, kTotalLayers = 65;
+constexpr uint32_t kRecurrent = 48, kFullLayers = 17;
+constexpr uint32_t kQKV = 10240, kLinV = 6144, kVHeads = 48, kHeadDim = 128;
+constexpr uint32_t kQGDim = 12288, kQDim = 6144, kKVDim = 1024, kAttnHeads = 24;
+constexpr uint32_t kVocab = 248320;
+constexpr uint32_t kBatch = 8;           /* rows per batched step (GEMM limit) */
+constexpr uint32_t kQ8KBytes = 292;
+
+enum : uint32_t { F32 = 0, Q4_K = 12, Q6_K = 14, IQ1_M = 29 };
+
+bool report(const char *what)
+{
+    fprintf(stderr, "qwen38: %s\n", what);
+    return false;
+}
+
+bool hip_ok(hipError_t e, const char *what)
+{
+    if (e == hipSuccess) return true;
+    fprintf(stderr, "qwen38: %s: %s\n", what, hipGetErrorString(e));
+    return false;
+}
+
+/* ---- GGUF reader (format v2/v3) ------------------------------------------ */
+
+/* elements and bytes per block of the GGML types (the GGUF format's own
+ * constants; src/io/qwen38_gguf.c:129-185 lists the same) */
+void ggml_block(uint32_t type, uint32_t *elements, uint32_t *bytes)
+{
+    uint32_t e = 0, b = 0;
+    switch (type) {
+    case 0: e = 1; b = 4; break;                    /* F32 */
+    case 1: case 30: e = 1; b = 2; break;           /* F16, BF16 */
+    case 2: e = 32; b = 18; break;                  /* Q4_0 */
+    case 3: e = 32; b = 20; break;                  /* Q4_1 */
+    case 6: e = 32; b = 22; break;                  /* Q5_0 */
+    case 7: e = 32; b = 24; break;                  /* Q5_1 */
+    case 8: e = 32; b = 34; break;                  /* Q8_0 */
+    case 20: e = 32; b = 18; break;                 /* IQ4_NL */
+    case 10: e = 256; b = 84; break;                /* Q2_K */
+    case 11: e = 256; b = 110; break;               /* Q3_K */
+    case 12: e = 256; b = 144; break;               /* Q4_K */
+    case 13: e = 256; b = 176; break;               /* Q5_K */
+    case 14: e = 256; b = 210; break;               /* Q6_K */
+    case 16: e = 256; b = 66; break;                /* IQ2_XXS */
+    case 17: e = 256; b = 74; break;                /* IQ2_XS */
+    case 18: e = 256; b = 98; break;                /* IQ3_XXS */
+    case 19: e = 256; b = 50; break;                /* IQ1_S */
+    case 21: e = 256; b = 110; break;               /* IQ3_S */
+    case 22: e = 256; b = 82; break;                /* IQ2_S */
+    case 23: e = 256; b = 136; break;               /* IQ4_XS */
+    case 29: e = 256; b = 56; break;                /* IQ1_M */
+    default: break;
+    }
+    *elements = e;
+    *bytes = b;
+}
+
+struct TensorInfo {
+    uint32_t n_dims = 0;
+    uint64_t shape[8] = {0};
+    uint32_t type = 0;
+    uint64_t offset = 0;
+    uint64_t nbytes = 0;
+};
+
+struct MetaValue {
+    uint32_t type = 0;
+    uint32_t u32 = 0;
+    std::string str;
+};
+
+struct GGUFFile {
+    int fd = -1;
+    const uint8_t *map = nullptr;
+    uint64_t size = 0;
+    uint64_t data_offset = 0;
+    uint64_t data_bytes = 0;
+    std::unordered_map<std::string, TensorInfo> tensors;
+    std::unordered_map<std::string, MetaValue> meta;
+
+    ~GGUFFile() { close(); }
+    void close()
+    {
+        if (map) munmap(const_cast<uint8_t *>(map), size);
+        if (fd >= 0) ::close(fd);
+        map = nullptr;
+        fd = -1;
+    }
+
+    struct Reader {
+        const uint8_t *p, *end;
+        bool failed = false;
+        bool take(uint64_t n, const uint8_t **out)
+        {
+            if (failed || (uint64_t)(end - p) < n) return !(failed = true);
+            *out = p;
+            p += n;
+            return true;
+        }
+        uint32_t u32()
+        {
+            const uint8_t *q;
+            uint32_t v = 0;
+            if (take(4, &q)) memcpy(&v, q, 4);
+            return v;
+        }
+        uint64_t u64()
+        {
+            const uint8_t *q;
+            uint64_t v = 0;
+            if (take(8, &q)) memcpy(&v, q, 8);
+            return v;
+        }
+        bool str(std::string *s)
+        {
+            const uint64_t n = u64();
+            const uint8_t *q;
+            if (!take(n, &q)) return false;
+            if (s) s->assign(reinterpret_cast<const char *>(q), n);
+            return true;
+        }
+        bool skip_value(uint32_t type, uint64_t count)
+        {
+            static const uint8_t sizes[13] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
+            if (type > 12 || type == 9) return !(failed = true);
+            if (type == 8) {
+                for (uint64_t i = 0; i < count; ++i)
+                    if (!str(nullptr)) return false;
+                return true;
+            }
+            const uint8_t *q;
+            if (count > UINT64_MAX / sizes[type]) return !(failed = true);
+            return take(count * sizes[type], &q);
+        }
+    };
+
+    bool open(const char *path)
+    {
+        fd = ::open(path, O_RDONLY);
+        if (fd < 0) {
+            perror(path);
+            return false;
+        }
+        struct stat st;
+        if (fstat(fd, &st) != 0 || st.st_size < 24) return report("invalid GGUF file size");
+        size = (uint64_t)st.st_size;
+        void *m = mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
+        if (m == MAP_FAILED) return report("mmap of the GGUF file failed");
+        map = static_cast<const uint8_t *>(m);
+        Reader r{map, map + size};
+        const uint32_t magic = r.u32();
+        const uint32_t version = r.u32();
+        const uint64_t n_tensors = r.u64();
+        const uint64_t n_meta = r.u64();
+        if (magic != 0x46554747u || version < 2 || version > 3 || n_tensors == 0)
+            return report("unsupported or corrupt GGUF header");
+        for (uint64_t i = 0; i < n_meta; ++i) {
+            std::string key;
+            MetaValue v;
+            if (!r.str(&key)) return report("malformed GGUF metadata");
+            v.type = r.u32();
+            if (r.failed || v.type > 12) return report("malformed GGUF metadata");
+            if (v.type == 8) {
+                if (!r.str(&v.str)) return report("malformed GGUF metadata");
+            } else if (v.type == 9) {
+                const uint32_t at = r.u32();
+                const uint64_t count = r.u64();
+                if (at == 9 || !r.skip_value(at, count)) return report("malformed GGUF metadata");
+            } else if (v.type == 4) {
+                v.u32 = r.u32();
+            } else if (!r.skip_value(v.type, 1)) {
+                return report("malformed GGUF metadata");
+            }
+            meta[key] = v;
+        }
+        for (uint64_t i = 0; i < n_tensors; ++i) {
+            std::string name;
+            TensorInfo t;
+            if (!r.str(&name)) return report("malformed GGUF tensor table");
+            t.n_dims = r.u32();
+            if (r.failed || t.n_dims == 0 || t.n_dims > 8) return report("malformed GGUF tensor table");
+            uint64_t elements = 1;
+            for (uint32_t d = 0; d < t.n_dims; ++d) {
+                t.shape[d] = r.u64();
+                if (!t.shape[d] || elements > UINT64_MAX / t.shape[d]) return report("malformed GGUF tensor table");
+                elements *= t.shape[d];
+            }
+            t.type = r.u32();
+            t.offset = r.u64();
+            uint32_t be, bb;
+            ggml_block(t.type, &be, &bb);
+            if (r.failed || !be || t.shape[0] % be || elements % be || elements / be > UINT64_MAX / bb)
+                return report("malformed GGUF tensor table");
+            t.nbytes = elements / be * bb;
+            tensors[name] = t;
+        }
+        uint64_t alignment = 32;
+        auto a = meta.find("general.alignment");
+        if (a != meta.end() && a->second.type == 4) {
+            alignment = a->second.u32;
+            if (!alignment || (alignment & (alignment - 1))) return report("invalid GGUF alignment");
+        }
+        const uint64_t end = (uint64_t)(r.p - map);
+        data_offset = (end + alignment - 1) & ~(alignment - 1);
+        if (data_offset > size) return report("GGUF tensor data begins past end of file");
+        data_bytes = size - data_offset;
+        for (auto &kv : tensors) {
+            const TensorInfo &t = kv.second;
+            if (t.offset > data_bytes || t.nbytes > data_bytes - t.offset)
+                return report(("tensor outside GGUF file: " + kv.first).c_str());
+        }
+        return true;
+    }
+
+    bool u32_is(const char *key, uint32_t want) const
+    {
+        auto it = meta.find(key);
+        return it != meta.end() && it->second.type == 4 && it->second.u32 == want;
+    }
+    bool get_u32(const char *key, uint32_t *out) const
+    {
+        auto it = meta.find(key);
+        if (it == meta.end() || it->second.type != 4) return false;
+        *out = it->second.u32;
+        return true;
+    }
+    bool str_is(const char *key, const char *want) const
+    {
+        auto it = meta.find(key);
+        return it != meta.end() && it->second.type == 8 && it->second.str == want;
+    }
+};
+
+/* ---- device-resident model ------------------------------------------------ */
+
+struct DevTensor {
+    uint32_t type = 0;
+    uint32_t n_dims = 0;
+    uint64_t width = 0, rows = 0;
+    const uint8_t *data = nullptr;
+    const float *f32() const { return reinterpret_cast<const float *>(data); }
+};
+
+struct Layer {
+    bool full = false;
+    DevTensor attn_norm, post_norm, ffn_gate, ffn_up, ffn_down;
+    DevTensor qkv, z, alpha, beta, conv, dt, a, ssm_norm, ssm_out;   /* DeltaNet */
+    DevTensor q, k, v, out, q_norm, k_norm;                          /* full attention */
+};
+
+bool matrix_type_ok(uint32_t t) { return t == Q4_K || t == Q6_K || t == IQ1_M; }
+
+}  // namespace
+
+struct Q38Model {
+    GGUFFile gguf, mtp_gguf;
+    void *weights = nullptr, *mtp_weights = nullptr;
+    DevTensor embedding, output_norm, output, mtp_embedding, mtp_output;
+    DevTensor eh_proj, enorm, hnorm, shared_head_norm;
+    Layer layers[kTotalLayers];
+    uint32_t context_length = 0, position = 0, mtp_position = 0;
+    bool mtp_weights_loaded = false, mtp_enabled = false;
+    uint32_t ck_position = 0, ck_mtp_position = 0;
+
+    hipStream_t stream = nullptr;
+    const void *grid = nullptr;
+    /* state */
+    float *conv_state = nullptr, *delta_state = nullptr, *key_cache = nullptr, *value_cache = nullptr;
+    float *mtp_hidden = nullptr, *ck_conv = nullptr, *ck_delta = nullptr, *ck_mtp_hidden = nullptr;
+    float *rope = nullptr;
+    /* scratch, kBatch rows */
+    float *hidden = nullptr, *norm = nullptr, *branch = nullptr, *wide0 = nullptr, *wide1 = nullptr;
+    float *kbuf = nullptr, *vbuf = nullptr, *qbuf = nullptr, *attn = nullptr, *beta = nullptr, *alpha = nullptr;
+    float *scores = nullptr, *logits = nullptr, *target_norm = nullptr;
+    uint8_t *q8k = nullptr;
+    uint32_t *tokens = nullptr, *positions = nullptr, *targets = nullptr, *drafts = nullptr, *accept = nullptr;
+    float *argmax_pv = nullptr;
+    uint32_t *argmax_pi = nullptr;
+    /* host side */
+    float *host_logits = nullptr;
+    uint32_t *host_words = nullptr;
+    float query_scale = 0.0f;
+};
+
+namespace {
+
+bool bind_tensor(const GGUFFile &f, const uint8_t *base, const std::string &name, DevTensor *out)
+{
+    auto it = f.tensors.find(name);
+    if (it == f.tensors.end()) {
+        fprintf(stderr, "qwen38: missing tensor %s\n", name.c_str());
+        return false;
+    }
+    const TensorInfo &t = it->second;
+    out->type = t.type;
+    out->n_dims = t.n_dims;
+    out->width = t.shape[0];
+    out->rows = t.n_dims > 1 ? t.shape[1] : 0;
+    out->data = base + t.offset;
+    return true;
+}
+
+/* q38_expect_tensor (qwen38_model.c:190-207), restricted to the matrix types
+ * this library has kernels for */
+bool expect(const DevTensor &t, const std::string &name, uint64_t width, uint64_t rows, bool f32_only)
+{
+    const uint32_t dims = rows ? 2u : 1u;
+    const bool shape_ok = t.n_dims == dims && t.width == width && (!rows || t.rows == rows);
+    const bool type_ok = f32_only ? t.type == F32 : matrix_type_ok(t.type);
+    if (shape_ok && type_ok) return true;
+    fprintf(stderr, "qwen38: incompatible tensor %s; expected %s[%llu", name.c_str(), f32_only ? "F32 " : "",
+            (unsigned long long)width);
+    if (rows) fprintf(stderr, ",%llu", (unsigned long long)rows);
+    fprintf(stderr, "] of type %s\n", f32_only ? "F32" : "Q4_K, Q6_K or IQ1_M");
+    return false;
+}
+
+bool bind_layer(Layer *L, const GGUFFile &f, const uint8_t *base, int layer)
+{
+    const std::string p = "blk." + std::to_string(layer) + ".";
+    L->full = (layer + 1) % 4 == 0 || layer == (int)kLayers;
+    int ok = bind_tensor(f, base, p + "attn_norm.weight", &L->attn_norm) &&
+              bind_tensor(f, base, p + "post_attention_norm.weight", &L->post_norm) &&
+              bind_tensor(f, base, p + "ffn_gate.weight", &L->ffn_gate) && bind_tensor(f, base, p + "ffn_up.weight", &L->ffn_up) &&
+              bind_tensor(f, base, p + "ffn_down.weight", &L->ffn_down);
+    if (!ok) return false;
+    ok = (int)expect(L->attn_norm, p + "attn_norm.weight", kHidden, 0, true) &
+         (int)expect(L->post_norm, p + "post_attention_norm.weight", kHidden, 0, true) &
+         (int)expect(L->ffn_gate, p + "ffn_gate.weight", kHidden, kFFN, false) &
+         (int)expect(L->ffn_up, p + "ffn_up.weight", kHidden, kFFN, false) &
+         (int)expect(L->ffn_down, p + "ffn_down.weight", kFFN, kHidden, false);
+    if (L->full) {
+        if (!(bind_tensor(f, base, p + "attn_q.weight", &L->q) && bind_tensor(f, base, p + "attn_k.weight", &L->k) &&
+              bind_tensor(f, base, p + "attn_v.weight", &L->v) && bind_tensor(f, base, p + "attn_output.weight", &L->out) &&
+              bind_tensor(f, base, p + "attn_q_norm.weight", &L->q_norm) &&
+              bind_tensor(f, base, p + "attn_k_norm.weight", &L->k_norm)))
+            return false;
+        ok &= (int)expect(L->q, p + "attn_q.weight", kHidden, kQGDim, false) &
+              (int)expect(L->k, p + "attn_k.weight", kHidden, kKVDim, false) &
+              (int)expect(L->v, p + "attn_v.weight", kHidden, kKVDim, false) &
+              (int)expect(L->out, p + "attn_output.weight", kQDim, kHidden, false) &
+              (int)expect(L->q_norm, p + "attn_q_norm.weight", 256, 0, true) &
+              (int)expect(L->k_norm, p + "attn_k_norm.weight", 256, 0, true);
+    } else {
+        if (!(bind_tensor(f, base, p + "attn_qkv.weight", &L->qkv) && bind_tensor(f, base, p + "attn_gate.weight", &L->z) &&
+              bind_tensor(f, base, p + "ssm_alpha.weight", &L->alpha) && bind_tensor(f, base, p + "ssm_beta.weight", &L->beta) &&
+              bind_tensor(f, base, p + "ssm_conv1d.weight", &L->conv) && bind_tensor(f, base, p + "ssm_dt.bias", &L->dt) &&
+              bind_tensor(f, base, p + "ssm_a", &L->a) && bind_tensor(f, base, p + "ssm_norm.weight", &L->ssm_norm) &&
+              bind_tensor(f, base, p + "ssm_out.weight", &L->ssm_out)))
+            return false;
+        ok &= (int)expect(L->qkv, p + "attn_qkv.weight", kHidden, kQKV, false) &
+              (int)expect(L->z, p + "attn_gate.weight", kHidden, kLinV, false) &
+              (int)expect(L->alpha, p + "ssm_alpha.weight", kHidden, kVHeads, false) &
+              (int)expect(L->beta, p + "ssm_beta.weight", kHidden, kVHeads, false) &
+              (int)expect(L->conv, p + "ssm_conv1d.weight", 4, kQKV, true) &
+              (int)expect(L->dt, p + "ssm_dt.bias", kVHeads, 0, true) & (int)expect(L->a, p + "ssm_a", kVHeads, 0, true) &
+              (int)expect(L->ssm_norm, p + "ssm_norm.weight", kHeadDim, 0, true) &
+              (int)expect(L->ssm_out, p + "ssm_out.weight", kLinV, kHidden, false);
+    }
+    return ok;
+}
+
+/* Copy the whole tensor-data region of a GGUF file to one HBM allocation
+ * through two pinned staging buffers. */
+bool upload(const GGUFFile &f, void **device)
+{
+    if (!hip_ok(hipMalloc(device, f.data_bytes ? f.data_bytes : 1), "weight allocation")) return false;
+    const size_t chunk = 256u << 20;
+    void *stage[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    hipStream_t s = nullptr;
+    bool ok = hip_ok(hipHostMalloc(&stage[0], chunk), "pinned staging") &&
+              hip_ok(hipHostMalloc(&stage[1], chunk), "pinned staging") &&
+              hip_ok(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "upload stream") &&
+              hip_ok(hipEventCreate(&done[0]), "event") && hip_ok(hipEventCreate(&done[1]), "event");
+    uint64_t off = 0;
+    for (int i = 0; ok && off < f.data_bytes; ++i, off += chunk) {
+        const size_t n = (size_t)std::min<uint64_t>(chunk, f.data_bytes - off);
+        const int b = i & 1;
+        ok = hip_ok(hipEventSynchronize(done[b]), "upload wait");
+        uint64_t got = 0;
+        while (ok && got < n) {
+            const ssize_t r = pread(f.fd, static_cast<uint8_t *>(stage[b]) + got, n - got,
+                                    (off_t)(f.data_offset + off + got));
+            if (r <= 0) ok = report("reading GGUF tensor data failed");
+            else got += (uint64_t)r;
+        }
+        ok = ok && hip_ok(hipMemcpyAsync(static_cast<uint8_t *>(*device) + off, stage[b], n,
+                                         hipMemcpyHostToDevice, s), "weight upload") &&
+             hip_ok(hipEventRecord(done[b], s), "event");
+    }
+    if (s) ok = hip_ok(hipStreamSynchronize(s), "upload") && ok;
+    for (int b = 0; b < 2; ++b) {
+        if (done[b]) (void)hipEventDestroy(done[b]);
+        if (stage[b]) (void)hipHostFree(stage[b]);
+    }
+    if (s) (void)hipStreamDestroy(s);
+    return ok;
+}
+
+template <typename T>
+bool dalloc(T **p, size_t count)
+{
+    return hip_ok(hipMalloc(reinterpret_cast<void **>(p), count * sizeof(T) + 256), "device allocation");
+}
+
+template <typename T>
+void dfree(T *&p)
+{
+    if (p) (void)hipFree(p);
+    p = nullptr;
+}
+
+size_t conv_count() { return (size_t)kRecurrent * kQKV * 3; }
+size_t delta_count() { return (size_t)kRecurrent * kVHeads * kHeadDim * kHeadDim; }
+size_t kv_count(uint32_t ctx) { return (size_t)kFullLayers * ctx * kKVDim; }
+
+bool validate_base(Q38Model *m)
+{
+    const GGUFFile &f = m->gguf;
+    uint32_t blocks = 0, nextn = 0;
+    const bool ok = f.get_u32("qwen35.block_count", &blocks) && f.get_u32("qwen35.nextn_predict_layers", &nextn) &&
+                    ((blocks == kLayers && nextn == 0) || (blocks == kTotalLayers && nextn == 1)) &&
+                    f.str_is("general.architecture", "qwen35") && f.u32_is("qwen35.embedding_length", kHidden) &&
+                    f.u32_is("qwen35.feed_forward_length", kFFN) && f.u32_is("qwen35.attention.head_count", 24) &&
+                    f.u32_is("qwen35.attention.head_count_kv", 4) &&
+                    f.u32_is("qwen35.full_attention_interval", 4) && f.u32_is("qwen35.ssm.state_size", 128) &&
+                    f.u32_is("qwen35.ssm.group_count", 16) && f.u32_is("qwen35.ssm.time_step_rank", 48) &&
+                    f.u32_is("qwen35.ssm.inner_size", kLinV);
+    if (!ok) return report("checkpoint metadata is not Qwen3.8-27B");
+    return true;
+}
+
+bool bind_mtp(Q38Model *m, const GGUFFile &f, const uint8_t *base)
+{
+    const bool meta_ok = f.str_is("general.architecture", "qwen35") && f.u32_is("qwen35.block_count", kTotalLayers) &&
+                         f.u32_is("qwen35.nextn_predict_layers", 1) && f.u32_is("qwen35.embedding_length", kHidden) &&
+                         f.u32_is("qwen35.feed_forward_length", kFFN);
+    if (!meta_ok) return report("MTP checkpoint metadata is not Qwen3.8-27B");
+    if (!bind_tensor(f, base, "token_embd.weight", &m->mtp_embedding) || !bind_tensor(f, base, "output.weight", &m->mtp_output) ||
+        !bind_layer(&m->layers[kLayers], f, base, kLayers) ||
+        !bind_tensor(f, base, "blk.64.nextn.eh_proj.weight", &m->eh_proj) ||
+        !bind_tensor(f, base, "blk.64.nextn.enorm.weight", &m->enorm) ||
+        !bind_tensor(f, base, "blk.64.nextn.hnorm.weight", &m->hnorm) ||
+        !bind_tensor(f, base, "blk.64.nextn.shared_head_norm.weight", &m->shared_head_norm))
+        return false;
+    bool ok = expect(m->mtp_embedding, "token_embd.weight", kHidden, kVocab, false) &&
+              expect(m->mtp_output, "output.weight", kHidden, kVocab, false) &&
+              expect(m->eh_proj, "blk.64.nextn.eh_proj.weight", 2 * kHidden, kHidden, false) &&
+              expect(m->enorm, "blk.64.nextn.enorm.weight", kHidden, 0, true) &&
+              expect(m->hnorm, "blk.64.nextn.hnorm.weight", kHidden, 0, true) &&
+              expect(m->shared_head_norm, "blk.64.nextn.shared_head_norm.weight", kHidden, 0, true);
+    if (ok && m->mtp_embedding.type != Q4_K) ok = report("MTP token_embd.weight must be Q4_K");
+    if (ok) m->mtp_weights_loaded = true;
+    return ok;
+}
+
+void release(Q38Model *m)
+{
+    if (!m) return;
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    float **fbufs[] = {&m->conv_state, &m->delta_state, &m->key_cache, &m->value_cache, &m->mtp_hidden,
+                       &m->ck_conv, &m->ck_delta, &m->ck_mtp_hidden, &m->rope, &m->hidden, &m->norm,
+                       &m->branch, &m->wide0, &m->wide1, &m->kbuf, &m->vbuf, &m->qbuf, &m->attn, &m->beta,
+                       &m->alpha, &m->scores, &m->logits, &m->target_norm, &m->argmax_pv};
+    for (float **p : fbufs) dfree(*p);
+    uint32_t **ubufs[] = {&m->tokens, &m->positions, &m->targets, &m->drafts, &m->accept, &m->argmax_pi};
+    for (uint32_t **p : ubufs) dfree(*p);
+    dfree(m->q8k);
+    if (m->weights) (void)hipFree(m->weights);
+    if (m->mtp_weights) (void)hipFree(m->mtp_weights);
+    if (m->host_logits) (void)hipHostFree(m->host_logits);
+    if (m->host_words) (void)hipHostFree(m->host_words);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+}
+
+bool allocate_state(Q38Model *m)
+{
+    const uint32_t ctx = m->context_length;
+    const uint32_t B = kBatch;
+    bool ok = dalloc(&m->conv_state, conv_count()) && dalloc(&m->delta_state, delta_count()) &&
+              dalloc(&m->key_cache, kv_count(ctx)) && dalloc(&m->value_cache, kv_count(ctx)) &&
+              dalloc(&m->mtp_hidden, kHidden) && dalloc(&m->rope, (size_t)ctx * 64) &&
+              dalloc(&m->hidden, (size_t)B * kHidden) && dalloc(&m->norm, (size_t)B * 2 * kHidden) &&
+              dalloc(&m->branch, (size_t)B * kHidden) && dalloc(&m->wide0, (size_t)B * kFFN) &&
+              dalloc(&m->wide1, (size_t)B * kFFN) && dalloc(&m->kbuf, (size_t)B * kKVDim) &&
+              dalloc(&m->vbuf, (size_t)B * kKVDim) && dalloc(&m->qbuf, kQDim) &&
+              dalloc(&m->attn, (size_t)B * kLinV) && dalloc(&m->beta, (size_t)B * kVHeads) &&
+              dalloc(&m->alpha, (size_t)B * kVHeads) && dalloc(&m->scores, (size_t)kAttnHeads * ctx) &&
+              dalloc(&m->logits, (size_t)B * kVocab) && dalloc(&m->target_norm, (size_t)B * kHidden) &&
+              dalloc(&m->q8k, (size_t)B * (kFFN / 256) * kQ8KBytes) && dalloc(&m->tokens, B) &&
+              dalloc(&m->positions, 4) && dalloc(&m->targets, B) && dalloc(&m->drafts, B) &&
+              dalloc(&m->accept, B + 3) && dalloc(&m->argmax_pv, (size_t)B * q38::argmax_chunks(kVocab)) &&
+              dalloc(&m->argmax_pi, (size_t)B * q38::argmax_chunks(kVocab)) &&
+              hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_logits), kVocab * sizeof(float)),
+                     "pinned logits") &&
+              hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_words), 64 * sizeof(uint32_t)), "pinned ids");
+    if (!ok) return false;
+    /* RoPE table: theta starts at the position and is multiplied by
+     * powf(1e7, -2/64) per pair; cosf/sinf of the host C library, exactly the
+     * values q38_rope computes (qwen38_model.c:697-713). */
+    std::vector<float> table((size_t)ctx * 64);
+    const float theta_scale = powf(10000000.0f, -2.0f / 64.0f);
+    for (uint32_t pos = 0; pos < ctx; ++pos) {
+        float theta = (float)pos;
+        for (int pair = 0; pair < 32; ++pair) {
+            table[(size_t)pos * 64 + pair] = cosf(theta);
+            table[(size_t)pos * 64 + 32 + pair] = sinf(theta);
+            theta *= theta_scale;
+        }
+    }
+    m->query_scale = 1.0f / sqrtf(128.0f);
+    return hip_ok(hipMemcpy(m->rope, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice),
+                  "rope table upload");
+}
+
+/* zero the recurrent state, KV caches and MTP hidden (q38_model_reset) */
+bool clear_state(Q38Model *m)
+{
+    hipStream_t s = m->stream;
+    return hip_ok(hipMemsetAsync(m->conv_state, 0, conv_count() * sizeof(float), s), "reset") &&
+           hip_ok(hipMemsetAsync(m->delta_state, 0, delta_count() * sizeof(float), s), "reset") &&
+           hip_ok(hipMemsetAsync(m->key_cache, 0, kv_count(m->context_length) * sizeof(float), s), "reset") &&
+           hip_ok(hipMemsetAsync(m->value_cache, 0, kv_count(m->context_length) * sizeof(float), s), "reset") &&
+           hip_ok(hipMemsetAsync(m->mtp_hidden, 0, kHidden * sizeof(float), s), "reset") &&
+           hip_ok(hipStreamSynchronize(s), "reset");
+}
+
+/* ---- layer trace (QWEN38_TRACE_LAYERS, as src/qwen38/qwen38_model.c:556-591) */
+
+bool trace_enabled()
+{
+    static int enabled = -1;
+    if (enabled < 0) {
+        const char *v = getenv("QWEN38_TRACE_LAYERS");
+        enabled = v && v[0] && strcmp(v, "0") != 0;
+    }
+    return enabled == 1;
+}
+
+/* same line format as the reference's q38_trace_vector; synchronises the
+ * stream, so it is only for correctness probes */
+void trace(Q38Model *m, const char *name, int layer, const float *device, uint64_t length)
+{
+    if (!trace_enabled()) return;
+    std::vector<float> v(length);
+    if (hipMemcpyAsync(v.data(), device, length * sizeof(float), hipMemcpyDeviceToHost, m->stream) != hipSuccess ||
+        hipStreamSynchronize(m->stream) != hipSuccess)
+        return;
+    float sum = 0.0f;
+    double sum_abs = 0.0;
+    for (uint64_t i = 0; i < length; ++i) {
+        sum += v[i];
+        sum_abs += fabsf(v[i]);
+    }
+    fprintf(stderr, "trace %s%d sum=%.9g abs=%.9g first=%.9g,%.9g,%.9g last=%.9g,%.9g,%.9g\n", name, layer, sum,
+            sum_abs, v[0], v[1], v[2], v[length - 3], v[length - 2], v[length - 1]);
+    /* QWEN38_TRACE_DIR: also write the whole vector as raw float32 */
+    if (const char *dir = getenv("QWEN38_TRACE_DIR")) {
+        const std::string path = std::string(dir) + "/" + name + std::to_string(layer) + ".f32";
+        if (FILE *f = fopen(path.c_str(), "wb")) {
+            fwrite(v.data(), sizeof(float), length, f);
+            fclose(f);
+        }
+    }
+}
+
+/* ---- step building blocks -------------------------------------------------- */
+
+bool gemm(Q38Model *m, const DevTensor &w, const float *in_rows, uint32_t count, float *out)
+{
+    const uint32_t nblk = (uint32_t)(w.width / 256);
+    q38::launch_quantize(in_rows, m->q8k, count * nblk, m->stream);
+    if (!q38::launch_gemm((int)w.type, (int)count, w.data, m->q8k, out, (uint32_t)w.rows, nblk, m->grid, m->stream))
+        return report("unsupported GEMM configuration");
+    return true;
+}
+
+/* GEMM over an input that is already quantised in m->q8k */
+bool gemm_q(Q38Model *m, const DevTensor &w, uint32_t count, float *out)
+{
+    if (!q38::launch_gemm((int)w.type, (int)count, w.data, m->q8k, out, (uint32_t)w.rows, (uint32_t)(w.width / 256),
+                          m->grid, m->stream))
+        return report("unsupported GEMM configuration");
+    return true;
+}
+
+bool set_positions(Q38Model *m, uint32_t base)
+{
+    m->host_words[32] = base;
+    return hip_ok(hipMemcpyAsync(m->positions, &m->host_words[32], 4, hipMemcpyHostToDevice, m->stream),
+                  "position upload") &&
+           hip_ok(hipStreamSynchronize(m->stream), "position upload");
+}
+
+/* attention mixer of a full-attention layer over `count` rows at positions
+ * base.., rows of m->norm in, rows of m->branch out
+ * (q38_batch_full_attention, qwen38_model.c:1089-1119) */
+bool full_attention_rows(Q38Model *m, int layer, uint32_t count)
+{
+    const Layer &L = m->layers[layer];
+    const int full_index = layer / 4;
+    const size_t kv_off = (size_t)full_index * m->context_length * kKVDim;
+    q38::launch_quantize(m->norm, m->q8k, count * (kHidden / 256), m->stream);
+    if (!gemm_q(m, L.q, count, m->wide0) || !gemm_q(m, L.k, count, m->kbuf) || !gemm_q(m, L.v, count, m->vbuf))
+        return false;
+    for (uint32_t t = 0; t < count; ++t)
+        q38::launch_attention(m->attn + (size_t)t * kQDim, m->qbuf, m->wide0 + (size_t)t * kQGDim,
+                              m->kbuf + (size_t)t * kKVDim, m->vbuf + (size_t)t * kKVDim, L.q_norm.f32(),
+                              L.k_norm.f32(), m->rope, m->key_cache + kv_off, m->value_cache + kv_off, m->scores,
+                              (int)m->context_length, m->positions, (int)t, m->stream);
+    if (count == 1 && trace_enabled()) {
+        uint32_t pos = 0;
+        (void)hipMemcpy(&pos, m->positions, 4, hipMemcpyDeviceToHost);
+        trace(m, "Qcur_full-", layer, m->wide0, kQGDim);
+        trace(m, "Kcur-", layer, m->key_cache + kv_off + (size_t)pos * kKVDim, kKVDim);
+        trace(m, "Vcur-", layer, m->vbuf, kKVDim);
+        trace(m, "attn_gated-", layer, m->attn, kQDim);
+    }
+    if (!gemm(m, L.out, m->attn, count, m->branch)) return false;
+    if (count == 1) trace(m, "attn_output-", layer, m->branch, kHidden);
+    return true;
+}
+
+/* DeltaNet mixer (q38_batch_linear_attention, qwen38_model.c:1062-1087) */
+bool linear_attention_rows(Q38Model *m, int layer, uint32_t count)
+{
+    const Layer &L = m->layers[layer];
+    const int r = layer - (layer + 1) / 4;
+    q38::launch_quantize(m->norm, m->q8k, count * (kHidden / 256), m->stream);
+    if (!gemm_q(m, L.qkv, count, m->wide0) || !gemm_q(m, L.z, count, m->wide1) ||
+        !gemm_q(m, L.beta, count, m->beta) || !gemm_q(m, L.alpha, count, m->alpha))
+        return false;
+    const bool tr = count == 1 && trace_enabled();
+    if (tr) {
+        trace(m, "dn_norm-", layer, m->norm, kHidden);
+        trace(m, "dn_qkv_proj-", layer, m->wide0, kQKV);
+        trace(m, "dn_z-", layer, m->wide1, kLinV);
+        trace(m, "dn_beta_proj-", layer, m->beta, kVHeads);
+        trace(m, "dn_alpha_proj-", layer, m->alpha, kVHeads);
+    }
+    for (uint32_t t = 0; t < count; ++t) {
+        float *qkv = m->wide0 + (size_t)t * kQKV, *attn = m->attn + (size_t)t * kLinV;
+        float *beta = m->beta + (size_t)t * kVHeads, *alpha = m->alpha + (size_t)t * kVHeads;
+        q38::launch_deltanet_prep(qkv, beta, alpha, m->conv_state + (size_t)r * kQKV * 3, L.conv.f32(), L.a.f32(),
+                                  L.dt.f32(), m->stream);
+        if (tr) {
+            trace(m, "dn_qkv-", layer, qkv, kQKV);
+            trace(m, "dn_beta-", layer, beta, kVHeads);
+            trace(m, "dn_alpha-", layer, alpha, kVHeads);
+        }
+        q38::launch_deltanet_state(attn, m->delta_state + (size_t)r * kVHeads * kHeadDim * kHeadDim, qkv, beta, alpha,
+                                   m->query_scale, m->stream);
+        if (tr) trace(m, "dn_core-", layer, attn, kLinV);
+        q38::launch_deltanet_out(attn, m->wide1 + (size_t)t * kLinV, L.ssm_norm.f32(), m->stream);
+        if (tr) trace(m, "dn_gated-", layer, attn, kLinV);
+    }
+    return gemm(m, L.ssm_out, m->attn, count, m->branch);
+}
+
+/* FFN of a block over rows of m->norm into m->branch */
+bool ffn_rows(Q38Model *m, const Layer &L, uint32_t count)
+{
+    if (!gemm(m, L.ffn_gate, m->norm, count, m->wide0) || !gemm_q(m, L.ffn_up, count, m->wide1)) return false;
+    q38::launch_swiglu(m->wide0, m->wide1, (long long)count * kFFN, m->stream);
+    return gemm(m, L.ffn_down, m->wide0, count, m->branch);
+}
+
+/* one transformer block over `count` rows of m->hidden
+ * (q38_layer_forward / q38_batch_layer, qwen38_model.c:955-984, 1121-1155) */
+bool layer_rows(Q38Model *m, int layer, uint32_t count)
+{
+    const Layer &L = m->layers[layer];
+    q38::launch_rmsnorm(m->norm, m->hidden, L.attn_norm.f32(), kHidden, (int)count, kHidden, kHidden, m->stream);
+    if (!(L.full ? full_attention_rows(m, layer, count) : linear_attention_rows(m, layer, count))) return false;
+    if (count == 1) trace(m, "attention_branch-", layer, m->branch, kHidden);
+    q38::launch_add_rmsnorm(m->norm, m->hidden, m->branch, L.post_norm.f32(), kHidden, (int)count, m->stream);
+    if (count == 1) trace(m, "attn_residual-", layer, m->hidden, kHidden);
+    if (!ffn_rows(m, L, count)) return false;
+    if (count == 1) trace(m, "ffn_out-", layer, m->branch, kHidden);
+    q38::launch_add(m->hidden, m->branch, (long long)count * kHidden, m->stream);
+    if (count == 1 && layer < (int)kLayers) trace(m, "l_out-", layer, m->hidden, kHidden);
+    return true;
+}
+
+/* Target model over `count` (<= kBatch) tokens already in m->tokens at
+ * positions base..base+count-1: all 64 blocks, the output norm into
+ * m->target_norm and, if `logit_rows`, the LM head of the last `logit_rows`
+ * rows into m->logits (q38_batch_target_eval, qwen38_model.c:1241-1266). */
+bool target_rows(Q38Model *m, uint32_t count, uint32_t base, uint32_t logit_rows)
+{
+    if (!set_positions(m, base)) return false;
+    q38::launch_embed_q4k(m->hidden, m->embedding.data, m->tokens, (int)count, kHidden, kVocab, m->stream);
+    if (count == 1) trace(m, "model.input_embed", -1, m->hidden, kHidden);
+    for (uint32_t layer = 0; layer < kLayers; ++layer)
+        if (!layer_rows(m, (int)layer, count)) return false;
+    q38::launch_rmsnorm(m->target_norm, m->hidden, m->output_norm.f32(), kHidden, (int)count, kHidden, kHidden,
+                        m->stream);
+    if (logit_rows) {
+        const float *rows = m->target_norm + (size_t)(count - logit_rows) * kHidden;
+        if (!gemm(m, m->output, rows, logit_rows, m->logits)) return false;
+    }
+    return true;
+}
+
+bool upload_tokens(Q38Model *m, const uint32_t *tokens, uint32_t count)
+{
+    for (uint32_t i = 0; i < count; ++i) {
+        if (tokens[i] >= kVocab) return report("token id out of range");
+        m->host_words[i] = tokens[i];
+    }
+    return hip_ok(hipMemcpyAsync(m->tokens, m->host_words, count * sizeof(uint32_t), hipMemcpyHostToDevice,
+                                 m->stream),
+                  "token upload");
+}
+
+bool logits_to_host(Q38Model *m, const float *device_row)
+{
+    return hip_ok(hipMemcpyAsync(m->host_logits, device_row, kVocab * sizeof(float), hipMemcpyDeviceToHost,
+                                 m->stream),
+                  "logits download") &&
+           hip_ok(hipStreamSynchronize(m->stream), "logits download");
+}
+
+/* KV-cache rows of the MTP block for the tokens in m->tokens: eh_proj over
+ * [enorm(embedding) | hnorm(previous hidden)], attn_norm, K and V projections
+ * and the k-norm / RoPE / cache write at positions base.. (q38_mtp_catchup,
+ * qwen38_model.c:1268-1294).  The rest of the reference's catch-up block
+ * (queries, attention output, FFN) is computed there and never read, so it
+ * is not computed here. */
+bool mtp_catchup(Q38Model *m, uint32_t count, uint32_t base)
+{
+    const Layer &L = m->layers[kLayers];
+    if (!set_positions(m, base)) return false;
+    q38::launch_embed_q4k(m->hidden, m->mtp_embedding.data, m->tokens, (int)count, kHidden, kVocab, m->stream);
+    /* m->norm holds count rows of 2*kHidden: [enorm(e_t) | hnorm(prev_t)] */
+    q38::launch_rmsnorm(m->norm, m->hidden, m->enorm.f32(), kHidden, (int)count, 2 * kHidden, kHidden, m->stream);
+    q38::launch_rmsnorm(m->norm + kHidden, m->mtp_hidden, m->hnorm.f32(), kHidden, 1, 2 * kHidden, kHidden,
+                        m->stream);
+    if (count > 1)
+        q38::launch_rmsnorm(m->norm + 3 * kHidden, m->target_norm, m->hnorm.f32(), kHidden, (int)count - 1,
+                            2 * kHidden, kHidden, m->stream);
+    if (!gemm(m, m->eh_proj, m->norm, count, m->hidden)) return false;
+    q38::launch_rmsnorm(m->norm, m->hidden, L.attn_norm.f32(), kHidden, (int)count, kHidden, kHidden, m->stream);
+    q38::launch_quantize(m->norm, m->q8k, count * (kHidden / 256), m->stream);
+    if (!gemm_q(m, L.k, count, m->kbuf) || !gemm_q(m, L.v, count, m->vbuf)) return false;
+    const size_t kv_off = (size_t)(kLayers / 4) * m->context_length * kKVDim;
+    for (uint32_t t = 0; t < count; ++t)
+        q38::launch_kv_write(m->kbuf + (size_t)t * kKVDim, m->vbuf + (size_t)t * kKVDim, L.k_norm.f32(), m->rope,
+                             m->key_cache + kv_off, m->value_cache + kv_off, m->positions, (int)t, m->stream);
+    if (!hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm + (size_t)(count - 1) * kHidden,
+                               kHidden * sizeof(float), hipMemcpyDeviceToDevice, m->stream),
+                "mtp hidden"))
+        return false;
+    m->mtp_position = base + count;
+    return true;
+}
+
+/* one MTP draft step for the token in m->tokens[0] (q38_model_mtp_forward,
+ * qwen38_model.c:1588-1612; the block is q38_mtp_layer_forward :932-953) */
+bool mtp_step(Q38Model *m)
+{
+    if (!set_positions(m, m->mtp_position)) return false;
+    q38::launch_embed_q4k(m->hidden, m->mtp_embedding.data, m->tokens, 1, kHidden, kVocab, m->stream);
+    q38::launch_rmsnorm(m->norm, m->hidden, m->enorm.f32(), kHidden, 1, kHidden, kHidden, m->stream);
+    q38::launch_rmsnorm(m->norm + kHidden, m->mtp_hidden, m->hnorm.f32(), kHidden, 1, kHidden, kHidden, m->stream);
+    if (!gemm(m, m->eh_proj, m->norm, 1, m->hidden)) return false;
+    if (!layer_rows(m, (int)kLayers, 1)) return false;
+    q38::launch_rmsnorm(m->mtp_hidden, m->hidden, m->shared_head_norm.f32(), kHidden, 1, kHidden, kHidden, m->stream);
+    if (!gemm(m, m->mtp_output, m->mtp_hidden, 1, m->logits)) return false;
+    ++m->mtp_position;
+    return true;
+}
+
+bool checkpoint(Q38Model *m)
+{
+    m->ck_position = m->position;
+    m->ck_mtp_position = m->mtp_position;
+    return hip_ok(hipMemcpyAsync(m->ck_conv, m->conv_state, conv_count() * sizeof(float), hipMemcpyDeviceToDevice,
+                                 m->stream), "checkpoint") &&
+           hip_ok(hipMemcpyAsync(m->ck_delta, m->delta_state, delta_count() * sizeof(float),
+                                 hipMemcpyDeviceToDevice, m->stream), "checkpoint") &&
+           hip_ok(hipMemcpyAsync(m->ck_mtp_hidden, m->mtp_hidden, kHidden * sizeof(float), hipMemcpyDeviceToDevice,
+                                 m->stream), "checkpoint");
+}
+
+bool restore_target(Q38Model *m)
+{
+    m->position = m->ck_position;
+    return hip_ok(hipMemcpyAsync(m->conv_state, m->ck_conv, conv_count() * sizeof(float), hipMemcpyDeviceToDevice,
+                                 m->stream), "restore") &&
+           hip_ok(hipMemcpyAsync(m->delta_state, m->ck_delta, delta_count() * sizeof(float),
+                                 hipMemcpyDeviceToDevice, m->stream), "restore");
+}
+
+bool restore_mtp(Q38Model *m)
+{
+    m->mtp_position = m->ck_mtp_position;
+    return hip_ok(hipMemcpyAsync(m->mtp_hidden, m->ck_mtp_hidden, kHidden * sizeof(float), hipMemcpyDeviceToDevice,
+                                 m->stream), "restore");
+}
+
+}  // namespace
+
+extern "C" {
+
+Q38Model *q38_model_open_gguf(const char *path, uint32_t context_length)
+{
+    if (!path || context_length == 0) return nullptr;
+    Q38Model *m = new Q38Model();
+    m->context_length = context_length;
+    bool ok = m->gguf.open(path) && validate_base(m) && hip_ok(hipStreamCreateWithFlags(&m->stream,
+                                                                                          hipStreamNonBlocking),
+                                                                "stream");
+    ok = ok && (m->grid = q38::iq1m_grid_for_current_device()) != nullptr;
+    ok = ok && upload(m->gguf, &m->weights);
+    const uint8_t *base = static_cast<const uint8_t *>(m->weights);
+    ok = ok && bind_tensor(m->gguf, base, "token_embd.weight", &m->embedding) &&
+         bind_tensor(m->gguf, base, "output_norm.weight", &m->output_norm) && bind_tensor(m->gguf, base, "output.weight", &m->output);
+    for (uint32_t layer = 0; ok && layer < kLayers; ++layer) ok = bind_layer(&m->layers[layer], m->gguf, base, (int)layer);
+    ok = ok && expect(m->embedding, "token_embd.weight", kHidden, kVocab, false) &&
+         expect(m->output_norm, "output_norm.weight", kHidden, 0, true) &&
+         expect(m->output, "output.weight", kHidden, kVocab, false);
+    if (ok && m->embedding.type != Q4_K) ok = report("token_embd.weight must be Q4_K");
+    uint32_t blocks = 0;
+    if (ok && m->gguf.get_u32("qwen35.block_count", &blocks) && blocks == kTotalLayers)
+        ok = bind_mtp(m, m->gguf, base);
+    ok = ok && allocate_state(m) && clear_state(m);
+    if (!ok) {
+        release(m);
+        return nullptr;
+    }
+    return m;
+}
+
+int q38_model_attach_mtp_gguf(Q38Model *m, const char *path)
+{
+    if (!m || !path || m->position != 0 || m->mtp_position != 0 || m->mtp_enabled || m->mtp_weights_loaded ||
+        m->mtp_gguf.fd >= 0)
+        return 0;
+    const bool ok = m->mtp_gguf.open(path) && upload(m->mtp_gguf, &m->mtp_weights) &&
+                    bind_mtp(m, m->mtp_gguf, static_cast<const uint8_t *>(m->mtp_weights));
+    if (!ok) {
+        m->layers[kLayers] = Layer();
+        m->mtp_embedding = m->mtp_output = m->eh_proj = m->enorm = m->hnorm = m->shared_head_norm = DevTensor();
+        m->mtp_weights_loaded = false;
+        if (m->mtp_weights) (void)hipFree(m->mtp_weights);
+        m->mtp_weights = nullptr;
+        m->mtp_gguf.close();
+        return 0;
+    }
+    return 1;
+}
+
+void q38_model_close(Q38Model *m) { release(m); }
+
+void q38_model_reset(Q38Model *m)
+{
+    if (!m) return;
+    (void)clear_state(m);
+    m->position = 0;
+    m->mtp_position = 0;
+}
+
+int q38_model_forward_token(Q38Model *m, uint32_t token, const float **logits)
+{
+    if (!m || !logits || token >= kVocab || m->position >= m->context_length) return 0;
+    if (!upload_tokens(m, &token, 1) || !target_rows(m, 1, m->position, 1)) return 0;
+    if (m->mtp_enabled &&
+        !hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm, kHidden * sizeof(float), hipMemcpyDeviceToDevice,
+                               m->stream), "mtp hidden"))
+        return 0;
+    if (!logits_to_host(m, m->logits)) return 0;
+    ++m->position;
+    *logits = m->host_logits;
+    return 1;
+}
+
+int q38_model_forward_token_layers(Q38Model *m, uint32_t token, uint32_t layer_count, float *hidden_out)
+{
+    if (!m || !hidden_out || token >= kVocab || layer_count > kLayers || m->position >= m->context_length) return 0;
+    if (!upload_tokens(m, &token, 1) || !set_positions(m, m->position)) return 0;
+    q38::launch_embed_q4k(m->hidden, m->embedding.data, m->tokens, 1, kHidden, kVocab, m->stream);
+    trace(m, "model.input_embed", -1, m->hidden, kHidden);
+    for (uint32_t layer = 0; layer < layer_count; ++layer)
+        if (!layer_rows(m, (int)layer, 1)) return 0;
+    if (!hip_ok(hipMemcpyAsync(hidden_out, m->hidden, kHidden * sizeof(float), hipMemcpyDeviceToHost, m->stream),
+                "hidden download") ||
+        !hip_ok(hipStreamSynchronize(m->stream), "hidden download"))
+        return 0;
+    ++m->position;
+    return 1;
+}
+
+int q38_model_prefill(Q38Model *m, const uint32_t *tokens, uint32_t count, const float **logits)
+{
+    if (!m || !tokens || !count || !logits || count > m->context_length - m->position) return 0;
+    for (uint32_t i = 0; i < count; ++i)
+        if (tokens[i] >= kVocab) return 0;
+    const uint32_t base = m->position;
+    /* chunks of kBatch tokens through all blocks: every row's arithmetic is
+     * independent of the chunking, and state advances in token order */
+    for (uint32_t done = 0; done < count; done += kBatch) {
+        const uint32_t n = std::min(kBatch, count - done);
+        const bool last = done + n == count;
+        if (!upload_tokens(m, tokens + done, n) || !target_rows(m, n, base + done, last ? 1 : 0)) return 0;
+        if (m->mtp_enabled && !mtp_catchup(m, n, base + done)) return 0;
+    }
+    if (!logits_to_host(m, m->logits)) return 0;
+    m->position = base + count;
+    *logits = m->host_logits;
+    return 1;
+}
+
+int q38_model_enable_mtp(Q38Model *m)
+{
+    if (!m || m->position != 0 || m->mtp_position != 0) return 0;
+    if (!m->mtp_weights_loaded) {
+        fprintf(stderr, "qwen38: MTP weights are unavailable; attach the MTP GGUF first\n");
+        return 0;
+    }
+    if (!m->ck_conv && !(dalloc(&m->ck_conv, conv_count()) && dalloc(&m->ck_delta, delta_count()) &&
+                         dalloc(&m->ck_mtp_hidden, kHidden)))
+        return 0;
+    m->mtp_enabled = true;
+    return 1;
+}
+
+int q38_model_mtp_forward(Q38Model *m, uint32_t token, const float **logits)
+{
+    if (!m || !m->mtp_enabled || !logits || token >= kVocab || m->mtp_position >= m->context_length) return 0;
+    if (!upload_tokens(m, &token, 1) || !mtp_step(m) || !logits_to_host(m, m->logits)) return 0;
+    *logits = m->host_logits;
+    return 1;
+}
+
+int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_token, uint32_t draft_count,
+                                 uint32_t *accepted_tokens, uint32_t *accepted_count, const float **next_logits)
+{
+    if (!m || !m->mtp_enabled || !accepted_tokens || !accepted_count || !next_logits || token >= kVocab ||
+        draft_count == 0 || m->position != m->mtp_position || draft_count > m->context_length - m->position)
+        return 0;
+    if (draft_count > kBatch) return report("draft_count above 8 is not supported"), 0;
+    if (!checkpoint(m)) return 0;
+
+    /* drafts: chained MTP steps, argmax on the device (qwen38_model.c:1638-1648) */
+    uint32_t drafts[kBatch];
+    uint32_t n = 0, input = token;
+    bool ok = true;
+    while (ok && n < draft_count) {
+        if (m->mtp_position >= m->context_length) { ok = false; break; }
+        ok = upload_tokens(m, &input, 1) && mtp_step(m);
+        if (!ok) break;
+        q38::launch_argmax(m->logits, kVocab, 1, m->argmax_pv, m->argmax_pi, m->drafts + n, m->stream);
+        ok = hip_ok(hipMemcpyAsync(&m->host_words[40], m->drafts + n, 4, hipMemcpyDeviceToHost, m->stream), "draft") &&
+             hip_ok(hipStreamSynchronize(m->stream), "draft");
+        if (!ok) break;
+        input = m->host_words[40];
+        drafts[n++] = input;
+        if (input == stop_token) break;
+    }
+    if (!ok) {
+        (void)restore_mtp(m);
+        return 0;
+    }
+
+    /* verify rows [token, d0 .. d_{n-2}] in one batch, argmax per row and
+     * greedy acceptance on the device (qwen38_model.c:1655-1682) */
+    uint32_t inputs[kBatch];
+    inputs[0] = token;
+    for (uint32_t i = 1; i < n; ++i) inputs[i] = drafts[i - 1];
+    ok = upload_tokens(m, inputs, n) && target_rows(m, n, m->position, n);
+    if (ok) {
+        m->position = m->ck_position + n;
+        q38::launch_argmax(m->logits, kVocab, n, m->argmax_pv, m->argmax_pi, m->targets, m->stream);
+        q38::launch_accept(m->accept, m->targets, m->drafts, n, m->stream);
+        ok = hip_ok(hipMemcpyAsync(&m->host_words[44], m->accept, (n + 3) * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                                   m->stream), "acceptance") &&
+             hip_ok(hipStreamSynchronize(m->stream), "acceptance");
+    }
+    uint32_t consumed = 0, matched = 0;
+    uint32_t accepted[kBatch];
+    if (ok) {
+        consumed = m->host_words[44];
+        matched = m->host_words[45];
+        for (uint32_t i = 0; i < consumed; ++i) accepted[i] = m->host_words[47 + i];
+    }
+    const float *last_row = m->logits + (size_t)(consumed ? consumed - 1 : 0) * kVocab;
+    if (ok && consumed < n) {
+        /* rejected: restore the target state and replay the consumed rows
+         * (qwen38_model.c:1684-1691) */
+        ok = restore_target(m) && upload_tokens(m, inputs, consumed) &&
+             target_rows(m, consumed, m->position, 1);
+        last_row = m->logits;
+        if (ok) m->position = m->ck_position + consumed;
+    }
+    if (ok) {
+        ok = logits_to_host(m, last_row) && restore_mtp(m) && upload_tokens(m, inputs, consumed) &&
+             mtp_catchup(m, consumed, m->ck_mtp_position);
+        ok = ok && hip_ok(hipStreamSynchronize(m->stream), "catch-up");
+    }
+    if (!ok) {
+        (void)restore_target(m);
+        (void)restore_mtp(m);
+        (void)hipStreamSynchronize(m->stream);
+        return 0;
+    }
+    (void)matched;
+    for (uint32_t i = 0; i < consumed; ++i) accepted_tokens[i] = accepted[i];
+    *accepted_count = consumed;
+    *next_logits = m->host_logits;
+    return 1;
+}
+
+uint32_t q38_model_vocab_size(const Q38Model *m) { return m ? kVocab : 0; }
+uint32_t q38_model_position(const Q38Model *m) { return m ? m->position : 0; }
+uint32_t q38_model_context_length(const Q38Model *m) { return m ? m->context_length : 0; }
+
+}  // extern "C"

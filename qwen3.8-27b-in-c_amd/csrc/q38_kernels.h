@@ -1,0 +1,46 @@
+/* Host-side launchers of the gfx950 kernels (enqueue only; no synchronisation). */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q38 {
+
+/* q38_gemm.hip: y[m][rows] = W (rows x nblk*256, GGUF type) . x (m Q8_K rows);
+ * m <= 8.  `grid` is the device IQ1_M codebook (2048 x 8 int8). */
+bool launch_gemm(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, uint32_t nblk,
+                 const void *grid, hipStream_t stream);
+
+/* q38_misc.hip */
+void launch_quantize(const float *x, uint8_t *out, uint32_t nblocks, hipStream_t stream);
+uint32_t argmax_chunks(uint32_t count);
+void launch_argmax(const float *values, uint32_t count, uint32_t rows, float *pv, uint32_t *pi, uint32_t *out,
+                   hipStream_t stream);
+void launch_accept(uint32_t *result, const uint32_t *targets, const uint32_t *drafts, uint32_t rows,
+                   hipStream_t stream);
+
+/* q38_model.hip */
+void launch_rmsnorm(float *out, const float *in, const float *weight, int n, int rows, long long out_stride,
+                    long long in_stride, hipStream_t stream);
+void launch_add_rmsnorm(float *norm, float *hidden, const float *branch, const float *weight, int n, int rows,
+                        hipStream_t stream);
+void launch_add(float *hidden, const float *branch, long long n, hipStream_t stream);
+void launch_swiglu(float *gate, const float *up, long long n, hipStream_t stream);
+void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int count, int width, uint32_t vocab,
+                      hipStream_t stream);
+/* gated DeltaNet core of one row: conv + SiLU + q/k L2 norm + beta/alpha,
+ * the state update, then the per-head norm and z gate */
+void launch_deltanet_prep(float *qkv, float *beta, float *alpha, float *conv_state, const float *conv_w,
+                          const float *ssm_a, const float *ssm_dt, hipStream_t stream);
+void launch_deltanet_state(float *attn, float *delta_state, const float *qkv, const float *beta, const float *alpha,
+                           float query_scale, hipStream_t stream);
+void launch_deltanet_out(float *attn, const float *z, const float *ssm_norm, hipStream_t stream);
+void launch_attention(float *attn, float *q_buf, const float *q_and_gate, const float *key, const float *value,
+                      const float *q_norm, const float *k_norm, const float *rope, float *key_cache,
+                      float *value_cache, float *scores, int context, const uint32_t *position, int row_offset,
+                      hipStream_t stream);
+/* K-norm, RoPE and K/V cache write of one row without the query side */
+void launch_kv_write(const float *key, const float *value, const float *k_norm, const float *rope, float *key_cache,
+                     float *value_cache, const uint32_t *position, int row_offset, hipStream_t stream);
+
+}  // namespace q38

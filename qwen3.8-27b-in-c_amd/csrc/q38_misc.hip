@@ -40,7 +40,7 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restri
     const int k = idx & 3;
     const float mine = k == 0 ? v[0] : k == 1 ? v[1] : k == 2 ? v[2] : v[3];
     const float maximum = __shfl(mine, idx >> 2, 64);
-    const float inv = __fdiv_rn(-127.0f, maximum);
+    const float inv = div_rn(-127.0f, maximum);
 
     uint32_t packed = 0;
     int sum = 0;
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restri
     reinterpret_cast<uint32_t *>(blk + 4)[lane] = packed;
     sum = quad_sum(sum);
     if ((lane & 3) == 0) reinterpret_cast<int16_t *>(blk + 260)[lane >> 2] = static_cast<int16_t>(sum);
-    if (lane == 0) *reinterpret_cast<float *>(blk) = __fdiv_rn(1.0f, inv);
+    if (lane == 0) *reinterpret_cast<float *>(blk) = div_rn(1.0f, inv);
 }
 
 /* First-maximum selection: NaN never wins, ties go to the lower index.  With

@@ -1,0 +1,449 @@
+/* Decode-step kernels of the Qwen3.8 hybrid model on gfx950: embedding rows,
+ * RMS/L2 norms, SwiGLU, residual adds, the gated DeltaNet recurrence and the
+ * full-attention KV-cache decode.
+ *
+ * Every kernel reproduces the reference's fp32 operation order
+ * (src/qwen38/qwen38_model.c, compiled with -ffp-contract=off): plain
+ * products and sums round separately, fmaf appears only where the reference
+ * calls it or uses an FMA intrinsic, transcendentals are the exact restated
+ * expf/logf of q38_libm.h, and the double-precision squared sums of the norms
+ * reproduce the reference's sequential loop (see block_sum_squares).
+ */
+#include "q38_device.h"
+#include "q38_kernels.h"
+#include "q38_libm.h"
+#include "q38_math.h"
+
+namespace q38 {
+
+/* ---- exact sequential double sums ---------------------------------------- */
+
+/* The reference norms compute sum += (double)(x[i]*x[i]) for i = 0..n-1 in
+ * order and use only a monotone, float-rounded function of the sum:
+ * (float)(sum / n) for RMSNorm (qwen38_model.c:426-435) and (float)sum for
+ * the L2 norm (:608-614).  The block first sums in parallel (any order);
+ * for non-negative terms both that sum and the sequential one are within
+ * (n + 8) * 2^-53 relative of the exact sum, far inside the 2^-36 margin used
+ * here for n <= 65536.  If the float result is the same at both ends of the
+ * margin it is the reference's result; otherwise (about one call in 4000,
+ * and always for NaN) one thread redoes the sequential loop.  `post` is the
+ * float-rounding step. */
+template <int THREADS, typename Post>
+__device__ float block_sum_squares(const float *x, int n, Post post)
+{
+    static_assert(THREADS % 64 == 0 && THREADS <= 1024, "block size");
+    __shared__ double partial[THREADS / 64];
+    __shared__ float result;
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += THREADS) {
+        const float v = x[i];
+        s += (double)__fmul_rn(v, v);
+    }
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double total = 0.0;
+        for (int w = 0; w < THREADS / 64; ++w) total += partial[w];
+        const float lo = post(total * (1.0 - 0x1p-36));
+        const float hi = post(total * (1.0 + 0x1p-36));
+        if (lo == hi) {
+            result = lo;
+        } else {
+            double seq = 0.0;
+            for (int i = 0; i < n; ++i) seq += (double)__fmul_rn(x[i], x[i]);
+            result = post(seq);
+        }
+    }
+    __syncthreads();
+    const float r = result;
+    __syncthreads();
+    return r;
+}
+
+struct MeanPost {
+    double n;
+    __device__ float operator()(double s) const { return (float)(s / n); }
+};
+struct FloatPost {
+    __device__ float operator()(double s) const { return (float)s; }
+};
+
+/* ---- RMSNorm ------------------------------------------------------------- */
+
+/* out[r] = rmsnorm(in[r]) * weight for `rows` rows of n floats
+ * (q38_rmsnorm, qwen38_model.c:426-435): y = (x * scale) * w. */
+__global__ __launch_bounds__(256) void rmsnorm_kernel(float *__restrict__ out, const float *__restrict__ in,
+                                                      const float *__restrict__ weight, int n,
+                                                      long long out_stride, long long in_stride)
+{
+    const float *x = in + (long long)blockIdx.x * in_stride;
+    float *y = out + (long long)blockIdx.x * out_stride;
+    const float mean = block_sum_squares<256>(x, n, MeanPost{(double)n});
+    const float scale = rms_scale(mean);
+    for (int i = threadIdx.x; i < n; i += 256) y[i] = __fmul_rn(__fmul_rn(x[i], scale), weight[i]);
+}
+
+/* hidden += branch, then norm = rmsnorm(hidden) * weight (the residual add of
+ * qwen38_model.c:975/983 followed by the next block's norm). */
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *__restrict__ norm, float *__restrict__ hidden,
+                                                          const float *__restrict__ branch,
+                                                          const float *__restrict__ weight, int n)
+{
+    float *h = hidden + (long long)blockIdx.x * n;
+    const float *b = branch + (long long)blockIdx.x * n;
+    for (int i = threadIdx.x; i < n; i += 256) h[i] = __fadd_rn(h[i], b[i]);
+    __syncthreads();
+    const float mean = block_sum_squares<256>(h, n, MeanPost{(double)n});
+    const float scale = rms_scale(mean);
+    float *y = norm + (long long)blockIdx.x * n;
+    for (int i = threadIdx.x; i < n; i += 256) y[i] = __fmul_rn(__fmul_rn(h[i], scale), weight[i]);
+}
+
+__global__ __launch_bounds__(256) void add_kernel(float *__restrict__ hidden, const float *__restrict__ branch,
+                                                  long long n)
+{
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) hidden[i] = __fadd_rn(hidden[i], branch[i]);
+}
+
+/* gate[i] = silu(gate[i]) * up[i] (q38_swiglu scalar path, qwen38_model.c:532-549) */
+__global__ __launch_bounds__(256) void swiglu_kernel(float *__restrict__ gate, const float *__restrict__ up,
+                                                     long long n)
+{
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) gate[i] = __fmul_rn(siluf_exact(gate[i]), up[i]);
+}
+
+/* ---- embedding rows ------------------------------------------------------ */
+
+/* Dequantised Q4_K row (q38_tensor_row_f32 -> q38_dot_q4_k with unit
+ * vectors, src/qwen38/qwen38_quant.c:396-426, 3186-3223): element 64c+i of a
+ * block is (d*sc)*q - dmin*m, plus 0.0f (a -0 result becomes +0).  One block
+ * of 256 threads per (token, super-block). */
+__global__ __launch_bounds__(256) void embed_q4k_kernel(float *__restrict__ out, const uint8_t *__restrict__ w,
+                                                        const uint32_t *__restrict__ tokens, int blocks_per_row,
+                                                        uint32_t vocab)
+{
+    const int t = blockIdx.y;
+    const int b = blockIdx.x;
+    const uint32_t token = tokens[t];
+    if (token >= vocab) return;
+    const uint8_t *blk = w + ((size_t)token * blocks_per_row + b) * 144;
+    const int e = threadIdx.x;          /* element 0..255 */
+    const int c = e >> 6, hi = (e >> 5) & 1, i = e & 31;
+    const int j = 2 * c + hi;           /* sub-block */
+    const uint8_t *s = blk + 4;
+    int sc, m;
+    if (j < 4) {
+        sc = s[j] & 63;
+        m = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 0x0f) | ((s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+    const float d = f16_to_f32(blk[0] | (blk[1] << 8));
+    const float dmin = f16_to_f32(blk[2] | (blk[3] << 8));
+    const uint8_t qb = blk[16 + 32 * c + i];
+    const int q = hi ? (qb >> 4) : (qb & 15);
+    const float scaled = __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
+    const float v = __fadd_rn(__fsub_rn(scaled, __fmul_rn(dmin, (float)m)), 0.0f);
+    out[(size_t)t * blocks_per_row * 256 + (size_t)b * 256 + e] = v;
+}
+
+/* ---- gated DeltaNet ------------------------------------------------------ */
+
+constexpr int kQKV = 10240, kQKDim = 2048, kVHeads = 48, kHeadDim = 128;
+
+/* Causal conv (4 taps, state of 3 per channel), SiLU, per-head L2 norm of q
+ * and k, and the beta / alpha transforms (q38_linear_core,
+ * qwen38_model.c:720-757).  Blocks 0..79 each own 128 channels (blocks 0..31
+ * are the 16 q heads and 16 k heads); block 80 does beta/alpha. */
+__global__ __launch_bounds__(128) void deltanet_prep_kernel(float *__restrict__ qkv, float *__restrict__ conv_state,
+                                                            const float *__restrict__ conv_w,
+                                                            float *__restrict__ beta, float *__restrict__ alpha,
+                                                            const float *__restrict__ ssm_a,
+                                                            const float *__restrict__ ssm_dt)
+{
+    const int tid = threadIdx.x;
+    if (blockIdx.x == kQKV / 128) {
+        if (tid < kVHeads) {
+            beta[tid] = sigmoidf_exact(beta[tid]);
+            alpha[tid] = __fmul_rn(ssm_a[tid], softplusf_exact(__fadd_rn(alpha[tid], ssm_dt[tid])));
+        }
+        return;
+    }
+    const int ch = blockIdx.x * 128 + tid;
+    float *st = conv_state + (size_t)ch * 3;
+    const float *k = conv_w + (size_t)ch * 4;
+    const float x = qkv[ch];
+    float value = 0.0f;
+    value = __fadd_rn(value, __fmul_rn(st[0], k[0]));
+    value = __fadd_rn(value, __fmul_rn(st[1], k[1]));
+    value = __fadd_rn(value, __fmul_rn(st[2], k[2]));
+    value = __fadd_rn(value, __fmul_rn(x, k[3]));
+    st[0] = st[1];
+    st[1] = st[2];
+    st[2] = x;
+    const float y = siluf_exact(value);
+    if (ch >= 2 * kQKDim) {
+        qkv[ch] = y;
+        return;
+    }
+    __shared__ float head[128];
+    head[tid] = y;
+    __syncthreads();
+    const float sum = block_sum_squares<128>(head, 128, FloatPost{});
+    const float scale = div_rn(1.0f, fmaxf(sqrt_rn(sum), 1e-6f));
+    qkv[ch] = __fmul_rn(y, scale);
+}
+
+/* Sum of 32 per-lane values in the reference's AVX2 reduction order
+ * (q38_dot_f32_128, qwen38_model.c:616-637): lane l = 8*a + j holds the
+ * accumulator of vector a, element j; result = ((H0+H1)+(H2+H3)) with
+ * H[j] = Q[j] + Q[j+4], Q[j] = (P0[j]+P2[j]) + (P1[j]+P3[j]).
+ * Operates on 32-lane halves of the wavefront; every lane gets the result. */
+__device__ __forceinline__ float avx2_tree32(float v)
+{
+    v = __fadd_rn(v, __shfl_down(v, 16, 32));   /* l<16: P0+P2 (l<8), P1+P3 (8..15) */
+    v = __fadd_rn(v, __shfl_down(v, 8, 32));    /* l<8:  Q[l] */
+    v = __fadd_rn(v, __shfl_down(v, 4, 32));    /* l<4:  H[l] */
+    v = __fadd_rn(v, __shfl_down(v, 1, 32));    /* l=0: H0+H1, l=2: H2+H3 */
+    v = __fadd_rn(v, __shfl_down(v, 2, 32));    /* l=0: (H0+H1)+(H2+H3) */
+    return __shfl(v, 0, 32);
+}
+
+/* State update of one value head (qwen38_model.c:759-783): S *= decay; per
+ * column c: pred = dot(S_c, k); delta = (v[c] - pred) * beta;
+ * S_c = fma(k, delta, S_c); out[c] = dot(S_c, q) * (1/sqrt(128)).
+ * Columns are independent: 32 lanes per column (lane l owns elements
+ * l, l+32, l+64, l+96, the reference's fixed 4 x 8-lane accumulators), two
+ * columns per wavefront, eight per block of 256. */
+__global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__ out, float *__restrict__ state,
+                                                             const float *__restrict__ qkv,
+                                                             const float *__restrict__ beta,
+                                                             const float *__restrict__ alpha, float query_scale)
+{
+    const int column_global = blockIdx.x * 8 + (threadIdx.x >> 5);   /* 0 .. 48*128-1 */
+    const int h = column_global >> 7;
+    const int c = column_global & 127;
+    const int l = threadIdx.x & 31;
+    const int kh = h % 16;
+    const float *q = qkv + kh * kHeadDim;
+    const float *k = qkv + kQKDim + kh * kHeadDim;
+    const float *v = qkv + 2 * kQKDim + h * kHeadDim;
+    float *s = state + ((size_t)h * kHeadDim + c) * kHeadDim;
+    const float decay = q38_expf(alpha[h]);
+    float sv[4], kv[4], qv[4];
+    for (int a = 0; a < 4; ++a) {
+        sv[a] = __fmul_rn(s[32 * a + l], decay);
+        kv[a] = k[32 * a + l];
+        qv[a] = q[32 * a + l];
+    }
+    float p = 0.0f;
+    for (int a = 0; a < 4; ++a) p = __builtin_fmaf(sv[a], kv[a], p);
+    const float pred = avx2_tree32(p);
+    const float delta = __fmul_rn(__fsub_rn(v[c], pred), beta[h]);
+    float r = 0.0f;
+    for (int a = 0; a < 4; ++a) {
+        sv[a] = __builtin_fmaf(kv[a], delta, sv[a]);
+        s[32 * a + l] = sv[a];
+        r = __builtin_fmaf(sv[a], qv[a], r);
+    }
+    const float result = avx2_tree32(r);
+    if (l == 0) out[h * kHeadDim + c] = __fmul_rn(result, query_scale);
+}
+
+/* Per value head: RMSNorm over 128 (ssm_norm weight), then
+ * out *= silu(z) (qwen38_model.c:785-791). */
+__global__ __launch_bounds__(128) void deltanet_out_kernel(float *__restrict__ attn, const float *__restrict__ z,
+                                                           const float *__restrict__ norm_w)
+{
+    float *x = attn + blockIdx.x * kHeadDim;
+    const float mean = block_sum_squares<128>(x, kHeadDim, MeanPost{128.0});
+    const float scale = rms_scale(mean);
+    const int i = threadIdx.x;
+    const float y = __fmul_rn(__fmul_rn(x[i], scale), norm_w[i]);
+    x[i] = __fmul_rn(y, siluf_exact(z[blockIdx.x * kHeadDim + i]));
+}
+
+/* ---- full attention ------------------------------------------------------ */
+
+constexpr int kAttnHeads = 24, kKVHeads = 4, kAttnDim = 256, kKVDim = 1024;
+
+/* q / gate split, per-head RMSNorm of q and k (q_norm / k_norm weights),
+ * RoPE on dims 0..63 (pairs i, i+32) and the K/V cache write
+ * (q38_full_core, qwen38_model.c:816-846; q38_rope :697-713).  Blocks 0..23
+ * are q heads, 24..27 k heads, 28 copies v.  `rope` holds cos (32) then
+ * sin (32) per position, computed once on the host with the C library.
+ * `block_base` = 24 runs only the K/V part. */
+__global__ __launch_bounds__(256) void attn_prep_kernel(float *__restrict__ q_out, const float *__restrict__ q_and_gate,
+                                                        const float *__restrict__ key, const float *__restrict__ value,
+                                                        const float *__restrict__ q_norm,
+                                                        const float *__restrict__ k_norm,
+                                                        const float *__restrict__ rope, float *__restrict__ key_cache,
+                                                        float *__restrict__ value_cache,
+                                                        const uint32_t *__restrict__ position_ptr, int row_offset,
+                                                        int block_base)
+{
+    const uint32_t pos = *position_ptr + row_offset;
+    const int i = threadIdx.x;
+    const int block = blockIdx.x + block_base;
+    float *kc = key_cache + (size_t)pos * kKVDim;
+    if (block == kAttnHeads + kKVHeads) {
+        for (int e = i; e < kKVDim; e += 256) value_cache[(size_t)pos * kKVDim + e] = value[e];
+        return;
+    }
+    const bool is_q = block < kAttnHeads;
+    const int h = is_q ? block : block - kAttnHeads;
+    const float *src = is_q ? q_and_gate + h * 2 * kAttnDim : key + h * kAttnDim;
+    const float *w = is_q ? q_norm : k_norm;
+    const float mean = block_sum_squares<256>(src, kAttnDim, MeanPost{256.0});
+    const float scale = rms_scale(mean);
+    __shared__ float v[kAttnDim];
+    v[i] = __fmul_rn(__fmul_rn(src[i], scale), w[i]);
+    __syncthreads();
+    float y = v[i];
+    if (i < 64) {
+        const int pair = i & 31;
+        const float c = rope[(size_t)pos * 64 + pair];
+        const float s = rope[(size_t)pos * 64 + 32 + pair];
+        const float x0 = v[pair], x1 = v[pair + 32];
+        y = i < 32 ? __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s))
+                   : __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+    }
+    if (is_q) q_out[h * kAttnDim + i] = y;
+    else kc[h * kAttnDim + i] = y;
+}
+
+/* Decode attention of one q head over positions 0..pos of its KV head
+ * (GQA 6:1), qwen38_model.c:848-882: score_p = fmaf-chain over the 256 dims
+ * (i ascending) times 1/16; maximum; e_p = expf(score_p - max); denominator
+ * summed in position order; out_i = fmaf-chain over positions of
+ * (e_p / denominator) * v_p[i]; out_i *= sigmoid(gate_i).
+ * One block of 256 threads per head; `scores` is [24][context] scratch. */
+__global__ __launch_bounds__(256) void attn_decode_kernel(float *__restrict__ out, const float *__restrict__ q,
+                                                          const float *__restrict__ q_and_gate,
+                                                          const float *__restrict__ key_cache,
+                                                          const float *__restrict__ value_cache,
+                                                          float *__restrict__ scores, int context,
+                                                          const uint32_t *__restrict__ position_ptr, int row_offset)
+{
+    const int h = blockIdx.x;
+    const int kvh = h / (kAttnHeads / kKVHeads);
+    const int tid = threadIdx.x;
+    const int n = (int)(*position_ptr + row_offset) + 1;
+    float *sc = scores + (size_t)h * context;
+    __shared__ float qs[kAttnDim];
+    __shared__ float red[4];
+    __shared__ float denom_s;
+    qs[tid] = q[h * kAttnDim + tid];
+    __syncthreads();
+
+    float local_max = -__builtin_inff();
+    for (int p = tid; p < n; p += 256) {
+        const float4 *k4 = reinterpret_cast<const float4 *>(key_cache + (size_t)p * kKVDim + kvh * kAttnDim);
+        float s = 0.0f;
+        for (int i4 = 0; i4 < kAttnDim / 4; ++i4) {
+            const float4 kk = k4[i4];
+            s = __builtin_fmaf(qs[4 * i4 + 0], kk.x, s);
+            s = __builtin_fmaf(qs[4 * i4 + 1], kk.y, s);
+            s = __builtin_fmaf(qs[4 * i4 + 2], kk.z, s);
+            s = __builtin_fmaf(qs[4 * i4 + 3], kk.w, s);
+        }
+        s = __fmul_rn(s, 0.0625f);
+        sc[p] = s;
+        local_max = fmaxf(local_max, s);
+    }
+    /* the reference's running max (score > maximum from -inf) equals the
+     * max over non-NaN scores; NaN scores never win */
+    for (int off = 32; off > 0; off >>= 1) local_max = fmaxf(local_max, __shfl_xor(local_max, off, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = local_max;
+    __syncthreads();
+    const float maximum = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int p = tid; p < n; p += 256) sc[p] = q38_expf(__fsub_rn(sc[p], maximum));
+    __syncthreads();
+    if (tid == 0) {
+        float d = 0.0f;
+        for (int p = 0; p < n; ++p) d = __fadd_rn(d, sc[p]);
+        denom_s = d;
+    }
+    __syncthreads();
+    const float denominator = denom_s;
+    for (int p = tid; p < n; p += 256) sc[p] = div_rn(sc[p], denominator);
+    __syncthreads();
+    float o = 0.0f;
+    const float *vcol = value_cache + kvh * kAttnDim + tid;
+    for (int p = 0; p < n; ++p) o = __builtin_fmaf(sc[p], vcol[(size_t)p * kKVDim], o);
+    const float g = q_and_gate[h * 2 * kAttnDim + kAttnDim + tid];
+    out[h * kAttnDim + tid] = __fmul_rn(o, sigmoidf_exact(g));
+}
+
+/* ---- launchers ----------------------------------------------------------- */
+
+void launch_rmsnorm(float *out, const float *in, const float *weight, int n, int rows, long long out_stride,
+                    long long in_stride, hipStream_t stream)
+{
+    rmsnorm_kernel<<<rows, 256, 0, stream>>>(out, in, weight, n, out_stride, in_stride);
+}
+
+void launch_add_rmsnorm(float *norm, float *hidden, const float *branch, const float *weight, int n, int rows,
+                        hipStream_t stream)
+{
+    add_rmsnorm_kernel<<<rows, 256, 0, stream>>>(norm, hidden, branch, weight, n);
+}
+
+void launch_add(float *hidden, const float *branch, long long n, hipStream_t stream)
+{
+    add_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(hidden, branch, n);
+}
+
+void launch_swiglu(float *gate, const float *up, long long n, hipStream_t stream)
+{
+    swiglu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(gate, up, n);
+}
+
+void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int count, int width, uint32_t vocab,
+                      hipStream_t stream)
+{
+    embed_q4k_kernel<<<dim3(width / 256, count), 256, 0, stream>>>(out, w, tokens, width / 256, vocab);
+}
+
+void launch_deltanet_prep(float *qkv, float *beta, float *alpha, float *conv_state, const float *conv_w,
+                          const float *ssm_a, const float *ssm_dt, hipStream_t stream)
+{
+    deltanet_prep_kernel<<<kQKV / 128 + 1, 128, 0, stream>>>(qkv, conv_state, conv_w, beta, alpha, ssm_a, ssm_dt);
+}
+
+void launch_deltanet_state(float *attn, float *delta_state, const float *qkv, const float *beta, const float *alpha,
+                           float query_scale, hipStream_t stream)
+{
+    deltanet_state_kernel<<<kVHeads * kHeadDim / 8, 256, 0, stream>>>(attn, delta_state, qkv, beta, alpha,
+                                                                     query_scale);
+}
+
+void launch_deltanet_out(float *attn, const float *z, const float *ssm_norm, hipStream_t stream)
+{
+    deltanet_out_kernel<<<kVHeads, 128, 0, stream>>>(attn, z, ssm_norm);
+}
+
+void launch_attention(float *attn, float *q_buf, const float *q_and_gate, const float *key, const float *value,
+                      const float *q_norm, const float *k_norm, const float *rope, float *key_cache,
+                      float *value_cache, float *scores, int context, const uint32_t *position, int row_offset,
+                      hipStream_t stream)
+{
+    attn_prep_kernel<<<kAttnHeads + kKVHeads + 1, 256, 0, stream>>>(q_buf, q_and_gate, key, value, q_norm, k_norm,
+                                                                     rope, key_cache, value_cache, position,
+                                                                     row_offset, 0);
+    attn_decode_kernel<<<kAttnHeads, 256, 0, stream>>>(attn, q_buf, q_and_gate, key_cache, value_cache, scores,
+                                                       context, position, row_offset);
+}
+
+void launch_kv_write(const float *key, const float *value, const float *k_norm, const float *rope, float *key_cache,
+                     float *value_cache, const uint32_t *position, int row_offset, hipStream_t stream)
+{
+    attn_prep_kernel<<<kKVHeads + 1, 256, 0, stream>>>(nullptr, nullptr, key, value, nullptr, k_norm, rope, key_cache,
+                                                       value_cache, position, row_offset, kAttnHeads);
+}
+
+}  // namespace q38

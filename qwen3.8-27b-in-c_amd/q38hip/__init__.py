@@ -49,7 +49,11 @@ def make_tensor(data_ptr, qtype, width, rows, nbytes=0):
 # Every symbol the C header declares (tests check the library exports them).
 EXPORTS = ("q38_f16_to_f32", "q38_quantize_q8_k", "q38_tensor_gemv_q8_k", "q38_tensor_gemm_q8_k",
            "q38hip_quantize_q8_k", "q38hip_gemm_q8_k", "q38hip_argmax", "q38hip_accept",
-           "q38hip_last_error", "q38hip_synchronize")
+           "q38hip_last_error", "q38hip_synchronize",
+           "q38_model_open_gguf", "q38_model_attach_mtp_gguf", "q38_model_close", "q38_model_reset",
+           "q38_model_forward_token", "q38_model_prefill", "q38_model_enable_mtp", "q38_model_mtp_forward",
+           "q38_model_speculative_greedy", "q38_model_forward_token_layers", "q38_model_vocab_size",
+           "q38_model_position", "q38_model_context_length")
 
 
 def load_library(path=LIB_PATH):

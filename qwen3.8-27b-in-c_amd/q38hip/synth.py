@@ -12,6 +12,8 @@ engine reads (shape[0] = input width, shape[1] = output rows):
 * Q6_K  210-byte blocks: ql[128] @0, qh[64] @128, int8 scales[16] @192,
   fp16 d @208 (ggml-common.h:362-368).
 """
+import os
+
 import numpy as np
 
 Q4_K, Q6_K, IQ1_M = 12, 14, 29
@@ -80,3 +82,20 @@ def matrix(qtype, rows, width, seed, sigma=0.01):
 def activations(width, seed, count=1):
     """fp32 rows ~ N(0, 1), shape [count, width]."""
     return _rng(seed).normal(0.0, 1.0, size=(count, width)).astype(np.float32)
+
+
+SYNTH_GGUF = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "synth", "q38_synth_gguf")
+MODEL_GGUF_BYTES = {"q4km": 15704910464}
+
+
+def write_model_gguf(path, seed, variant="q4km"):
+    """Write the deterministic synthetic 27B-shaped GGUF (synth/q38_synth_gguf.c)
+    to `path` unless a file of the expected size is already there."""
+    import subprocess
+    expected = MODEL_GGUF_BYTES.get(variant)
+    if expected and os.path.exists(path) and os.path.getsize(path) == expected:
+        return path
+    if not os.path.exists(SYNTH_GGUF):
+        raise RuntimeError("synthetic GGUF writer not built: make -C qwen3.8-27b-in-c_amd")
+    subprocess.run([SYNTH_GGUF, path, str(seed), variant], check=True)
+    return path

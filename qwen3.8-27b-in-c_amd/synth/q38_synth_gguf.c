@@ -1,0 +1,336 @@
+/* Deterministic synthetic Qwen3.8-27B GGUF writer (random-init weights).
+ *
+ * Writes the 65-block "qwen35" GGUF that the reference engine's loader accepts
+ * (metadata and tensor contract of src/qwen38/qwen38_model.c:196-319 and
+ * src/io/qwen38_gguf.c:263-370): 64 layers (every fourth a full-attention
+ * layer, the rest DeltaNet), the MTP block 64 with its nextn.* tensors, a Q4_K
+ * token embedding and a Q6_K LM head.  Layer matrices are Q4_K ("q4km") or
+ * IQ1_M ("iq1m").
+ *
+ * Every byte is a pure function of (seed, tensor index, position): a
+ * splitmix64 hash of a counter, so the file is identical on every host and
+ * thread count.  Block scales are chosen so that the effective weights have
+ * mean ~0 and standard deviation ~1/sqrt(fan_in), which keeps 64 random layers
+ * finite:
+ *   Q4_K  w = d*sc*q - dmin*m with dmin = 8d and m = round(15 sc / 16), so
+ *         each 32-element sub-block is centred (q uniform 0..15);
+ *   Q6_K  w = d*sc*(q-32), sc uniform int8;
+ *   IQ1_M w = d*(2s+1)*(grid +- 1/8), grid values in {-1,0,1}.
+ *
+ * Usage: q38_synth_gguf OUT.gguf SEED q4km|iq1m
+ */
+#define _GNU_SOURCE
+#include <fcntl.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+enum { F32 = 0, Q4_K = 12, Q6_K = 14, IQ1_M = 29 };
+enum { HIDDEN = 5120, FFN = 17408, VOCAB = 248320, LAYERS = 64 };
+
+static uint64_t mix64(uint64_t z)
+{
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+static uint64_t hash3(uint64_t seed, uint64_t tensor, uint64_t counter)
+{
+    return mix64(mix64(seed ^ (tensor * 0xd1b54a32d192ed03ull)) ^ counter);
+}
+
+/* uniform in [0, 1) from the top 53 bits */
+static double unit(uint64_t h) { return (double)(h >> 11) * 0x1p-53; }
+
+/* IEEE binary16, round to nearest even (finite, |x| < 65504) */
+static uint16_t f32_to_f16(float value)
+{
+    uint32_t x;
+    memcpy(&x, &value, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    x &= 0x7fffffffu;
+    if (x >= 0x477fe000u) return (uint16_t)(sign | 0x7c00u);          /* overflow */
+    if (x < 0x38800000u) {                                           /* subnormal half */
+        if (x < 0x33000000u) return (uint16_t)sign;                  /* < 2^-25 -> 0 */
+        const uint32_t e = x >> 23, m = (x & 0x7fffffu) | 0x800000u;
+        const uint32_t shift = 126 - e;                              /* 14..24 */
+        uint32_t h = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (h & 1))) ++h;
+        return (uint16_t)(sign | h);
+    }
+    uint32_t h = ((x >> 13) - (112u << 10));
+    const uint32_t rem = x & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1))) ++h;
+    return (uint16_t)(sign | h);
+}
+
+typedef struct {
+    char name[64];
+    uint32_t n_dims;
+    uint64_t shape[2];
+    uint32_t type;
+    uint64_t offset;
+    uint64_t nbytes;
+    int kind;      /* 0 matrix, 1 norm weight, 2 conv, 3 dt bias, 4 ssm_a */
+} Tensor;
+
+static Tensor tensors[1024];
+static int tensor_count;
+
+static uint64_t block_bytes(uint32_t type)
+{
+    switch (type) {
+    case Q4_K: return 144;
+    case Q6_K: return 210;
+    case IQ1_M: return 56;
+    default: return 4;
+    }
+}
+
+static void add(const char *name, uint64_t width, uint64_t rows, uint32_t type, int kind)
+{
+    Tensor *t = &tensors[tensor_count++];
+    snprintf(t->name, sizeof(t->name), "%s", name);
+    t->n_dims = rows ? 2 : 1;
+    t->shape[0] = width;
+    t->shape[1] = rows ? rows : 1;
+    t->type = type;
+    t->kind = kind;
+    const uint64_t elements = width * (rows ? rows : 1);
+    t->nbytes = type == F32 ? elements * 4 : elements / 256 * block_bytes(type);
+}
+
+static void add_layer(int layer, uint32_t m)
+{
+    char name[64];
+#define T(suffix, w, r, type, kind) \
+    do { snprintf(name, sizeof(name), "blk.%d.%s", layer, suffix); add(name, w, r, type, kind); } while (0)
+    T("attn_norm.weight", HIDDEN, 0, F32, 1);
+    T("post_attention_norm.weight", HIDDEN, 0, F32, 1);
+    T("ffn_gate.weight", HIDDEN, FFN, m, 0);
+    T("ffn_up.weight", HIDDEN, FFN, m, 0);
+    T("ffn_down.weight", FFN, HIDDEN, m, 0);
+    if ((layer + 1) % 4 == 0 || layer == LAYERS) {
+        T("attn_q.weight", HIDDEN, 12288, m, 0);
+        T("attn_k.weight", HIDDEN, 1024, m, 0);
+        T("attn_v.weight", HIDDEN, 1024, m, 0);
+        T("attn_output.weight", 6144, HIDDEN, m, 0);
+        T("attn_q_norm.weight", 256, 0, F32, 1);
+        T("attn_k_norm.weight", 256, 0, F32, 1);
+    } else {
+        T("attn_qkv.weight", HIDDEN, 10240, m, 0);
+        T("attn_gate.weight", HIDDEN, 6144, m, 0);
+        T("ssm_alpha.weight", HIDDEN, 48, m, 0);
+        T("ssm_beta.weight", HIDDEN, 48, m, 0);
+        T("ssm_conv1d.weight", 4, 10240, F32, 2);
+        T("ssm_dt.bias", 48, 0, F32, 3);
+        T("ssm_a", 48, 0, F32, 4);
+        T("ssm_norm.weight", 128, 0, F32, 1);
+        T("ssm_out.weight", 6144, HIDDEN, m, 0);
+    }
+    if (layer == LAYERS) {
+        T("nextn.eh_proj.weight", 2 * HIDDEN, HIDDEN, m, 0);
+        T("nextn.enorm.weight", HIDDEN, 0, F32, 1);
+        T("nextn.hnorm.weight", HIDDEN, 0, F32, 1);
+        T("nextn.shared_head_norm.weight", HIDDEN, 0, F32, 1);
+    }
+#undef T
+}
+
+/* ---- block generators ---------------------------------------------------- */
+
+static void fill_words(uint8_t *out, uint64_t bytes, uint64_t seed, uint64_t tid, uint64_t counter)
+{
+    for (uint64_t i = 0; i < bytes; i += 8) {
+        const uint64_t h = hash3(seed, tid, counter + i / 8);
+        memcpy(out + i, &h, bytes - i < 8 ? bytes - i : 8);
+    }
+}
+
+static void q4k_block(uint8_t *b, uint64_t seed, uint64_t tid, uint64_t index, double base)
+{
+    fill_words(b, 144, seed, tid, index * 32);
+    const uint64_t h = hash3(seed, tid, index * 32 + 30);
+    const float d = (float)(base * (0.5 + unit(h)));
+    const uint16_t dh = f32_to_f16(d), mh = f32_to_f16(8.0f * d);
+    memcpy(b, &dh, 2);
+    memcpy(b + 2, &mh, 2);
+    /* 6-bit scales sc[j] from the random bytes, mins m[j] = round(15 sc / 16) */
+    uint8_t sc[8], mn[8];
+    for (int j = 0; j < 8; ++j) {
+        sc[j] = b[4 + j] & 63;
+        mn[j] = (uint8_t)((15 * sc[j] + 8) / 16);
+    }
+    uint8_t *s = b + 4;
+    for (int j = 0; j < 4; ++j) {
+        s[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+        s[j + 4] = (uint8_t)((mn[j] & 63) | ((mn[j + 4] >> 4) << 6));
+        s[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4));
+    }
+}
+
+static void q6k_block(uint8_t *b, uint64_t seed, uint64_t tid, uint64_t index, double base)
+{
+    fill_words(b, 210, seed, tid, index * 32);
+    const uint64_t h = hash3(seed, tid, index * 32 + 30);
+    const uint16_t dh = f32_to_f16((float)(base * (0.5 + unit(h))));
+    memcpy(b + 208, &dh, 2);
+}
+
+static void iq1m_block(uint8_t *b, uint64_t seed, uint64_t tid, uint64_t index, double base)
+{
+    fill_words(b, 56, seed, tid, index * 8);
+    const uint64_t h = hash3(seed, tid, index * 8 + 7);
+    const uint16_t dh = f32_to_f16((float)(base * (0.5 + unit(h))));
+    for (int i = 0; i < 4; ++i) {
+        uint16_t v;
+        memcpy(&v, b + 48 + 2 * i, 2);
+        v = (uint16_t)((v & 0x0fffu) | (((dh >> (4 * i)) & 15u) << 12));
+        memcpy(b + 48 + 2 * i, &v, 2);
+    }
+}
+
+static float f32_value(const Tensor *t, uint64_t seed, uint64_t tid, uint64_t i)
+{
+    const double u = unit(hash3(seed, tid, i));
+    switch (t->kind) {
+    case 1: return (float)(0.9 + 0.2 * u);            /* norm weights */
+    case 2: return (float)(1.2 * u - 0.6);            /* conv taps */
+    case 3: return (float)(2.0 * u - 1.0);            /* dt bias */
+    case 4: return (float)(-(0.05 + 0.95 * u));       /* ssm_a < 0 */
+    default: return 0.0f;
+    }
+}
+
+/* Fill bytes [begin, end) of tensor t (block aligned for quantised types). */
+static void generate(const Tensor *t, uint64_t seed, uint64_t tid, uint64_t begin, uint64_t end, uint8_t *out)
+{
+    if (t->type == F32) {
+        for (uint64_t i = begin / 4; i < end / 4; ++i) {
+            const float v = f32_value(t, seed, tid, i);
+            memcpy(out + (i * 4 - begin), &v, 4);
+        }
+        return;
+    }
+    const uint64_t bb = block_bytes(t->type);
+    const double fan_in = (double)t->shape[0];
+    for (uint64_t off = begin; off < end; off += bb) {
+        const uint64_t index = off / bb;
+        uint8_t *b = out + (off - begin);
+        if (t->type == Q4_K) q4k_block(b, seed, tid, index, 1.0 / (168.0 * sqrt(fan_in)));
+        else if (t->type == Q6_K) q6k_block(b, seed, tid, index, 1.0 / (1367.0 * sqrt(fan_in)));
+        else iq1m_block(b, seed, tid, index, 1.0 / (7.5 * sqrt(fan_in)));
+    }
+}
+
+/* ---- GGUF header ---------------------------------------------------------- */
+
+typedef struct { uint8_t *p; size_t n, cap; } Buf;
+
+static void put(Buf *b, const void *data, size_t n)
+{
+    if (b->n + n > b->cap) {
+        b->cap = (b->n + n) * 2;
+        b->p = realloc(b->p, b->cap);
+    }
+    memcpy(b->p + b->n, data, n);
+    b->n += n;
+}
+static void put_u32(Buf *b, uint32_t v) { put(b, &v, 4); }
+static void put_u64(Buf *b, uint64_t v) { put(b, &v, 8); }
+static void put_str(Buf *b, const char *s) { put_u64(b, strlen(s)); put(b, s, strlen(s)); }
+static void meta_u32(Buf *b, const char *key, uint32_t v) { put_str(b, key); put_u32(b, 4); put_u32(b, v); }
+
+int main(int argc, char **argv)
+{
+    if (argc != 4 || (strcmp(argv[3], "q4km") && strcmp(argv[3], "iq1m"))) {
+        fprintf(stderr, "usage: %s OUT.gguf SEED q4km|iq1m\n", argv[0]);
+        return 2;
+    }
+    const uint64_t seed = strtoull(argv[2], NULL, 0);
+    const uint32_t m = strcmp(argv[3], "q4km") == 0 ? Q4_K : IQ1_M;
+
+    add("token_embd.weight", HIDDEN, VOCAB, Q4_K, 0);
+    add("output_norm.weight", HIDDEN, 0, F32, 1);
+    add("output.weight", HIDDEN, VOCAB, Q6_K, 0);
+    for (int layer = 0; layer <= LAYERS; ++layer) add_layer(layer, m);
+
+    uint64_t offset = 0;
+    for (int i = 0; i < tensor_count; ++i) {
+        tensors[i].offset = offset;
+        offset = (offset + tensors[i].nbytes + 31) & ~31ull;
+    }
+    const uint64_t data_bytes = offset;
+
+    Buf h = {0};
+    put_u32(&h, 0x46554747u);
+    put_u32(&h, 3);
+    put_u64(&h, (uint64_t)tensor_count);
+    put_u64(&h, 14);
+    put_str(&h, "general.architecture"); put_u32(&h, 8); put_str(&h, "qwen35");
+    meta_u32(&h, "general.alignment", 32);
+    meta_u32(&h, "qwen35.block_count", LAYERS + 1);
+    meta_u32(&h, "qwen35.nextn_predict_layers", 1);
+    meta_u32(&h, "qwen35.embedding_length", HIDDEN);
+    meta_u32(&h, "qwen35.feed_forward_length", FFN);
+    meta_u32(&h, "qwen35.attention.head_count", 24);
+    meta_u32(&h, "qwen35.attention.head_count_kv", 4);
+    meta_u32(&h, "qwen35.full_attention_interval", 4);
+    meta_u32(&h, "qwen35.ssm.state_size", 128);
+    meta_u32(&h, "qwen35.ssm.group_count", 16);
+    meta_u32(&h, "qwen35.ssm.time_step_rank", 48);
+    meta_u32(&h, "qwen35.ssm.inner_size", 6144);
+    meta_u32(&h, "general.file_type", m == Q4_K ? 15u : 31u);
+    for (int i = 0; i < tensor_count; ++i) {
+        const Tensor *t = &tensors[i];
+        put_str(&h, t->name);
+        put_u32(&h, t->n_dims);
+        for (uint32_t d = 0; d < t->n_dims; ++d) put_u64(&h, t->shape[d]);
+        put_u32(&h, t->type);
+        put_u64(&h, t->offset);
+    }
+    const uint64_t data_start = (h.n + 31) & ~31ull;
+    while (h.n < data_start) put(&h, "", 1);
+
+    const int fd = open(argv[1], O_CREAT | O_TRUNC | O_WRONLY, 0644);
+    if (fd < 0) { perror(argv[1]); return 1; }
+    if (ftruncate(fd, (off_t)(data_start + data_bytes)) != 0) { perror("ftruncate"); return 1; }
+    if (pwrite(fd, h.p, h.n, 0) != (ssize_t)h.n) { perror("pwrite"); return 1; }
+
+    /* work items: 4 MiB slices of every tensor, block aligned */
+    const uint64_t slice = 4u << 20;
+    int failed = 0;
+    uint64_t written = 0, next_report = data_bytes / 10;
+    for (int i = 0; i < tensor_count; ++i) {
+        const Tensor *t = &tensors[i];
+        const uint64_t unit_bytes = t->type == F32 ? 4 : block_bytes(t->type);
+        const uint64_t step = slice / unit_bytes * unit_bytes;
+        const int64_t slices = (int64_t)((t->nbytes + step - 1) / step);
+#pragma omp parallel for schedule(dynamic, 1) reduction(| : failed)
+        for (int64_t s = 0; s < slices; ++s) {
+            const uint64_t begin = (uint64_t)s * step;
+            const uint64_t end = begin + step < t->nbytes ? begin + step : t->nbytes;
+            uint8_t *buffer = malloc(end - begin);
+            generate(t, seed, (uint64_t)i, begin, end, buffer);
+            if (pwrite(fd, buffer, end - begin, (off_t)(data_start + t->offset + begin)) != (ssize_t)(end - begin))
+                failed |= 1;
+            free(buffer);
+        }
+        written += t->nbytes;
+        if (written >= next_report) {
+            printf("  %3d%% (%d/%d tensors)\n", (int)(100 * written / data_bytes), i + 1, tensor_count);
+            fflush(stdout);
+            next_report += data_bytes / 10;
+        }
+    }
+    if (close(fd) != 0 || failed) { fprintf(stderr, "write failed\n"); return 1; }
+    printf("wrote %s: %d tensors, %llu bytes\n", argv[1], tensor_count,
+           (unsigned long long)(data_start + data_bytes));
+    return 0;
+}

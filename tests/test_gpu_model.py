@@ -1,0 +1,102 @@
+"""Full-model parity on the GPU: the engine ABI of libq38hip (include/q38model.h)
+against the compiled reference engine's outputs on the same synthetic
+27B-shaped Q4_K_M checkpoint (tests/golden/model_q4km_s1.npz, written by
+tests/golden/make_model_golden.py from oracle/_ref).
+
+Bar: bit-identical.  Hidden states after 1 and 4 blocks compare as uint32;
+every logits row compares by SHA-256 of its float32 bytes; token ids and
+accepted counts compare exactly.  Each scenario follows the reference's own
+call sequence (src/cli/qwen38_spec_bench.c:37-83)."""
+import hashlib
+import os
+import time
+
+import numpy as np
+import pytest
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "model_q4km_s1.npz")
+NO_STOP = 0xFFFFFFFF
+
+
+def digest(logits):
+    return hashlib.sha256(np.ascontiguousarray(logits, dtype=np.float32).tobytes()).hexdigest()
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return dict(np.load(GOLDEN))
+
+
+@pytest.fixture(scope="module")
+def model(device, model_gguf, golden):
+    from q38hip.model import Model
+    t0 = time.time()
+    context = int(golden["seed"][1])
+    m = Model.open(model_gguf, context)
+    print("model open + upload %.1f s" % (time.time() - t0), flush=True)
+    m.enable_mtp()
+    yield m
+    m.close()
+
+
+def same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+def test_hidden_after_first_blocks(model, golden):
+    prompt = golden["prompt"]
+    model.reset()
+    h1 = model.forward_token_layers(int(prompt[0]), 1)
+    assert np.isfinite(h1).all()
+    assert same_bits(h1, golden["hidden_l1"]), "max abs diff %g" % np.abs(h1 - golden["hidden_l1"]).max()
+    model.reset()
+    h4 = model.forward_token_layers(int(prompt[0]), 4)
+    assert same_bits(h4, golden["hidden_l4"]), "max abs diff %g" % np.abs(h4 - golden["hidden_l4"]).max()
+
+
+def test_prefill_and_greedy_decode(model, golden):
+    model.reset()
+    logits = model.prefill(golden["prompt"])
+    sample = logits[::1009]
+    assert same_bits(sample, golden["prefill_sample"]), \
+        "prefill logits differ: max rel %g" % (np.abs(sample - golden["prefill_sample"]).max()
+                                              / np.abs(golden["prefill_sample"]).max())
+    assert digest(logits) == golden["greedy_digests"][0]
+    tokens = [int(np.argmax(logits))]
+    for step in range(1, len(golden["greedy_tokens"])):
+        logits = model.forward_token(tokens[-1])
+        assert digest(logits) == golden["greedy_digests"][step], "decode step %d" % step
+        tokens.append(int(np.argmax(logits)))
+    assert tokens == [int(t) for t in golden["greedy_tokens"]]
+    assert model.position() == len(golden["prompt"]) + len(tokens) - 1
+
+
+def test_mtp_drafts(model, golden):
+    model.reset()
+    token = int(np.argmax(model.prefill(golden["prompt"])))
+    for i, want in enumerate(golden["mtp_drafts"]):
+        logits = model.mtp_forward(token)
+        assert digest(logits) == golden["mtp_digests"][i], "draft %d" % i
+        token = int(np.argmax(logits))
+        assert token == int(want)
+
+
+def test_speculative_greedy_matches_reference(model, golden):
+    model.reset()
+    produced = [int(np.argmax(model.prefill(golden["prompt"])))]
+    want_tokens = [int(t) for t in golden["spec_tokens"]]
+    counts = []
+    step = 0
+    while len(produced) < len(want_tokens):
+        requested = min(3, len(want_tokens) - len(produced))
+        accepted, logits = model.speculative_greedy(produced[-1], NO_STOP, requested)
+        assert digest(logits) == golden["spec_digests"][step], "transaction %d" % step
+        counts.append(len(accepted))
+        produced.extend(int(t) for t in accepted)
+        step += 1
+    assert produced[:len(want_tokens)] == want_tokens
+    assert counts == [int(c) for c in golden["spec_counts"]]
+    # speculative decoding reproduces plain greedy decoding
+    assert produced[:len(want_tokens)] == [int(t) for t in golden["greedy_tokens"]]
