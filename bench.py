@@ -1,13 +1,22 @@
 #!/usr/bin/env python3
 """Benchmark of the decode hot path on one MI355X.
 
-Default workload: the Q4_K x Q8_K GEMV at 17408 x 5120 (the FFN gate/up shape
-of the 27B model), quantised activations resident in HBM, weights rotated over
->= 1 GiB of distinct copies so every launch streams from HBM rather than the
-256 MB last-level cache.  A "step" is one GEMV launch over one weight copy.
+Default workload (`decode`): greedy decoding of the 27B-shaped Q4_K_M model
+(64 layers, hidden 5120, FFN 17408, vocab 248320, Q6_K LM head, one MTP
+block; random-init weights from the seeded synthetic GGUF writer) with MTP
+draft length 3 through the engine ABI (q38_model_speculative_greedy): a
+512-token random prompt is prefilled, then 256 tokens are decoded.  A "step"
+is one speculative transaction; `value` is decoded tokens per second.
+The `roofline` object is that of the dominant kernel of the step, the
+Q4_K x Q8_K GEMV at 17408 x 5120 (FFN gate/up), timed in the same run.
+
+GEMV workloads (`q4k_gemv` ...): the GEMV alone, quantised activations
+resident in HBM, weights rotated over >= 1 GiB of distinct copies so every
+launch streams from HBM rather than the 256 MB last-level cache; a "step" is
+one launch.
 
 Prints one JSON line (see the fields below).  `roofline.achieved` is the
-algorithmic bytes of one launch divided by its average duration measured
+algorithmic bytes of one GEMV launch divided by its average duration measured
 with HIP events on the stream the kernels run on.  `roofline.traffic` is the
 HBM bytes per launch read from the committed counter summary
 profiles/<kernel>.<workload>.pmc.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated
@@ -50,9 +59,12 @@ COPY_BYTES = 64 << 20
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--workload", default="q4k_gemv", choices=sorted(WORKLOADS) + ["copy"])
+    p.add_argument("--steps", type=int, default=None)
+    p.add_argument("--warmup", type=int, default=None)
+    p.add_argument("--workload", default="decode", choices=["decode"] + sorted(WORKLOADS) + ["copy"])
+    p.add_argument("--decode-tokens", type=int, default=256)
+    p.add_argument("--prompt", type=int, default=512)
+    p.add_argument("--draft", type=int, default=3)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     return p.parse_args()
@@ -128,29 +140,22 @@ def run_copy(torch, args):
     bufs = [torch.empty(n, dtype=torch.float32, device=dev).fill_(i) for i in range(32)]
     stream = torch.cuda.current_stream()
     launch = lambda i: bufs[(2 * i + 1) % 32].copy_(bufs[(2 * i) % 32])  # noqa: E731
-    for i in range(args.warmup):
+    steps = args.steps if args.steps is not None else 100
+    for i in range(args.warmup if args.warmup is not None else 10):
         launch(i)
-    per_ms, wall = timed(torch, stream, args.steps, launch)
+    per_ms, wall = timed(torch, stream, steps, launch)
     print(json.dumps({"metric": "device copy GB/s (counter calibration)", "value":
                       round(2 * COPY_BYTES / (per_ms * 1e-3) / 1e9, 2), "unit": "GB/s",
                       "bytes_read_per_launch": COPY_BYTES, "bytes_written_per_launch": COPY_BYTES,
-                      "steps": args.steps, "ms_per_step": round(wall * 1e3 / args.steps, 5)}))
+                      "steps": steps, "ms_per_step": round(wall * 1e3 / steps, 5)}))
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",
-              file=sys.stderr)
-        sys.exit(2)
-    import torch
-    if args.workload == "copy":
-        run_copy(torch, args)
-        return
+def gemv_roofline(torch, workload, steps, warmup):
+    """Time `steps` back-to-back launches of one GEMV workload on the current
+    stream (HIP events); returns (per-launch ms, wall s, roofline dict)."""
     import q38hip
     from q38hip import synth
-
-    qtype, rows, width, label = WORKLOADS[args.workload]
+    qtype, rows, width, _ = WORKLOADS[workload]
     dev = torch.device("cuda:0")
     nbytes = algorithmic_bytes(qtype, rows, width)
     wbytes = rows * (width // 256) * BLOCK[qtype]
@@ -165,31 +170,157 @@ def main():
     def launch(i):
         q38hip.gemm_q8_k(weights[i % copies], qtype, width, rows, xq, 1, out=out)
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         launch(i)
-    per_launch_ms, wall = timed(torch, stream, args.steps, launch)
+    per_launch_ms, wall = timed(torch, stream, steps, launch)
     achieved = nbytes / (per_launch_ms * 1e-3) / 1e9
-    traffic = committed_traffic(args.workload)
+    traffic = committed_traffic(workload)
+    roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None if traffic is None else int(traffic),
+                "kernel": "gemm_q8k (%s GEMV %dx%d, M=1)" % (TYPE_NAME[qtype], rows, width),
+                "bytes_per_launch": nbytes, "launch_us": round(per_launch_ms * 1e3, 3)}
+    del weights, base
+    return per_launch_ms, wall, roofline, copies
 
+
+def prompt_ids(count, seed=11):
+    return np.random.Generator(np.random.PCG64(seed)).integers(0, 248320, count).astype(np.uint32)
+
+
+def cpu_decode_baseline(path, draft, budget_s):
+    """The reference engine (oracle/_ref, its own C sources, AVX2 build) on the
+    host cores: a 4-token prompt, then speculative_greedy(draft) transactions
+    for about `budget_s` seconds; decoded tokens per second."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Reference, reference_model
+    if not Reference.available():
+        return None
+    model = reference_model().open(path, 1024)
+    model.enable_mtp()
+    logits = model.prefill(prompt_ids(4))
+    token = int(np.argmax(logits))
+    produced = 0
+    transactions = 0
+    start = time.perf_counter()
+    while time.perf_counter() - start < budget_s:
+        accepted, _ = model.speculative_greedy(token, 0xFFFFFFFF, draft)
+        produced += len(accepted)
+        token = int(accepted[-1])
+        transactions += 1
+    elapsed = time.perf_counter() - start
+    model.close()
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(produced / elapsed, 4), "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": "reference engine q38_model_speculative_greedy(k=%d) on the same synthetic 27B Q4_K_M "
+                      "GGUF: 4-token prompt, %d transactions, %d tokens in %.1f s, OpenMP threads=%d"
+                      % (draft, transactions, produced, elapsed, threads)}
+
+
+def run_decode(torch, args):
+    from q38hip import synth
+    from q38hip.model import Model
+    steps = args.steps if args.steps is not None else 248
+    warmup = args.warmup if args.warmup is not None else 8
+    path = synth.model_path(1, "q4km")
+    if path is None:
+        raise SystemExit("no directory with room for the 15.7 GB synthetic model (set Q38_MODEL_DIR)")
+    t0 = time.perf_counter()
+    synth.write_model_gguf(path, 1, "q4km")
+    t_synth = time.perf_counter() - t0
+    context = args.prompt + args.draft * (warmup + steps) + 16
+    t0 = time.perf_counter()
+    model = Model.open(path, context)
+    t_open = time.perf_counter() - t0
+    model.enable_mtp()
+    prompt = prompt_ids(args.prompt)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = model.prefill(prompt)
+    t_prefill = time.perf_counter() - t0
+    token = int(np.argmax(logits))
+    for _ in range(warmup):
+        accepted, _ = model.speculative_greedy(token, 0xFFFFFFFF, args.draft)
+        token = int(accepted[-1])
+    produced = 0
+    counts = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        accepted, _ = model.speculative_greedy(token, 0xFFFFFFFF, args.draft)
+        counts.append(len(accepted))
+        produced += len(accepted)
+        token = int(accepted[-1])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # plain greedy decode on the same model (no MTP) for reference
+    plain_n = 32
+    t1 = time.perf_counter()
+    for _ in range(plain_n):
+        token = int(np.argmax(model.forward_token(token)))
+    plain_wall = time.perf_counter() - t1
+    model.close()
+
+    _, _, roofline, copies = gemv_roofline(torch, "q4k_gemv", 200, 20)
+    result = {
+        "metric": "decode tokens/s (27B Q4_K_M + MTP k=%d, greedy)" % args.draft,
+        "value": round(produced / wall, 3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(wall * 1e3 / steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i8xQ4_K/Q6_K->i32, f32",
+        "data": "synthetic (seeded random-init 27B Q4_K_M GGUF, random prompt ids)",
+        "config": {"workload": "decode 27B Q4_K_M + MTP k=%d" % args.draft, "layers": 64, "hidden": 5120,
+                   "ffn": 17408, "vocab": 248320, "prompt_tokens": args.prompt, "context": context,
+                   "decoded_tokens": produced, "transactions": steps,
+                   "accepted_per_transaction": round(produced / steps, 4),
+                   "prefill_s": round(t_prefill, 3), "open_upload_s": round(t_open, 3),
+                   "synth_s": round(t_synth, 3),
+                   "plain_greedy_tokens_per_s": round(plain_n / plain_wall, 3)},
+        "roofline": roofline,
+        "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(path, args.draft, args.cpu_seconds),
+    }
+    print(json.dumps(result))
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if args.workload == "copy":
+        run_copy(torch, args)
+        return
+    if args.workload == "decode":
+        run_decode(torch, args)
+        return
+    qtype, rows, width, label = WORKLOADS[args.workload]
+    steps = args.steps if args.steps is not None else 200
+    warmup = args.warmup if args.warmup is not None else 20
+    per_launch_ms, wall, roofline, copies = gemv_roofline(torch, args.workload, steps, warmup)
     result = {
         "metric": "quant-GEMV HBM GB/s (%s x Q8_K decode GEMV)" % TYPE_NAME[qtype],
-        "value": round(achieved, 2),
+        "value": roofline["achieved"],
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(wall * 1e3 / steps, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "i8x%s->i32, f32" % TYPE_NAME[qtype],
         "data": "synthetic (seeded GGUF blocks, N(0,1) activations)",
         "config": {"workload": label, "weight_copies_rotated": copies,
-                   "rotated_bytes": copies * wbytes, "bytes_per_launch": nbytes,
-                   "launch_us": round(per_launch_ms * 1e3, 3)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": None if traffic is None else int(traffic)},
+                   "rotated_bytes": copies * rows * (width // 256) * BLOCK[qtype],
+                   "bytes_per_launch": algorithmic_bytes(qtype, rows, width)},
+        "roofline": roofline,
         "cpu_baseline": None if args.no_cpu else cpu_baseline(qtype, rows, width, args.cpu_seconds),
     }
     print(json.dumps(result))

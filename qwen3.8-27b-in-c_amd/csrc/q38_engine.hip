@@ -316,6 +316,7 @@ struct Q38Model {
     float *host_logits = nullptr;
     uint32_t *host_words = nullptr;
     float query_scale = 0.0f;
+    bool pending_branch = false;   /* m->branch holds an FFN output not yet added to m->hidden */
 };
 
 namespace {
@@ -521,9 +522,9 @@ bool allocate_state(Q38Model *m)
               dalloc(&m->hidden, (size_t)B * kHidden) && dalloc(&m->norm, (size_t)B * 2 * kHidden) &&
               dalloc(&m->branch, (size_t)B * kHidden) && dalloc(&m->wide0, (size_t)B * kFFN) &&
               dalloc(&m->wide1, (size_t)B * kFFN) && dalloc(&m->kbuf, (size_t)B * kKVDim) &&
-              dalloc(&m->vbuf, (size_t)B * kKVDim) && dalloc(&m->qbuf, kQDim) &&
+              dalloc(&m->vbuf, (size_t)B * kKVDim) && dalloc(&m->qbuf, (size_t)B * kQDim) &&
               dalloc(&m->attn, (size_t)B * kLinV) && dalloc(&m->beta, (size_t)B * kVHeads) &&
-              dalloc(&m->alpha, (size_t)B * kVHeads) && dalloc(&m->scores, (size_t)kAttnHeads * ctx) &&
+              dalloc(&m->alpha, (size_t)B * kVHeads) && dalloc(&m->scores, (size_t)B * kAttnHeads * ctx) &&
               dalloc(&m->logits, (size_t)B * kVocab) && dalloc(&m->target_norm, (size_t)B * kHidden) &&
               dalloc(&m->q8k, (size_t)B * (kFFN / 256) * kQ8KBytes) && dalloc(&m->tokens, B) &&
               dalloc(&m->positions, 4) && dalloc(&m->targets, B) && dalloc(&m->drafts, B) &&
@@ -604,20 +605,12 @@ void trace(Q38Model *m, const char *name, int layer, const float *device, uint64
 
 /* ---- step building blocks -------------------------------------------------- */
 
-bool gemm(Q38Model *m, const DevTensor &w, const float *in_rows, uint32_t count, float *out)
+/* GEMM over `count` Q8_K rows already in m->q8k (starting at block
+ * `first_block`) */
+bool gemm_q(Q38Model *m, const DevTensor &w, uint32_t count, float *out, size_t first_block = 0)
 {
-    const uint32_t nblk = (uint32_t)(w.width / 256);
-    q38::launch_quantize(in_rows, m->q8k, count * nblk, m->stream);
-    if (!q38::launch_gemm((int)w.type, (int)count, w.data, m->q8k, out, (uint32_t)w.rows, nblk, m->grid, m->stream))
-        return report("unsupported GEMM configuration");
-    return true;
-}
-
-/* GEMM over an input that is already quantised in m->q8k */
-bool gemm_q(Q38Model *m, const DevTensor &w, uint32_t count, float *out)
-{
-    if (!q38::launch_gemm((int)w.type, (int)count, w.data, m->q8k, out, (uint32_t)w.rows, (uint32_t)(w.width / 256),
-                          m->grid, m->stream))
+    if (!q38::launch_gemm((int)w.type, (int)count, w.data, m->q8k + first_block * kQ8KBytes, out, (uint32_t)w.rows,
+                          (uint32_t)(w.width / 256), m->grid, m->stream))
         return report("unsupported GEMM configuration");
     return true;
 }
@@ -630,22 +623,35 @@ bool set_positions(Q38Model *m, uint32_t base)
            hip_ok(hipStreamSynchronize(m->stream), "position upload");
 }
 
+/* apply a pending FFN residual add to m->hidden */
+void flush_branch(Q38Model *m, uint32_t count)
+{
+    if (m->pending_branch) q38::launch_add(m->hidden, m->branch, (long long)count * kHidden, m->stream);
+    m->pending_branch = false;
+}
+
+/* RMSNorm of the rows of m->hidden (after adding the pending FFN branch of
+ * the previous block, if any) into Q8_K rows of m->q8k */
+void norm_hidden(Q38Model *m, const DevTensor &weight, uint32_t count, float *norm_out = nullptr)
+{
+    q38::launch_norm_quant(norm_out, kHidden, m->q8k, kHidden / 256, m->hidden, kHidden,
+                           m->pending_branch ? m->branch : nullptr, weight.f32(), (int)count, m->stream);
+    m->pending_branch = false;
+}
+
 /* attention mixer of a full-attention layer over `count` rows at positions
- * base.., rows of m->norm in, rows of m->branch out
- * (q38_batch_full_attention, qwen38_model.c:1089-1119) */
+ * base.. (q38_batch_full_attention, qwen38_model.c:1089-1119); input Q8_K rows
+ * in m->q8k, output rows in m->branch */
 bool full_attention_rows(Q38Model *m, int layer, uint32_t count)
 {
     const Layer &L = m->layers[layer];
     const int full_index = layer / 4;
     const size_t kv_off = (size_t)full_index * m->context_length * kKVDim;
-    q38::launch_quantize(m->norm, m->q8k, count * (kHidden / 256), m->stream);
     if (!gemm_q(m, L.q, count, m->wide0) || !gemm_q(m, L.k, count, m->kbuf) || !gemm_q(m, L.v, count, m->vbuf))
         return false;
-    for (uint32_t t = 0; t < count; ++t)
-        q38::launch_attention(m->attn + (size_t)t * kQDim, m->qbuf, m->wide0 + (size_t)t * kQGDim,
-                              m->kbuf + (size_t)t * kKVDim, m->vbuf + (size_t)t * kKVDim, L.q_norm.f32(),
-                              L.k_norm.f32(), m->rope, m->key_cache + kv_off, m->value_cache + kv_off, m->scores,
-                              (int)m->context_length, m->positions, (int)t, m->stream);
+    q38::launch_attention(m->attn, m->q8k, m->qbuf, m->wide0, m->kbuf, m->vbuf, L.q_norm.f32(), L.k_norm.f32(),
+                          m->rope, m->key_cache + kv_off, m->value_cache + kv_off, m->scores, (int)m->context_length,
+                          m->positions, (int)count, m->stream);
     if (count == 1 && trace_enabled()) {
         uint32_t pos = 0;
         (void)hipMemcpy(&pos, m->positions, 4, hipMemcpyDeviceToHost);
@@ -654,7 +660,7 @@ bool full_attention_rows(Q38Model *m, int layer, uint32_t count)
         trace(m, "Vcur-", layer, m->vbuf, kKVDim);
         trace(m, "attn_gated-", layer, m->attn, kQDim);
     }
-    if (!gemm(m, L.out, m->attn, count, m->branch)) return false;
+    if (!gemm_q(m, L.out, count, m->branch)) return false;
     if (count == 1) trace(m, "attn_output-", layer, m->branch, kHidden);
     return true;
 }
@@ -664,13 +670,11 @@ bool linear_attention_rows(Q38Model *m, int layer, uint32_t count)
 {
     const Layer &L = m->layers[layer];
     const int r = layer - (layer + 1) / 4;
-    q38::launch_quantize(m->norm, m->q8k, count * (kHidden / 256), m->stream);
     if (!gemm_q(m, L.qkv, count, m->wide0) || !gemm_q(m, L.z, count, m->wide1) ||
         !gemm_q(m, L.beta, count, m->beta) || !gemm_q(m, L.alpha, count, m->alpha))
         return false;
     const bool tr = count == 1 && trace_enabled();
     if (tr) {
-        trace(m, "dn_norm-", layer, m->norm, kHidden);
         trace(m, "dn_qkv_proj-", layer, m->wide0, kQKV);
         trace(m, "dn_z-", layer, m->wide1, kLinV);
         trace(m, "dn_beta_proj-", layer, m->beta, kVHeads);
@@ -689,34 +693,34 @@ bool linear_attention_rows(Q38Model *m, int layer, uint32_t count)
         q38::launch_deltanet_state(attn, m->delta_state + (size_t)r * kVHeads * kHeadDim * kHeadDim, qkv, beta, alpha,
                                    m->query_scale, m->stream);
         if (tr) trace(m, "dn_core-", layer, attn, kLinV);
-        q38::launch_deltanet_out(attn, m->wide1 + (size_t)t * kLinV, L.ssm_norm.f32(), m->stream);
-        if (tr) trace(m, "dn_gated-", layer, attn, kLinV);
     }
-    return gemm(m, L.ssm_out, m->attn, count, m->branch);
-}
-
-/* FFN of a block over rows of m->norm into m->branch */
-bool ffn_rows(Q38Model *m, const Layer &L, uint32_t count)
-{
-    if (!gemm(m, L.ffn_gate, m->norm, count, m->wide0) || !gemm_q(m, L.ffn_up, count, m->wide1)) return false;
-    q38::launch_swiglu(m->wide0, m->wide1, (long long)count * kFFN, m->stream);
-    return gemm(m, L.ffn_down, m->wide0, count, m->branch);
+    q38::launch_deltanet_out_quant(m->attn, m->q8k, m->wide1, L.ssm_norm.f32(), (int)count, m->stream);
+    if (tr) trace(m, "dn_gated-", layer, m->attn, kLinV);
+    return gemm_q(m, L.ssm_out, count, m->branch);
 }
 
 /* one transformer block over `count` rows of m->hidden
- * (q38_layer_forward / q38_batch_layer, qwen38_model.c:955-984, 1121-1155) */
+ * (q38_layer_forward / q38_batch_layer, qwen38_model.c:955-984, 1121-1155).
+ * The FFN's residual add is left pending in m->branch and fused into the
+ * next RMSNorm. */
 bool layer_rows(Q38Model *m, int layer, uint32_t count)
 {
     const Layer &L = m->layers[layer];
-    q38::launch_rmsnorm(m->norm, m->hidden, L.attn_norm.f32(), kHidden, (int)count, kHidden, kHidden, m->stream);
+    norm_hidden(m, L.attn_norm, count);
     if (!(L.full ? full_attention_rows(m, layer, count) : linear_attention_rows(m, layer, count))) return false;
     if (count == 1) trace(m, "attention_branch-", layer, m->branch, kHidden);
-    q38::launch_add_rmsnorm(m->norm, m->hidden, m->branch, L.post_norm.f32(), kHidden, (int)count, m->stream);
+    m->pending_branch = true;
+    norm_hidden(m, L.post_norm, count);
     if (count == 1) trace(m, "attn_residual-", layer, m->hidden, kHidden);
-    if (!ffn_rows(m, L, count)) return false;
-    if (count == 1) trace(m, "ffn_out-", layer, m->branch, kHidden);
-    q38::launch_add(m->hidden, m->branch, (long long)count * kHidden, m->stream);
-    if (count == 1 && layer < (int)kLayers) trace(m, "l_out-", layer, m->hidden, kHidden);
+    if (!gemm_q(m, L.ffn_gate, count, m->wide0) || !gemm_q(m, L.ffn_up, count, m->wide1)) return false;
+    q38::launch_swiglu_quant(m->q8k, m->wide0, m->wide1, (int)count, m->stream);
+    if (!gemm_q(m, L.ffn_down, count, m->branch)) return false;
+    m->pending_branch = true;
+    if (count == 1 && trace_enabled()) {
+        trace(m, "ffn_out-", layer, m->branch, kHidden);
+        flush_branch(m, count);
+        if (layer < (int)kLayers) trace(m, "l_out-", layer, m->hidden, kHidden);
+    }
     return true;
 }
 
@@ -728,15 +732,13 @@ bool target_rows(Q38Model *m, uint32_t count, uint32_t base, uint32_t logit_rows
 {
     if (!set_positions(m, base)) return false;
     q38::launch_embed_q4k(m->hidden, m->embedding.data, m->tokens, (int)count, kHidden, kVocab, m->stream);
+    m->pending_branch = false;
     if (count == 1) trace(m, "model.input_embed", -1, m->hidden, kHidden);
     for (uint32_t layer = 0; layer < kLayers; ++layer)
         if (!layer_rows(m, (int)layer, count)) return false;
-    q38::launch_rmsnorm(m->target_norm, m->hidden, m->output_norm.f32(), kHidden, (int)count, kHidden, kHidden,
-                        m->stream);
-    if (logit_rows) {
-        const float *rows = m->target_norm + (size_t)(count - logit_rows) * kHidden;
-        if (!gemm(m, m->output, rows, logit_rows, m->logits)) return false;
-    }
+    norm_hidden(m, m->output_norm, count, m->target_norm);
+    if (logit_rows && !gemm_q(m, m->output, logit_rows, m->logits, (size_t)(count - logit_rows) * (kHidden / 256)))
+        return false;
     return true;
 }
 
@@ -768,23 +770,25 @@ bool logits_to_host(Q38Model *m, const float *device_row)
 bool mtp_catchup(Q38Model *m, uint32_t count, uint32_t base)
 {
     const Layer &L = m->layers[kLayers];
+    constexpr int kHB = kHidden / 256;   /* Q8_K blocks per hidden row */
     if (!set_positions(m, base)) return false;
     q38::launch_embed_q4k(m->hidden, m->mtp_embedding.data, m->tokens, (int)count, kHidden, kVocab, m->stream);
-    /* m->norm holds count rows of 2*kHidden: [enorm(e_t) | hnorm(prev_t)] */
-    q38::launch_rmsnorm(m->norm, m->hidden, m->enorm.f32(), kHidden, (int)count, 2 * kHidden, kHidden, m->stream);
-    q38::launch_rmsnorm(m->norm + kHidden, m->mtp_hidden, m->hnorm.f32(), kHidden, 1, 2 * kHidden, kHidden,
-                        m->stream);
+    /* Q8_K rows of 2*kHidden: [enorm(e_t) | hnorm(prev_t)], prev_0 = MTP hidden,
+     * prev_t = target_norm[t-1] */
+    q38::launch_norm_quant(nullptr, 0, m->q8k, 2 * kHB, m->hidden, kHidden, nullptr, m->enorm.f32(), (int)count,
+                           m->stream);
+    q38::launch_norm_quant(nullptr, 0, m->q8k + kHB * kQ8KBytes, 2 * kHB, m->mtp_hidden, kHidden, nullptr,
+                           m->hnorm.f32(), 1, m->stream);
     if (count > 1)
-        q38::launch_rmsnorm(m->norm + 3 * kHidden, m->target_norm, m->hnorm.f32(), kHidden, (int)count - 1,
-                            2 * kHidden, kHidden, m->stream);
-    if (!gemm(m, m->eh_proj, m->norm, count, m->hidden)) return false;
-    q38::launch_rmsnorm(m->norm, m->hidden, L.attn_norm.f32(), kHidden, (int)count, kHidden, kHidden, m->stream);
-    q38::launch_quantize(m->norm, m->q8k, count * (kHidden / 256), m->stream);
+        q38::launch_norm_quant(nullptr, 0, m->q8k + 3 * kHB * kQ8KBytes, 2 * kHB, m->target_norm, kHidden, nullptr,
+                               m->hnorm.f32(), (int)count - 1, m->stream);
+    if (!gemm_q(m, m->eh_proj, count, m->hidden)) return false;
+    m->pending_branch = false;
+    norm_hidden(m, L.attn_norm, count);
     if (!gemm_q(m, L.k, count, m->kbuf) || !gemm_q(m, L.v, count, m->vbuf)) return false;
     const size_t kv_off = (size_t)(kLayers / 4) * m->context_length * kKVDim;
-    for (uint32_t t = 0; t < count; ++t)
-        q38::launch_kv_write(m->kbuf + (size_t)t * kKVDim, m->vbuf + (size_t)t * kKVDim, L.k_norm.f32(), m->rope,
-                             m->key_cache + kv_off, m->value_cache + kv_off, m->positions, (int)t, m->stream);
+    q38::launch_kv_write(m->kbuf, m->vbuf, L.k_norm.f32(), m->rope, m->key_cache + kv_off, m->value_cache + kv_off,
+                         m->positions, (int)count, m->stream);
     if (!hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm + (size_t)(count - 1) * kHidden,
                                kHidden * sizeof(float), hipMemcpyDeviceToDevice, m->stream),
                 "mtp hidden"))
@@ -797,14 +801,20 @@ bool mtp_catchup(Q38Model *m, uint32_t count, uint32_t base)
  * qwen38_model.c:1588-1612; the block is q38_mtp_layer_forward :932-953) */
 bool mtp_step(Q38Model *m)
 {
+    constexpr int kHB = kHidden / 256;
     if (!set_positions(m, m->mtp_position)) return false;
     q38::launch_embed_q4k(m->hidden, m->mtp_embedding.data, m->tokens, 1, kHidden, kVocab, m->stream);
-    q38::launch_rmsnorm(m->norm, m->hidden, m->enorm.f32(), kHidden, 1, kHidden, kHidden, m->stream);
-    q38::launch_rmsnorm(m->norm + kHidden, m->mtp_hidden, m->hnorm.f32(), kHidden, 1, kHidden, kHidden, m->stream);
-    if (!gemm(m, m->eh_proj, m->norm, 1, m->hidden)) return false;
+    q38::launch_norm_quant(nullptr, 0, m->q8k, 2 * kHB, m->hidden, kHidden, nullptr, m->enorm.f32(), 1, m->stream);
+    q38::launch_norm_quant(nullptr, 0, m->q8k + kHB * kQ8KBytes, 2 * kHB, m->mtp_hidden, kHidden, nullptr,
+                           m->hnorm.f32(), 1, m->stream);
+    if (!gemm_q(m, m->eh_proj, 1, m->hidden)) return false;
+    m->pending_branch = false;
     if (!layer_rows(m, (int)kLayers, 1)) return false;
-    q38::launch_rmsnorm(m->mtp_hidden, m->hidden, m->shared_head_norm.f32(), kHidden, 1, kHidden, kHidden, m->stream);
-    if (!gemm(m, m->mtp_output, m->mtp_hidden, 1, m->logits)) return false;
+    /* mtp hidden = shared_head_norm(hidden + branch), and its Q8_K rows */
+    q38::launch_norm_quant(m->mtp_hidden, kHidden, m->q8k, kHB, m->hidden, kHidden,
+                           m->pending_branch ? m->branch : nullptr, m->shared_head_norm.f32(), 1, m->stream);
+    m->pending_branch = false;
+    if (!gemm_q(m, m->mtp_output, 1, m->logits)) return false;
     ++m->mtp_position;
     return true;
 }
@@ -863,6 +873,7 @@ Q38Model *q38_model_open_gguf(const char *path, uint32_t context_length)
     if (ok && m->gguf.get_u32("qwen35.block_count", &blocks) && blocks == kTotalLayers)
         ok = bind_mtp(m, m->gguf, base);
     ok = ok && allocate_state(m) && clear_state(m);
+    if (ok && !q38::configure_attention((int)context_length)) ok = report("attention kernel configuration failed");
     if (!ok) {
         release(m);
         return nullptr;
@@ -919,8 +930,10 @@ int q38_model_forward_token_layers(Q38Model *m, uint32_t token, uint32_t layer_c
     if (!upload_tokens(m, &token, 1) || !set_positions(m, m->position)) return 0;
     q38::launch_embed_q4k(m->hidden, m->embedding.data, m->tokens, 1, kHidden, kVocab, m->stream);
     trace(m, "model.input_embed", -1, m->hidden, kHidden);
+    m->pending_branch = false;
     for (uint32_t layer = 0; layer < layer_count; ++layer)
         if (!layer_rows(m, (int)layer, 1)) return 0;
+    flush_branch(m, 1);
     if (!hip_ok(hipMemcpyAsync(hidden_out, m->hidden, kHidden * sizeof(float), hipMemcpyDeviceToHost, m->stream),
                 "hidden download") ||
         !hip_ok(hipStreamSynchronize(m->stream), "hidden download"))

@@ -19,28 +19,30 @@ void launch_argmax(const float *values, uint32_t count, uint32_t rows, float *pv
 void launch_accept(uint32_t *result, const uint32_t *targets, const uint32_t *drafts, uint32_t rows,
                    hipStream_t stream);
 
-/* q38_model.hip */
-void launch_rmsnorm(float *out, const float *in, const float *weight, int n, int rows, long long out_stride,
-                    long long in_stride, hipStream_t stream);
-void launch_add_rmsnorm(float *norm, float *hidden, const float *branch, const float *weight, int n, int rows,
-                        hipStream_t stream);
+/* q38_model.hip.  Rows of a batch are contiguous; q_out receives Q8_K blocks. */
+void launch_norm_quant(float *norm_out, long long norm_stride, uint8_t *q_out, int q_stride_blocks, float *hidden,
+                       long long in_stride, const float *branch, const float *weight, int rows, hipStream_t stream);
 void launch_add(float *hidden, const float *branch, long long n, hipStream_t stream);
-void launch_swiglu(float *gate, const float *up, long long n, hipStream_t stream);
+void launch_swiglu_quant(uint8_t *q_out, const float *gate, const float *up, int rows, hipStream_t stream);
 void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int count, int width, uint32_t vocab,
                       hipStream_t stream);
 /* gated DeltaNet core of one row: conv + SiLU + q/k L2 norm + beta/alpha,
- * the state update, then the per-head norm and z gate */
+ * then the state update; the per-head norm, z gate and Q8_K run over all rows */
 void launch_deltanet_prep(float *qkv, float *beta, float *alpha, float *conv_state, const float *conv_w,
                           const float *ssm_a, const float *ssm_dt, hipStream_t stream);
 void launch_deltanet_state(float *attn, float *delta_state, const float *qkv, const float *beta, const float *alpha,
                            float query_scale, hipStream_t stream);
-void launch_deltanet_out(float *attn, const float *z, const float *ssm_norm, hipStream_t stream);
-void launch_attention(float *attn, float *q_buf, const float *q_and_gate, const float *key, const float *value,
-                      const float *q_norm, const float *k_norm, const float *rope, float *key_cache,
-                      float *value_cache, float *scores, int context, const uint32_t *position, int row_offset,
-                      hipStream_t stream);
-/* K-norm, RoPE and K/V cache write of one row without the query side */
+void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, const float *ssm_norm, int rows,
+                               hipStream_t stream);
+/* full attention over `rows` rows at positions *position + t: prep (norms,
+ * RoPE, K/V write), scores, softmax + V + gate + Q8_K of the output */
+bool configure_attention(int context);
+void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_and_gate, const float *key,
+                      const float *value, const float *q_norm, const float *k_norm, const float *rope,
+                      float *key_cache, float *value_cache, float *scores, int context, const uint32_t *position,
+                      int rows, hipStream_t stream);
+/* K-norm, RoPE and K/V cache write of `rows` rows without the query side */
 void launch_kv_write(const float *key, const float *value, const float *k_norm, const float *rope, float *key_cache,
-                     float *value_cache, const uint32_t *position, int row_offset, hipStream_t stream);
+                     float *value_cache, const uint32_t *position, int rows, hipStream_t stream);
 
 }  // namespace q38

@@ -1,14 +1,13 @@
 /* Q8_K activation quantiser, row argmax and greedy acceptance on gfx950. */
 #include "q38_device.h"
+#include "q38_q8k.h"
 
 namespace q38 {
 
-/* One wavefront per 256-element block, four elements per lane.
- * Restates q38_quantize_q8_k (src/qwen38/qwen38_quant.c:50-88): the block
- * maximum is the signed value of the FIRST element holding the largest |x|
- * (NaN never wins), inverse = -127/max (IEEE division), quants are
- * round-half-even via the 1.5*2^23 shift and clamped above at 127, sums are
- * per 16 elements, scale = 1/inverse.  An all-zero block stores zeros. */
+/* One wavefront per 256-element block, four elements per lane
+ * (wave_quantize_q8k restates q38_quantize_q8_k).  ALIGNED: x is 16-byte
+ * aligned, so each lane reads its four floats with one vector load. */
+template <bool ALIGNED>
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restrict__ x,
                                                            uint8_t *__restrict__ out,
                                                            uint32_t nblocks)
@@ -16,45 +15,15 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restri
     const int lane = threadIdx.x & 63;
     const uint32_t b = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (b >= nblocks) return;
-    const float *src = x + static_cast<size_t>(b) * kQK + 4 * lane;
-    const float v[4] = {src[0], src[1], src[2], src[3]};
-
-    float amax = 0.0f;
-    int idx = 0x7fffffff;
-    for (int i = 0; i < 4; ++i) {
-        const float a = fabsf(v[i]);
-        if (a > amax) { amax = a; idx = 4 * lane + i; }
+    const float *src = x + static_cast<size_t>(b) * kQK;
+    float v[4];
+    if (ALIGNED) {
+        const float4 v4 = reinterpret_cast<const float4 *>(src)[lane];
+        v[0] = v4.x; v[1] = v4.y; v[2] = v4.z; v[3] = v4.w;
+    } else {
+        for (int i = 0; i < 4; ++i) v[i] = src[4 * lane + i];
     }
-    for (int off = 32; off > 0; off >>= 1) {
-        const float oa = __shfl_xor(amax, off, 64);
-        const int oi = __shfl_xor(idx, off, 64);
-        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; idx = oi; }
-    }
-    uint8_t *blk = out + static_cast<size_t>(b) * kQ8KBytes;
-    if (amax == 0.0f) {
-        reinterpret_cast<uint32_t *>(blk + 4)[lane] = 0u;
-        if (lane < 16) reinterpret_cast<int16_t *>(blk + 260)[lane] = 0;
-        if (lane == 0) *reinterpret_cast<float *>(blk) = 0.0f;
-        return;
-    }
-    const int k = idx & 3;
-    const float mine = k == 0 ? v[0] : k == 1 ? v[1] : k == 2 ? v[2] : v[3];
-    const float maximum = __shfl(mine, idx >> 2, 64);
-    const float inv = div_rn(-127.0f, maximum);
-
-    uint32_t packed = 0;
-    int sum = 0;
-    for (int i = 0; i < 4; ++i) {
-        const float shifted = __fadd_rn(__fmul_rn(inv, v[i]), 12582912.0f);
-        int q = (int)(__float_as_uint(shifted) & 0x007fffffu) - 0x00400000;
-        if (q > 127) q = 127;
-        sum += q;
-        packed |= (static_cast<uint32_t>(q) & 0xffu) << (8 * i);
-    }
-    reinterpret_cast<uint32_t *>(blk + 4)[lane] = packed;
-    sum = quad_sum(sum);
-    if ((lane & 3) == 0) reinterpret_cast<int16_t *>(blk + 260)[lane >> 2] = static_cast<int16_t>(sum);
-    if (lane == 0) *reinterpret_cast<float *>(blk) = div_rn(1.0f, inv);
+    wave_quantize_q8k(v, out + static_cast<size_t>(b) * kQ8KBytes, lane);
 }
 
 /* First-maximum selection: NaN never wins, ties go to the lower index.  With
@@ -156,7 +125,10 @@ __global__ void accept_kernel(uint32_t *__restrict__ result, const uint32_t *__r
 
 void launch_quantize(const float *x, uint8_t *out, uint32_t nblocks, hipStream_t stream)
 {
-    hipLaunchKernelGGL(quantize_q8k_kernel, dim3((nblocks + 3) / 4), dim3(256), 0, stream, x, out, nblocks);
+    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0)
+        hipLaunchKernelGGL(quantize_q8k_kernel<true>, dim3((nblocks + 3) / 4), dim3(256), 0, stream, x, out, nblocks);
+    else
+        hipLaunchKernelGGL(quantize_q8k_kernel<false>, dim3((nblocks + 3) / 4), dim3(256), 0, stream, x, out, nblocks);
 }
 
 uint32_t argmax_chunks(uint32_t count) { return (count + kArgmaxChunk - 1) / kArgmaxChunk; }

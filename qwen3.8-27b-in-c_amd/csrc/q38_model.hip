@@ -13,6 +13,7 @@
 #include "q38_kernels.h"
 #include "q38_libm.h"
 #include "q38_math.h"
+#include "q38_q8k.h"
 
 namespace q38 {
 
@@ -29,16 +30,11 @@ namespace q38 {
  * and always for NaN) one thread redoes the sequential loop.  `post` is the
  * float-rounding step. */
 template <int THREADS, typename Post>
-__device__ float block_sum_squares(const float *x, int n, Post post)
+__device__ float block_sum_finish(double s, const float *x, int n, Post post)
 {
     static_assert(THREADS % 64 == 0 && THREADS <= 1024, "block size");
     __shared__ double partial[THREADS / 64];
     __shared__ float result;
-    double s = 0.0;
-    for (int i = threadIdx.x; i < n; i += THREADS) {
-        const float v = x[i];
-        s += (double)__fmul_rn(v, v);
-    }
     for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
     if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = s;
     __syncthreads();
@@ -61,6 +57,18 @@ __device__ float block_sum_squares(const float *x, int n, Post post)
     return r;
 }
 
+/* block_sum_finish over a vector the block reads itself */
+template <int THREADS, typename Post>
+__device__ float block_sum_squares(const float *x, int n, Post post)
+{
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += THREADS) {
+        const float v = x[i];
+        s += (double)__fmul_rn(v, v);
+    }
+    return block_sum_finish<THREADS>(s, x, n, post);
+}
+
 struct MeanPost {
     double n;
     __device__ float operator()(double s) const { return (float)(s / n); }
@@ -69,35 +77,61 @@ struct FloatPost {
     __device__ float operator()(double s) const { return (float)s; }
 };
 
-/* ---- RMSNorm ------------------------------------------------------------- */
+/* ---- RMSNorm + Q8_K ------------------------------------------------------ */
 
-/* out[r] = rmsnorm(in[r]) * weight for `rows` rows of n floats
- * (q38_rmsnorm, qwen38_model.c:426-435): y = (x * scale) * w. */
-__global__ __launch_bounds__(256) void rmsnorm_kernel(float *__restrict__ out, const float *__restrict__ in,
-                                                      const float *__restrict__ weight, int n,
-                                                      long long out_stride, long long in_stride)
+/* One block of 256 threads per row of N = 1024*NV floats.  ADD: the row of
+ * `hidden` first becomes hidden + branch (the residual add of
+ * qwen38_model.c:975/983, written back).  Then y = (x * scale) * w with
+ * scale = 1/sqrtf(mean + 1e-6) (q38_rmsnorm, :426-435), written to
+ * norm_out (when not null) and quantised to Q8_K into q_out (when not null):
+ * float4 f = tid + 256*j holds elements 4f..4f+3, i.e. lane `tid % 64` of
+ * Q8_K block 4*j + tid/64, so each wavefront quantises whole blocks. */
+template <int NV, bool ADD>
+__global__ __launch_bounds__(256) void norm_quant_kernel(float *__restrict__ norm_out, long long norm_stride,
+                                                         uint8_t *__restrict__ q_out, int q_stride_blocks,
+                                                         float *__restrict__ hidden, long long in_stride,
+                                                         const float *__restrict__ branch,
+                                                         const float *__restrict__ weight)
 {
-    const float *x = in + (long long)blockIdx.x * in_stride;
-    float *y = out + (long long)blockIdx.x * out_stride;
-    const float mean = block_sum_squares<256>(x, n, MeanPost{(double)n});
+    constexpr int N = 1024 * NV;
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float *h = hidden + (long long)row * in_stride;
+    float4 x[NV];
+    for (int j = 0; j < NV; ++j) x[j] = reinterpret_cast<const float4 *>(h)[tid + 256 * j];
+    if (ADD) {
+        const float4 *b = reinterpret_cast<const float4 *>(branch + (long long)row * in_stride);
+        for (int j = 0; j < NV; ++j) {
+            const float4 bj = b[tid + 256 * j];
+            x[j].x = __fadd_rn(x[j].x, bj.x);
+            x[j].y = __fadd_rn(x[j].y, bj.y);
+            x[j].z = __fadd_rn(x[j].z, bj.z);
+            x[j].w = __fadd_rn(x[j].w, bj.w);
+            reinterpret_cast<float4 *>(h)[tid + 256 * j] = x[j];
+        }
+    }
+    double s = 0.0;
+    for (int j = 0; j < NV; ++j) {
+        s += (double)__fmul_rn(x[j].x, x[j].x);
+        s += (double)__fmul_rn(x[j].y, x[j].y);
+        s += (double)__fmul_rn(x[j].z, x[j].z);
+        s += (double)__fmul_rn(x[j].w, x[j].w);
+    }
+    const float mean = block_sum_finish<256>(s, h, N, MeanPost{(double)N});
     const float scale = rms_scale(mean);
-    for (int i = threadIdx.x; i < n; i += 256) y[i] = __fmul_rn(__fmul_rn(x[i], scale), weight[i]);
-}
-
-/* hidden += branch, then norm = rmsnorm(hidden) * weight (the residual add of
- * qwen38_model.c:975/983 followed by the next block's norm). */
-__global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *__restrict__ norm, float *__restrict__ hidden,
-                                                          const float *__restrict__ branch,
-                                                          const float *__restrict__ weight, int n)
-{
-    float *h = hidden + (long long)blockIdx.x * n;
-    const float *b = branch + (long long)blockIdx.x * n;
-    for (int i = threadIdx.x; i < n; i += 256) h[i] = __fadd_rn(h[i], b[i]);
-    __syncthreads();
-    const float mean = block_sum_squares<256>(h, n, MeanPost{(double)n});
-    const float scale = rms_scale(mean);
-    float *y = norm + (long long)blockIdx.x * n;
-    for (int i = threadIdx.x; i < n; i += 256) y[i] = __fmul_rn(__fmul_rn(h[i], scale), weight[i]);
+    const float4 *w4 = reinterpret_cast<const float4 *>(weight);
+    for (int j = 0; j < NV; ++j) {
+        const float4 w = w4[tid + 256 * j];
+        float v[4];
+        v[0] = __fmul_rn(__fmul_rn(x[j].x, scale), w.x);
+        v[1] = __fmul_rn(__fmul_rn(x[j].y, scale), w.y);
+        v[2] = __fmul_rn(__fmul_rn(x[j].z, scale), w.z);
+        v[3] = __fmul_rn(__fmul_rn(x[j].w, scale), w.w);
+        if (norm_out)
+            reinterpret_cast<float4 *>(norm_out + (long long)row * norm_stride)[tid + 256 * j] =
+                make_float4(v[0], v[1], v[2], v[3]);
+        if (q_out)
+            wave_quantize_q8k(v, q_out + ((size_t)row * q_stride_blocks + 4 * j + wave) * kQ8KBytes, lane);
+    }
 }
 
 __global__ __launch_bounds__(256) void add_kernel(float *__restrict__ hidden, const float *__restrict__ branch,
@@ -107,12 +141,20 @@ __global__ __launch_bounds__(256) void add_kernel(float *__restrict__ hidden, co
     if (i < n) hidden[i] = __fadd_rn(hidden[i], branch[i]);
 }
 
-/* gate[i] = silu(gate[i]) * up[i] (q38_swiglu scalar path, qwen38_model.c:532-549) */
-__global__ __launch_bounds__(256) void swiglu_kernel(float *__restrict__ gate, const float *__restrict__ up,
-                                                     long long n)
+/* SwiGLU then Q8_K: y = silu(gate) * up (q38_swiglu scalar path,
+ * qwen38_model.c:532-549), one wavefront per 256-element block of the
+ * row-contiguous [rows][17408] vectors. */
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(uint8_t *__restrict__ q_out, const float *__restrict__ gate,
+                                                           const float *__restrict__ up, int nblocks)
 {
-    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) gate[i] = __fmul_rn(siluf_exact(gate[i]), up[i]);
+    const int lane = threadIdx.x & 63;
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nblocks) return;
+    const float4 g = reinterpret_cast<const float4 *>(gate)[b * 64 + lane];
+    const float4 u = reinterpret_cast<const float4 *>(up)[b * 64 + lane];
+    const float v[4] = {__fmul_rn(siluf_exact(g.x), u.x), __fmul_rn(siluf_exact(g.y), u.y),
+                        __fmul_rn(siluf_exact(g.z), u.z), __fmul_rn(siluf_exact(g.w), u.w)};
+    wave_quantize_q8k(v, q_out + (size_t)b * kQ8KBytes, lane);
 }
 
 /* ---- embedding rows ------------------------------------------------------ */
@@ -153,7 +195,7 @@ __global__ __launch_bounds__(256) void embed_q4k_kernel(float *__restrict__ out,
 
 /* ---- gated DeltaNet ------------------------------------------------------ */
 
-constexpr int kQKV = 10240, kQKDim = 2048, kVHeads = 48, kHeadDim = 128;
+constexpr int kQKV = 10240, kQKDim = 2048, kVHeads = 48, kHeadDim = 128, kLinV = 6144, kFFNWidth = 17408;
 
 /* Causal conv (4 taps, state of 3 per channel), SiLU, per-head L2 norm of q
  * and k, and the beta / alpha transforms (q38_linear_core,
@@ -254,54 +296,91 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
     if (l == 0) out[h * kHeadDim + c] = __fmul_rn(result, query_scale);
 }
 
-/* Per value head: RMSNorm over 128 (ssm_norm weight), then
- * out *= silu(z) (qwen38_model.c:785-791). */
-__global__ __launch_bounds__(128) void deltanet_out_kernel(float *__restrict__ attn, const float *__restrict__ z,
-                                                           const float *__restrict__ norm_w)
+/* Per value head: RMSNorm over 128 (ssm_norm weight), then out *= silu(z)
+ * (qwen38_model.c:785-791), then Q8_K of the 6144-wide result for the
+ * ssm_out projection.  One block of 256 threads per pair of heads (one Q8_K
+ * block) and row. */
+__global__ __launch_bounds__(256) void deltanet_out_quant_kernel(float *__restrict__ attn, uint8_t *__restrict__ q_out,
+                                                                 const float *__restrict__ z,
+                                                                 const float *__restrict__ norm_w)
 {
-    float *x = attn + blockIdx.x * kHeadDim;
-    const float mean = block_sum_squares<128>(x, kHeadDim, MeanPost{128.0});
-    const float scale = rms_scale(mean);
-    const int i = threadIdx.x;
-    const float y = __fmul_rn(__fmul_rn(x[i], scale), norm_w[i]);
-    x[i] = __fmul_rn(y, siluf_exact(z[blockIdx.x * kHeadDim + i]));
+    __shared__ double partial[4];
+    __shared__ float mean_s[2];
+    __shared__ float ybuf[256];
+    const int t = blockIdx.y, pair = blockIdx.x, tid = threadIdx.x;
+    const int half = tid >> 7, i = tid & 127;
+    const int head = 2 * pair + half;
+    float *x = attn + (size_t)t * kLinV + head * kHeadDim;
+    const float v = x[i];
+    double s = (double)__fmul_rn(v, v);
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if ((tid & 63) == 0) partial[tid >> 6] = s;
+    __syncthreads();
+    if (i == 0) {
+        const double total = partial[2 * half] + partial[2 * half + 1];
+        const MeanPost post{128.0};
+        const float lo = post(total * (1.0 - 0x1p-36)), hi = post(total * (1.0 + 0x1p-36));
+        if (lo == hi) {
+            mean_s[half] = lo;
+        } else {
+            double seq = 0.0;
+            for (int k = 0; k < kHeadDim; ++k) seq += (double)__fmul_rn(x[k], x[k]);
+            mean_s[half] = post(seq);
+        }
+    }
+    __syncthreads();
+    const float scale = rms_scale(mean_s[half]);
+    const float y = __fmul_rn(__fmul_rn(__fmul_rn(v, scale), norm_w[i]),
+                              siluf_exact(z[(size_t)t * kLinV + head * kHeadDim + i]));
+    x[i] = y;
+    ybuf[tid] = y;
+    __syncthreads();
+    if (tid < 64) {
+        const float q4[4] = {ybuf[4 * tid], ybuf[4 * tid + 1], ybuf[4 * tid + 2], ybuf[4 * tid + 3]};
+        wave_quantize_q8k(q4, q_out + ((size_t)t * (kLinV / 256) + pair) * kQ8KBytes, tid);
+    }
 }
 
 /* ---- full attention ------------------------------------------------------ */
 
-constexpr int kAttnHeads = 24, kKVHeads = 4, kAttnDim = 256, kKVDim = 1024;
+constexpr int kAttnHeads = 24, kKVHeads = 4, kAttnDim = 256, kKVDim = 1024, kQGDim = 12288, kQDim = 6144;
+constexpr int kScoreChunk = 64;
+constexpr int kMaxLdsPositions = 32768;   /* softmax weights kept in LDS up to this many positions */
 
 /* q / gate split, per-head RMSNorm of q and k (q_norm / k_norm weights),
  * RoPE on dims 0..63 (pairs i, i+32) and the K/V cache write
- * (q38_full_core, qwen38_model.c:816-846; q38_rope :697-713).  Blocks 0..23
- * are q heads, 24..27 k heads, 28 copies v.  `rope` holds cos (32) then
- * sin (32) per position, computed once on the host with the C library.
- * `block_base` = 24 runs only the K/V part. */
+ * (q38_full_core, qwen38_model.c:816-846; q38_rope :697-713) for row t
+ * (blockIdx.y) at position *position_ptr + t.  Blocks 0..23 are q heads,
+ * 24..27 k heads, 28 copies v.  `rope` holds cos (32) then sin (32) per
+ * position, computed once on the host with the C library.  `block_base` =
+ * 24 runs only the K/V part. */
 __global__ __launch_bounds__(256) void attn_prep_kernel(float *__restrict__ q_out, const float *__restrict__ q_and_gate,
                                                         const float *__restrict__ key, const float *__restrict__ value,
                                                         const float *__restrict__ q_norm,
                                                         const float *__restrict__ k_norm,
                                                         const float *__restrict__ rope, float *__restrict__ key_cache,
                                                         float *__restrict__ value_cache,
-                                                        const uint32_t *__restrict__ position_ptr, int row_offset,
-                                                        int block_base)
+                                                        const uint32_t *__restrict__ position_ptr, int block_base)
 {
-    const uint32_t pos = *position_ptr + row_offset;
+    const int t = blockIdx.y;
+    const uint32_t pos = *position_ptr + t;
     const int i = threadIdx.x;
     const int block = blockIdx.x + block_base;
     float *kc = key_cache + (size_t)pos * kKVDim;
     if (block == kAttnHeads + kKVHeads) {
-        for (int e = i; e < kKVDim; e += 256) value_cache[(size_t)pos * kKVDim + e] = value[e];
+        for (int e = i; e < kKVDim; e += 256) value_cache[(size_t)pos * kKVDim + e] = value[(size_t)t * kKVDim + e];
         return;
     }
     const bool is_q = block < kAttnHeads;
     const int h = is_q ? block : block - kAttnHeads;
-    const float *src = is_q ? q_and_gate + h * 2 * kAttnDim : key + h * kAttnDim;
+    const float *src = is_q ? q_and_gate + (size_t)t * kQGDim + h * 2 * kAttnDim
+                            : key + (size_t)t * kKVDim + h * kAttnDim;
     const float *w = is_q ? q_norm : k_norm;
-    const float mean = block_sum_squares<256>(src, kAttnDim, MeanPost{256.0});
+    const float x = src[i];
+    const float mean = block_sum_finish<256>((double)__fmul_rn(x, x), src, kAttnDim, MeanPost{256.0});
     const float scale = rms_scale(mean);
     __shared__ float v[kAttnDim];
-    v[i] = __fmul_rn(__fmul_rn(src[i], scale), w[i]);
+    v[i] = __fmul_rn(__fmul_rn(x, scale), w[i]);
     __syncthreads();
     float y = v[i];
     if (i < 64) {
@@ -312,48 +391,73 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float *__restrict__ q_ou
         y = i < 32 ? __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s))
                    : __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
     }
-    if (is_q) q_out[h * kAttnDim + i] = y;
+    if (is_q) q_out[(size_t)t * kQDim + h * kAttnDim + i] = y;
     else kc[h * kAttnDim + i] = y;
 }
 
-/* Decode attention of one q head over positions 0..pos of its KV head
- * (GQA 6:1), qwen38_model.c:848-882: score_p = fmaf-chain over the 256 dims
- * (i ascending) times 1/16; maximum; e_p = expf(score_p - max); denominator
- * summed in position order; out_i = fmaf-chain over positions of
- * (e_p / denominator) * v_p[i]; out_i *= sigmoid(gate_i).
- * One block of 256 threads per head; `scores` is [24][context] scratch. */
-__global__ __launch_bounds__(256) void attn_decode_kernel(float *__restrict__ out, const float *__restrict__ q,
-                                                          const float *__restrict__ q_and_gate,
-                                                          const float *__restrict__ key_cache,
-                                                          const float *__restrict__ value_cache,
-                                                          float *__restrict__ scores, int context,
-                                                          const uint32_t *__restrict__ position_ptr, int row_offset)
+/* Attention scores of row t (blockIdx.z) for the six q heads sharing KV head
+ * blockIdx.x, positions blockIdx.y*64 .. +63 (one per lane):
+ * score = fmaf-chain over the 256 dims in order, times 1/16
+ * (qwen38_model.c:854-862).  Each lane reads its K row once for six
+ * independent chains.  scores is [rows][24][context]. */
+__global__ __launch_bounds__(64) void attn_scores_kernel(float *__restrict__ scores, const float *__restrict__ q,
+                                                         const float *__restrict__ key_cache, int context,
+                                                         const uint32_t *__restrict__ position_ptr)
 {
-    const int h = blockIdx.x;
-    const int kvh = h / (kAttnHeads / kKVHeads);
-    const int tid = threadIdx.x;
-    const int n = (int)(*position_ptr + row_offset) + 1;
-    float *sc = scores + (size_t)h * context;
-    __shared__ float qs[kAttnDim];
-    __shared__ float red[4];
-    __shared__ float denom_s;
-    qs[tid] = q[h * kAttnDim + tid];
+    const int kvh = blockIdx.x, chunk = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
+    const int n = (int)*position_ptr + t + 1;
+    if (chunk * kScoreChunk >= n) return;
+    __shared__ float qs[6][kAttnDim];
+    const float *qsrc = q + (size_t)t * kQDim + kvh * 6 * kAttnDim;
+    for (int e = lane; e < 6 * kAttnDim; e += 64) qs[e >> 8][e & 255] = qsrc[e];
     __syncthreads();
+    const int p = chunk * kScoreChunk + lane;
+    if (p >= n) return;
+    const float4 *k4 = reinterpret_cast<const float4 *>(key_cache + (size_t)p * kKVDim + kvh * kAttnDim);
+    float acc[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < 4; ++c) {
+        float4 kk[16];
+        for (int m = 0; m < 16; ++m) kk[m] = k4[c * 16 + m];
+        for (int m = 0; m < 16; ++m) {
+            const float kv[4] = {kk[m].x, kk[m].y, kk[m].z, kk[m].w};
+            for (int e = 0; e < 4; ++e) {
+                const int d = c * 64 + 4 * m + e;
+                for (int j = 0; j < 6; ++j) acc[j] = __builtin_fmaf(qs[j][d], kv[e], acc[j]);
+            }
+        }
+    }
+    for (int j = 0; j < 6; ++j)
+        scores[((size_t)t * kAttnHeads + kvh * 6 + j) * context + p] = __fmul_rn(acc[j], 0.0625f);
+}
 
+/* Softmax and weighted sum of V for q head blockIdx.x of row blockIdx.y
+ * (qwen38_model.c:863-882): maximum; e_p = expf(score_p - max); denominator
+ * summed in position order; out_i = fmaf-chain over positions of
+ * (e_p / denominator) * v_p[i]; out_i *= sigmoid(gate_i); then Q8_K of the
+ * head's 256 outputs (one block of the out-projection input).  IN_LDS: the
+ * softmax weights live in dynamic LDS (context <= 32768), else in place in
+ * the scores row. */
+template <bool IN_LDS>
+__global__ __launch_bounds__(256) void attn_output_kernel(float *__restrict__ out, uint8_t *__restrict__ q_out,
+                                                          float *__restrict__ scores,
+                                                          const float *__restrict__ q_and_gate,
+                                                          const float *__restrict__ value_cache, int context,
+                                                          const uint32_t *__restrict__ position_ptr)
+{
+    extern __shared__ float lds_e[];
+    __shared__ float red[4];
+    __shared__ float den_s;
+    __shared__ float ybuf[kAttnDim];
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const int kvh = h / (kAttnHeads / kKVHeads);
+    const int n = (int)*position_ptr + t + 1;
+    float *sc = scores + ((size_t)t * kAttnHeads + h) * context;
+    float *e = IN_LDS ? lds_e : sc;
     float local_max = -__builtin_inff();
     for (int p = tid; p < n; p += 256) {
-        const float4 *k4 = reinterpret_cast<const float4 *>(key_cache + (size_t)p * kKVDim + kvh * kAttnDim);
-        float s = 0.0f;
-        for (int i4 = 0; i4 < kAttnDim / 4; ++i4) {
-            const float4 kk = k4[i4];
-            s = __builtin_fmaf(qs[4 * i4 + 0], kk.x, s);
-            s = __builtin_fmaf(qs[4 * i4 + 1], kk.y, s);
-            s = __builtin_fmaf(qs[4 * i4 + 2], kk.z, s);
-            s = __builtin_fmaf(qs[4 * i4 + 3], kk.w, s);
-        }
-        s = __fmul_rn(s, 0.0625f);
-        sc[p] = s;
-        local_max = fmaxf(local_max, s);
+        const float v = sc[p];
+        if (IN_LDS) e[p] = v;
+        local_max = fmaxf(local_max, v);
     }
     /* the reference's running max (score > maximum from -inf) equals the
      * max over non-NaN scores; NaN scores never win */
@@ -361,36 +465,54 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(float *__restrict__ ou
     if ((tid & 63) == 0) red[tid >> 6] = local_max;
     __syncthreads();
     const float maximum = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int p = tid; p < n; p += 256) sc[p] = q38_expf(__fsub_rn(sc[p], maximum));
+    for (int p = tid; p < n; p += 256) e[p] = q38_expf(__fsub_rn(e[p], maximum));
     __syncthreads();
     if (tid == 0) {
         float d = 0.0f;
-        for (int p = 0; p < n; ++p) d = __fadd_rn(d, sc[p]);
-        denom_s = d;
+        int p = 0;
+        for (; p + 8 <= n; p += 8) {
+            float a[8];
+            for (int k = 0; k < 8; ++k) a[k] = e[p + k];
+            for (int k = 0; k < 8; ++k) d = __fadd_rn(d, a[k]);
+        }
+        for (; p < n; ++p) d = __fadd_rn(d, e[p]);
+        den_s = d;
     }
     __syncthreads();
-    const float denominator = denom_s;
-    for (int p = tid; p < n; p += 256) sc[p] = div_rn(sc[p], denominator);
+    const float denominator = den_s;
+    for (int p = tid; p < n; p += 256) e[p] = div_rn(e[p], denominator);
     __syncthreads();
-    float o = 0.0f;
     const float *vcol = value_cache + kvh * kAttnDim + tid;
-    for (int p = 0; p < n; ++p) o = __builtin_fmaf(sc[p], vcol[(size_t)p * kKVDim], o);
-    const float g = q_and_gate[h * 2 * kAttnDim + kAttnDim + tid];
-    out[h * kAttnDim + tid] = __fmul_rn(o, sigmoidf_exact(g));
+    float o = 0.0f;
+    int p = 0;
+    for (; p + 8 <= n; p += 8) {
+        float vv[8];
+        for (int k = 0; k < 8; ++k) vv[k] = vcol[(size_t)(p + k) * kKVDim];
+        for (int k = 0; k < 8; ++k) o = __builtin_fmaf(e[p + k], vv[k], o);
+    }
+    for (; p < n; ++p) o = __builtin_fmaf(e[p], vcol[(size_t)p * kKVDim], o);
+    const float g = q_and_gate[(size_t)t * kQGDim + h * 2 * kAttnDim + kAttnDim + tid];
+    const float y = __fmul_rn(o, sigmoidf_exact(g));
+    out[(size_t)t * kQDim + h * kAttnDim + tid] = y;
+    ybuf[tid] = y;
+    __syncthreads();
+    if (tid < 64) {
+        const float q4[4] = {ybuf[4 * tid], ybuf[4 * tid + 1], ybuf[4 * tid + 2], ybuf[4 * tid + 3]};
+        wave_quantize_q8k(q4, q_out + ((size_t)t * kAttnHeads + h) * kQ8KBytes, tid);
+    }
 }
 
 /* ---- launchers ----------------------------------------------------------- */
 
-void launch_rmsnorm(float *out, const float *in, const float *weight, int n, int rows, long long out_stride,
-                    long long in_stride, hipStream_t stream)
+void launch_norm_quant(float *norm_out, long long norm_stride, uint8_t *q_out, int q_stride_blocks, float *hidden,
+                       long long in_stride, const float *branch, const float *weight, int rows, hipStream_t stream)
 {
-    rmsnorm_kernel<<<rows, 256, 0, stream>>>(out, in, weight, n, out_stride, in_stride);
-}
-
-void launch_add_rmsnorm(float *norm, float *hidden, const float *branch, const float *weight, int n, int rows,
-                        hipStream_t stream)
-{
-    add_rmsnorm_kernel<<<rows, 256, 0, stream>>>(norm, hidden, branch, weight, n);
+    if (branch)
+        norm_quant_kernel<5, true><<<rows, 256, 0, stream>>>(norm_out, norm_stride, q_out, q_stride_blocks, hidden,
+                                                              in_stride, branch, weight);
+    else
+        norm_quant_kernel<5, false><<<rows, 256, 0, stream>>>(norm_out, norm_stride, q_out, q_stride_blocks, hidden,
+                                                               in_stride, nullptr, weight);
 }
 
 void launch_add(float *hidden, const float *branch, long long n, hipStream_t stream)
@@ -398,9 +520,10 @@ void launch_add(float *hidden, const float *branch, long long n, hipStream_t str
     add_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(hidden, branch, n);
 }
 
-void launch_swiglu(float *gate, const float *up, long long n, hipStream_t stream)
+void launch_swiglu_quant(uint8_t *q_out, const float *gate, const float *up, int rows, hipStream_t stream)
 {
-    swiglu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(gate, up, n);
+    const int nblocks = rows * (kFFNWidth / 256);
+    swiglu_quant_kernel<<<(nblocks + 3) / 4, 256, 0, stream>>>(q_out, gate, up, nblocks);
 }
 
 void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int count, int width, uint32_t vocab,
@@ -422,28 +545,41 @@ void launch_deltanet_state(float *attn, float *delta_state, const float *qkv, co
                                                                      query_scale);
 }
 
-void launch_deltanet_out(float *attn, const float *z, const float *ssm_norm, hipStream_t stream)
+void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, const float *ssm_norm, int rows,
+                               hipStream_t stream)
 {
-    deltanet_out_kernel<<<kVHeads, 128, 0, stream>>>(attn, z, ssm_norm);
+    deltanet_out_quant_kernel<<<dim3(kVHeads / 2, rows), 256, 0, stream>>>(attn, q_out, z, ssm_norm);
 }
 
-void launch_attention(float *attn, float *q_buf, const float *q_and_gate, const float *key, const float *value,
-                      const float *q_norm, const float *k_norm, const float *rope, float *key_cache,
-                      float *value_cache, float *scores, int context, const uint32_t *position, int row_offset,
-                      hipStream_t stream)
+bool configure_attention(int context)
 {
-    attn_prep_kernel<<<kAttnHeads + kKVHeads + 1, 256, 0, stream>>>(q_buf, q_and_gate, key, value, q_norm, k_norm,
-                                                                     rope, key_cache, value_cache, position,
-                                                                     row_offset, 0);
-    attn_decode_kernel<<<kAttnHeads, 256, 0, stream>>>(attn, q_buf, q_and_gate, key_cache, value_cache, scores,
-                                                       context, position, row_offset);
+    if (context > kMaxLdsPositions) return true;
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_output_kernel<true>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, context * 4) == hipSuccess;
+}
+
+void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_and_gate, const float *key,
+                      const float *value, const float *q_norm, const float *k_norm, const float *rope,
+                      float *key_cache, float *value_cache, float *scores, int context, const uint32_t *position,
+                      int rows, hipStream_t stream)
+{
+    attn_prep_kernel<<<dim3(kAttnHeads + kKVHeads + 1, rows), 256, 0, stream>>>(
+        q_buf, q_and_gate, key, value, q_norm, k_norm, rope, key_cache, value_cache, position, 0);
+    attn_scores_kernel<<<dim3(kKVHeads, (context + kScoreChunk - 1) / kScoreChunk, rows), 64, 0, stream>>>(
+        scores, q_buf, key_cache, context, position);
+    if (context <= kMaxLdsPositions)
+        attn_output_kernel<true><<<dim3(kAttnHeads, rows), 256, (size_t)context * 4, stream>>>(
+            attn, q_out, scores, q_and_gate, value_cache, context, position);
+    else
+        attn_output_kernel<false><<<dim3(kAttnHeads, rows), 256, 0, stream>>>(attn, q_out, scores, q_and_gate,
+                                                                             value_cache, context, position);
 }
 
 void launch_kv_write(const float *key, const float *value, const float *k_norm, const float *rope, float *key_cache,
-                     float *value_cache, const uint32_t *position, int row_offset, hipStream_t stream)
+                     float *value_cache, const uint32_t *position, int rows, hipStream_t stream)
 {
-    attn_prep_kernel<<<kKVHeads + 1, 256, 0, stream>>>(nullptr, nullptr, key, value, nullptr, k_norm, rope, key_cache,
-                                                       value_cache, position, row_offset, kAttnHeads);
+    attn_prep_kernel<<<dim3(kKVHeads + 1, rows), 256, 0, stream>>>(nullptr, nullptr, key, value, nullptr, k_norm, rope,
+                                                                  key_cache, value_cache, position, kAttnHeads);
 }
 
 }  // namespace q38

@@ -99,3 +99,19 @@ def write_model_gguf(path, seed, variant="q4km"):
         raise RuntimeError("synthetic GGUF writer not built: make -C qwen3.8-27b-in-c_amd")
     subprocess.run([SYNTH_GGUF, path, str(seed), variant], check=True)
     return path
+
+
+def model_path(seed, variant="q4km"):
+    """Where the synthetic model of `seed` lives (or will be written): a file
+    q38_<variant>_s<seed>.gguf in $Q38_MODEL_DIR, /dev/shm or the system
+    temporary directory, the first with room for it.  None if none has."""
+    import shutil
+    import tempfile
+    need = MODEL_GGUF_BYTES.get(variant, 16 << 30)
+    name = "q38_%s_s%d.gguf" % (variant, seed)
+    for d in (os.environ.get("Q38_MODEL_DIR"), "/dev/shm", tempfile.gettempdir()):
+        if d and os.path.isdir(d) and os.access(d, os.W_OK):
+            path = os.path.join(d, name)
+            if os.path.exists(path) or shutil.disk_usage(d).free > need + (2 << 30):
+                return path
+    return None

@@ -38,29 +38,13 @@ def device():
 MODEL_SEED = 1
 
 
-def _model_dir(need_bytes):
-    """A directory with room for the synthetic model: $Q38_MODEL_DIR, then
-    /dev/shm, then the system temporary directory."""
-    import shutil
-    import tempfile
-    candidates = [os.environ.get("Q38_MODEL_DIR"), "/dev/shm", tempfile.gettempdir()]
-    for d in candidates:
-        if d and os.path.isdir(d) and os.access(d, os.W_OK):
-            existing = os.path.join(d, "q38_q4km_s%d.gguf" % MODEL_SEED)
-            if os.path.exists(existing) or shutil.disk_usage(d).free > need_bytes + (2 << 30):
-                return d
-    return None
-
-
 @pytest.fixture(scope="session")
 def model_gguf():
     """Path of the synthetic 27B-shaped Q4_K_M GGUF (seed 1), written by
     qwen3.8-27b-in-c_amd/synth/q38_synth_gguf when missing (about 15.7 GB)."""
     from q38hip import synth
-    need = synth.MODEL_GGUF_BYTES["q4km"]
-    d = _model_dir(need)
-    if d is None:
+    path = synth.model_path(MODEL_SEED, "q4km")
+    if path is None:
         pytest.skip("no directory with 17 GB free for the synthetic model")
-    path = os.path.join(d, "q38_q4km_s%d.gguf" % MODEL_SEED)
     print("synthetic model:", path, flush=True)
     return synth.write_model_gguf(path, MODEL_SEED, "q4km")
