@@ -301,15 +301,19 @@ struct Q38Model {
     hipStream_t stream = nullptr;
     const void *grid = nullptr;
     /* state */
+    /* recurrent state: kRecurrentStateSlots slots of [48 layers][...]; layer r's
+     * current slot is slot_host[r] (mirrored in params[1 + r]) */
     float *conv_state = nullptr, *delta_state = nullptr, *key_cache = nullptr, *value_cache = nullptr;
-    float *mtp_hidden = nullptr, *ck_conv = nullptr, *ck_delta = nullptr, *ck_mtp_hidden = nullptr;
+    float *mtp_hidden = nullptr, *ck_mtp_hidden = nullptr;
+    uint32_t slot_host[kRecurrent] = {0}, ck_slot[kRecurrent] = {0};
     float *rope = nullptr;
     /* scratch, kBatch rows */
     float *hidden = nullptr, *norm = nullptr, *branch = nullptr, *wide0 = nullptr, *wide1 = nullptr;
     float *kbuf = nullptr, *vbuf = nullptr, *qbuf = nullptr, *attn = nullptr, *beta = nullptr, *alpha = nullptr;
     float *scores = nullptr, *logits = nullptr, *target_norm = nullptr;
     uint8_t *q8k = nullptr;
-    uint32_t *tokens = nullptr, *positions = nullptr, *targets = nullptr, *drafts = nullptr, *accept = nullptr;
+    /* params[0] = position of row 0 of the current step, params[1 + r] = slot of recurrent layer r */
+    uint32_t *tokens = nullptr, *params = nullptr, *targets = nullptr, *drafts = nullptr, *accept = nullptr;
     float *argmax_pv = nullptr;
     uint32_t *argmax_pi = nullptr;
     /* host side */
@@ -497,11 +501,11 @@ void release(Q38Model *m)
     if (!m) return;
     if (m->stream) (void)hipStreamSynchronize(m->stream);
     float **fbufs[] = {&m->conv_state, &m->delta_state, &m->key_cache, &m->value_cache, &m->mtp_hidden,
-                       &m->ck_conv, &m->ck_delta, &m->ck_mtp_hidden, &m->rope, &m->hidden, &m->norm,
+                       &m->ck_mtp_hidden, &m->rope, &m->hidden, &m->norm,
                        &m->branch, &m->wide0, &m->wide1, &m->kbuf, &m->vbuf, &m->qbuf, &m->attn, &m->beta,
                        &m->alpha, &m->scores, &m->logits, &m->target_norm, &m->argmax_pv};
     for (float **p : fbufs) dfree(*p);
-    uint32_t **ubufs[] = {&m->tokens, &m->positions, &m->targets, &m->drafts, &m->accept, &m->argmax_pi};
+    uint32_t **ubufs[] = {&m->tokens, &m->params, &m->targets, &m->drafts, &m->accept, &m->argmax_pi};
     for (uint32_t **p : ubufs) dfree(*p);
     dfree(m->q8k);
     if (m->weights) (void)hipFree(m->weights);
@@ -516,7 +520,8 @@ bool allocate_state(Q38Model *m)
 {
     const uint32_t ctx = m->context_length;
     const uint32_t B = kBatch;
-    bool ok = dalloc(&m->conv_state, conv_count()) && dalloc(&m->delta_state, delta_count()) &&
+    const size_t slots = q38::kRecurrentStateSlots;
+    bool ok = dalloc(&m->conv_state, slots * conv_count()) && dalloc(&m->delta_state, slots * delta_count()) &&
               dalloc(&m->key_cache, kv_count(ctx)) && dalloc(&m->value_cache, kv_count(ctx)) &&
               dalloc(&m->mtp_hidden, kHidden) && dalloc(&m->rope, (size_t)ctx * 64) &&
               dalloc(&m->hidden, (size_t)B * kHidden) && dalloc(&m->norm, (size_t)B * 2 * kHidden) &&
@@ -527,12 +532,12 @@ bool allocate_state(Q38Model *m)
               dalloc(&m->alpha, (size_t)B * kVHeads) && dalloc(&m->scores, (size_t)B * kAttnHeads * ctx) &&
               dalloc(&m->logits, (size_t)B * kVocab) && dalloc(&m->target_norm, (size_t)B * kHidden) &&
               dalloc(&m->q8k, (size_t)B * (kFFN / 256) * kQ8KBytes) && dalloc(&m->tokens, B) &&
-              dalloc(&m->positions, 4) && dalloc(&m->targets, B) && dalloc(&m->drafts, B) &&
+              dalloc(&m->params, 64) && dalloc(&m->targets, B) && dalloc(&m->drafts, B) &&
               dalloc(&m->accept, B + 3) && dalloc(&m->argmax_pv, (size_t)B * q38::argmax_chunks(kVocab)) &&
               dalloc(&m->argmax_pi, (size_t)B * q38::argmax_chunks(kVocab)) &&
               hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_logits), kVocab * sizeof(float)),
                      "pinned logits") &&
-              hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_words), 64 * sizeof(uint32_t)), "pinned ids");
+              hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_words), 128 * sizeof(uint32_t)), "pinned ids");
     if (!ok) return false;
     /* RoPE table: theta starts at the position and is multiplied by
      * powf(1e7, -2/64) per pair; cosf/sinf of the host C library, exactly the
@@ -552,10 +557,12 @@ bool allocate_state(Q38Model *m)
                   "rope table upload");
 }
 
-/* zero the recurrent state, KV caches and MTP hidden (q38_model_reset) */
+/* zero the recurrent state (slot 0 of every layer becomes current), KV
+ * caches and MTP hidden (q38_model_reset) */
 bool clear_state(Q38Model *m)
 {
     hipStream_t s = m->stream;
+    for (uint32_t r = 0; r < kRecurrent; ++r) m->slot_host[r] = 0;
     return hip_ok(hipMemsetAsync(m->conv_state, 0, conv_count() * sizeof(float), s), "reset") &&
            hip_ok(hipMemsetAsync(m->delta_state, 0, delta_count() * sizeof(float), s), "reset") &&
            hip_ok(hipMemsetAsync(m->key_cache, 0, kv_count(m->context_length) * sizeof(float), s), "reset") &&
@@ -615,12 +622,26 @@ bool gemm_q(Q38Model *m, const DevTensor &w, uint32_t count, float *out, size_t 
     return true;
 }
 
+/* step parameters: position of row 0 and the current state slot of every
+ * recurrent layer */
 bool set_positions(Q38Model *m, uint32_t base)
 {
-    m->host_words[32] = base;
-    return hip_ok(hipMemcpyAsync(m->positions, &m->host_words[32], 4, hipMemcpyHostToDevice, m->stream),
-                  "position upload") &&
-           hip_ok(hipStreamSynchronize(m->stream), "position upload");
+    m->host_words[64] = base;
+    for (uint32_t r = 0; r < kRecurrent; ++r) m->host_words[65 + r] = m->slot_host[r];
+    return hip_ok(hipMemcpyAsync(m->params, &m->host_words[64], (1 + kRecurrent) * sizeof(uint32_t),
+                                 hipMemcpyHostToDevice, m->stream),
+                  "parameter upload") &&
+           hip_ok(hipStreamSynchronize(m->stream), "parameter upload");
+}
+
+/* after `rows` rows ran through recurrent layers 0..layers-1 */
+void advance_slots(Q38Model *m, uint32_t rows, uint32_t layers = kLayers)
+{
+    for (uint32_t layer = 0; layer < layers; ++layer) {
+        if ((layer + 1) % 4 == 0) continue;
+        const uint32_t r = layer - (layer + 1) / 4;
+        m->slot_host[r] = (m->slot_host[r] + rows) % q38::kRecurrentStateSlots;
+    }
 }
 
 /* apply a pending FFN residual add to m->hidden */
@@ -651,10 +672,10 @@ bool full_attention_rows(Q38Model *m, int layer, uint32_t count)
         return false;
     q38::launch_attention(m->attn, m->q8k, m->qbuf, m->wide0, m->kbuf, m->vbuf, L.q_norm.f32(), L.k_norm.f32(),
                           m->rope, m->key_cache + kv_off, m->value_cache + kv_off, m->scores, (int)m->context_length,
-                          m->positions, (int)count, m->stream);
+                          m->params, (int)count, m->stream);
     if (count == 1 && trace_enabled()) {
         uint32_t pos = 0;
-        (void)hipMemcpy(&pos, m->positions, 4, hipMemcpyDeviceToHost);
+        (void)hipMemcpy(&pos, m->params, 4, hipMemcpyDeviceToHost);
         trace(m, "Qcur_full-", layer, m->wide0, kQGDim);
         trace(m, "Kcur-", layer, m->key_cache + kv_off + (size_t)pos * kKVDim, kKVDim);
         trace(m, "Vcur-", layer, m->vbuf, kKVDim);
@@ -683,14 +704,15 @@ bool linear_attention_rows(Q38Model *m, int layer, uint32_t count)
     for (uint32_t t = 0; t < count; ++t) {
         float *qkv = m->wide0 + (size_t)t * kQKV, *attn = m->attn + (size_t)t * kLinV;
         float *beta = m->beta + (size_t)t * kVHeads, *alpha = m->alpha + (size_t)t * kVHeads;
-        q38::launch_deltanet_prep(qkv, beta, alpha, m->conv_state + (size_t)r * kQKV * 3, L.conv.f32(), L.a.f32(),
-                                  L.dt.f32(), m->stream);
+        q38::launch_deltanet_prep(qkv, beta, alpha, m->conv_state + (size_t)r * kQKV * 3, (long long)conv_count(),
+                                  m->params + 1 + r, (int)t, L.conv.f32(), L.a.f32(), L.dt.f32(), m->stream);
         if (tr) {
             trace(m, "dn_qkv-", layer, qkv, kQKV);
             trace(m, "dn_beta-", layer, beta, kVHeads);
             trace(m, "dn_alpha-", layer, alpha, kVHeads);
         }
-        q38::launch_deltanet_state(attn, m->delta_state + (size_t)r * kVHeads * kHeadDim * kHeadDim, qkv, beta, alpha,
+        q38::launch_deltanet_state(attn, m->delta_state + (size_t)r * kVHeads * kHeadDim * kHeadDim,
+                                   (long long)delta_count(), m->params + 1 + r, (int)t, qkv, beta, alpha,
                                    m->query_scale, m->stream);
         if (tr) trace(m, "dn_core-", layer, attn, kLinV);
     }
@@ -739,6 +761,7 @@ bool target_rows(Q38Model *m, uint32_t count, uint32_t base, uint32_t logit_rows
     norm_hidden(m, m->output_norm, count, m->target_norm);
     if (logit_rows && !gemm_q(m, m->output, logit_rows, m->logits, (size_t)(count - logit_rows) * (kHidden / 256)))
         return false;
+    advance_slots(m, count);
     return true;
 }
 
@@ -788,7 +811,7 @@ bool mtp_catchup(Q38Model *m, uint32_t count, uint32_t base)
     if (!gemm_q(m, L.k, count, m->kbuf) || !gemm_q(m, L.v, count, m->vbuf)) return false;
     const size_t kv_off = (size_t)(kLayers / 4) * m->context_length * kKVDim;
     q38::launch_kv_write(m->kbuf, m->vbuf, L.k_norm.f32(), m->rope, m->key_cache + kv_off, m->value_cache + kv_off,
-                         m->positions, (int)count, m->stream);
+                         m->params, (int)count, m->stream);
     if (!hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm + (size_t)(count - 1) * kHidden,
                                kHidden * sizeof(float), hipMemcpyDeviceToDevice, m->stream),
                 "mtp hidden"))
@@ -819,25 +842,26 @@ bool mtp_step(Q38Model *m)
     return true;
 }
 
+/* q38_checkpoint_state (qwen38_model.c:1200-1210): the recurrent state is
+ * not copied, only its slot indices are remembered; the slots a verify
+ * batch writes are the ones after the current one, so the checkpointed
+ * state stays intact. */
 bool checkpoint(Q38Model *m)
 {
     m->ck_position = m->position;
     m->ck_mtp_position = m->mtp_position;
-    return hip_ok(hipMemcpyAsync(m->ck_conv, m->conv_state, conv_count() * sizeof(float), hipMemcpyDeviceToDevice,
-                                 m->stream), "checkpoint") &&
-           hip_ok(hipMemcpyAsync(m->ck_delta, m->delta_state, delta_count() * sizeof(float),
-                                 hipMemcpyDeviceToDevice, m->stream), "checkpoint") &&
-           hip_ok(hipMemcpyAsync(m->ck_mtp_hidden, m->mtp_hidden, kHidden * sizeof(float), hipMemcpyDeviceToDevice,
+    for (uint32_t r = 0; r < kRecurrent; ++r) m->ck_slot[r] = m->slot_host[r];
+    return hip_ok(hipMemcpyAsync(m->ck_mtp_hidden, m->mtp_hidden, kHidden * sizeof(float), hipMemcpyDeviceToDevice,
                                  m->stream), "checkpoint");
 }
 
-bool restore_target(Q38Model *m)
+/* target state after the first `rows` rows of the batch that followed the
+ * checkpoint (rows = 0 restores the checkpoint itself) */
+void restore_target(Q38Model *m, uint32_t rows = 0)
 {
-    m->position = m->ck_position;
-    return hip_ok(hipMemcpyAsync(m->conv_state, m->ck_conv, conv_count() * sizeof(float), hipMemcpyDeviceToDevice,
-                                 m->stream), "restore") &&
-           hip_ok(hipMemcpyAsync(m->delta_state, m->ck_delta, delta_count() * sizeof(float),
-                                 hipMemcpyDeviceToDevice, m->stream), "restore");
+    m->position = m->ck_position + rows;
+    for (uint32_t r = 0; r < kRecurrent; ++r)
+        m->slot_host[r] = (m->ck_slot[r] + rows) % q38::kRecurrentStateSlots;
 }
 
 bool restore_mtp(Q38Model *m)
@@ -934,6 +958,7 @@ int q38_model_forward_token_layers(Q38Model *m, uint32_t token, uint32_t layer_c
     for (uint32_t layer = 0; layer < layer_count; ++layer)
         if (!layer_rows(m, (int)layer, 1)) return 0;
     flush_branch(m, 1);
+    advance_slots(m, 1, layer_count);
     if (!hip_ok(hipMemcpyAsync(hidden_out, m->hidden, kHidden * sizeof(float), hipMemcpyDeviceToHost, m->stream),
                 "hidden download") ||
         !hip_ok(hipStreamSynchronize(m->stream), "hidden download"))
@@ -969,9 +994,7 @@ int q38_model_enable_mtp(Q38Model *m)
         fprintf(stderr, "qwen38: MTP weights are unavailable; attach the MTP GGUF first\n");
         return 0;
     }
-    if (!m->ck_conv && !(dalloc(&m->ck_conv, conv_count()) && dalloc(&m->ck_delta, delta_count()) &&
-                         dalloc(&m->ck_mtp_hidden, kHidden)))
-        return 0;
+    if (!m->ck_mtp_hidden && !dalloc(&m->ck_mtp_hidden, kHidden)) return 0;
     m->mtp_enabled = true;
     return 1;
 }
@@ -1035,22 +1058,23 @@ int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_toke
         matched = m->host_words[45];
         for (uint32_t i = 0; i < consumed; ++i) accepted[i] = m->host_words[47 + i];
     }
+    /* On a rejection the reference restores its checkpoint and replays the
+     * consumed rows (qwen38_model.c:1684-1691).  Every row of the verify
+     * batch computed exactly what the replay would (rows are independent in
+     * the GEMMs and the recurrent state advanced row by row), so the state
+     * after the consumed rows is already in slot checkpoint + consumed, their
+     * K/V entries are in the caches, and the last consumed row's logits are
+     * row consumed - 1 of the batch; entries of the rejected rows are never
+     * read before being overwritten. */
     const float *last_row = m->logits + (size_t)(consumed ? consumed - 1 : 0) * kVocab;
-    if (ok && consumed < n) {
-        /* rejected: restore the target state and replay the consumed rows
-         * (qwen38_model.c:1684-1691) */
-        ok = restore_target(m) && upload_tokens(m, inputs, consumed) &&
-             target_rows(m, consumed, m->position, 1);
-        last_row = m->logits;
-        if (ok) m->position = m->ck_position + consumed;
-    }
+    if (ok) restore_target(m, consumed);
     if (ok) {
         ok = logits_to_host(m, last_row) && restore_mtp(m) && upload_tokens(m, inputs, consumed) &&
              mtp_catchup(m, consumed, m->ck_mtp_position);
         ok = ok && hip_ok(hipStreamSynchronize(m->stream), "catch-up");
     }
     if (!ok) {
-        (void)restore_target(m);
+        restore_target(m);
         (void)restore_mtp(m);
         (void)hipStreamSynchronize(m->stream);
         return 0;

@@ -6,6 +6,9 @@
 
 namespace q38 {
 
+/* state slots of each recurrent layer: one more than the largest batch */
+constexpr uint32_t kRecurrentStateSlots = 9;
+
 /* q38_gemm.hip: y[m][rows] = W (rows x nblk*256, GGUF type) . x (m Q8_K rows);
  * m <= 8.  `grid` is the device IQ1_M codebook (2048 x 8 int8). */
 bool launch_gemm(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, uint32_t nblk,
@@ -28,10 +31,16 @@ void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int 
                       hipStream_t stream);
 /* gated DeltaNet core of one row: conv + SiLU + q/k L2 norm + beta/alpha,
  * then the state update; the per-head norm, z gate and Q8_K run over all rows */
-void launch_deltanet_prep(float *qkv, float *beta, float *alpha, float *conv_state, const float *conv_w,
-                          const float *ssm_a, const float *ssm_dt, hipStream_t stream);
-void launch_deltanet_state(float *attn, float *delta_state, const float *qkv, const float *beta, const float *alpha,
-                           float query_scale, hipStream_t stream);
+/* Recurrent state lives in kRecurrentStateSlots slots per layer, `slot_stride`
+ * floats apart: row t of a batch reads slot (*slot + t) and writes slot
+ * (*slot + t + 1), both mod kRecurrentStateSlots, so the state after any
+ * prefix of the batch stays available. */
+void launch_deltanet_prep(float *qkv, float *beta, float *alpha, float *conv_state, long long slot_stride,
+                          const uint32_t *slot, int row, const float *conv_w, const float *ssm_a, const float *ssm_dt,
+                          hipStream_t stream);
+void launch_deltanet_state(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int row,
+                           const float *qkv, const float *beta, const float *alpha, float query_scale,
+                           hipStream_t stream);
 void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, const float *ssm_norm, int rows,
                                hipStream_t stream);
 /* full attention over `rows` rows at positions *position + t: prep (norms,

@@ -196,12 +196,17 @@ __global__ __launch_bounds__(256) void embed_q4k_kernel(float *__restrict__ out,
 /* ---- gated DeltaNet ------------------------------------------------------ */
 
 constexpr int kQKV = 10240, kQKDim = 2048, kVHeads = 48, kHeadDim = 128, kLinV = 6144, kFFNWidth = 17408;
+constexpr uint32_t kStateSlots = kRecurrentStateSlots;
 
 /* Causal conv (4 taps, state of 3 per channel), SiLU, per-head L2 norm of q
  * and k, and the beta / alpha transforms (q38_linear_core,
  * qwen38_model.c:720-757).  Blocks 0..79 each own 128 channels (blocks 0..31
- * are the 16 q heads and 16 k heads); block 80 does beta/alpha. */
+ * are the 16 q heads and 16 k heads); block 80 does beta/alpha.
+ * The conv state of row `row` is read from slot (*slot_ptr + row) and the
+ * shifted state written to the next slot (mod kStateSlots). */
 __global__ __launch_bounds__(128) void deltanet_prep_kernel(float *__restrict__ qkv, float *__restrict__ conv_state,
+                                                            long long slot_stride,
+                                                            const uint32_t *__restrict__ slot_ptr, int row,
                                                             const float *__restrict__ conv_w,
                                                             float *__restrict__ beta, float *__restrict__ alpha,
                                                             const float *__restrict__ ssm_a,
@@ -216,17 +221,20 @@ __global__ __launch_bounds__(128) void deltanet_prep_kernel(float *__restrict__ 
         return;
     }
     const int ch = blockIdx.x * 128 + tid;
-    float *st = conv_state + (size_t)ch * 3;
+    const uint32_t slot = *slot_ptr + row;
+    const float *st = conv_state + (size_t)(slot % kStateSlots) * slot_stride + (size_t)ch * 3;
+    float *st_out = conv_state + (size_t)((slot + 1) % kStateSlots) * slot_stride + (size_t)ch * 3;
     const float *k = conv_w + (size_t)ch * 4;
     const float x = qkv[ch];
+    const float s0 = st[0], s1 = st[1], s2 = st[2];
     float value = 0.0f;
-    value = __fadd_rn(value, __fmul_rn(st[0], k[0]));
-    value = __fadd_rn(value, __fmul_rn(st[1], k[1]));
-    value = __fadd_rn(value, __fmul_rn(st[2], k[2]));
+    value = __fadd_rn(value, __fmul_rn(s0, k[0]));
+    value = __fadd_rn(value, __fmul_rn(s1, k[1]));
+    value = __fadd_rn(value, __fmul_rn(s2, k[2]));
     value = __fadd_rn(value, __fmul_rn(x, k[3]));
-    st[0] = st[1];
-    st[1] = st[2];
-    st[2] = x;
+    st_out[0] = s1;
+    st_out[1] = s2;
+    st_out[2] = x;
     const float y = siluf_exact(value);
     if (ch >= 2 * kQKDim) {
         qkv[ch] = y;
@@ -260,8 +268,11 @@ __device__ __forceinline__ float avx2_tree32(float v)
  * S_c = fma(k, delta, S_c); out[c] = dot(S_c, q) * (1/sqrt(128)).
  * Columns are independent: 32 lanes per column (lane l owns elements
  * l, l+32, l+64, l+96, the reference's fixed 4 x 8-lane accumulators), two
- * columns per wavefront, eight per block of 256. */
+ * columns per wavefront, eight per block of 256.  The state of row `row` is
+ * read from slot (*slot_ptr + row) and written to the next slot. */
 __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__ out, float *__restrict__ state,
+                                                             long long slot_stride,
+                                                             const uint32_t *__restrict__ slot_ptr, int row,
                                                              const float *__restrict__ qkv,
                                                              const float *__restrict__ beta,
                                                              const float *__restrict__ alpha, float query_scale)
@@ -274,7 +285,9 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
     const float *q = qkv + kh * kHeadDim;
     const float *k = qkv + kQKDim + kh * kHeadDim;
     const float *v = qkv + 2 * kQKDim + h * kHeadDim;
-    float *s = state + ((size_t)h * kHeadDim + c) * kHeadDim;
+    const uint32_t slot = *slot_ptr + row;
+    const float *s = state + (size_t)(slot % kStateSlots) * slot_stride + ((size_t)h * kHeadDim + c) * kHeadDim;
+    float *s_out = state + (size_t)((slot + 1) % kStateSlots) * slot_stride + ((size_t)h * kHeadDim + c) * kHeadDim;
     const float decay = q38_expf(alpha[h]);
     float sv[4], kv[4], qv[4];
     for (int a = 0; a < 4; ++a) {
@@ -289,7 +302,7 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
     float r = 0.0f;
     for (int a = 0; a < 4; ++a) {
         sv[a] = __builtin_fmaf(kv[a], delta, sv[a]);
-        s[32 * a + l] = sv[a];
+        s_out[32 * a + l] = sv[a];
         r = __builtin_fmaf(sv[a], qv[a], r);
     }
     const float result = avx2_tree32(r);
@@ -532,17 +545,20 @@ void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int 
     embed_q4k_kernel<<<dim3(width / 256, count), 256, 0, stream>>>(out, w, tokens, width / 256, vocab);
 }
 
-void launch_deltanet_prep(float *qkv, float *beta, float *alpha, float *conv_state, const float *conv_w,
-                          const float *ssm_a, const float *ssm_dt, hipStream_t stream)
+void launch_deltanet_prep(float *qkv, float *beta, float *alpha, float *conv_state, long long slot_stride,
+                          const uint32_t *slot, int row, const float *conv_w, const float *ssm_a, const float *ssm_dt,
+                          hipStream_t stream)
 {
-    deltanet_prep_kernel<<<kQKV / 128 + 1, 128, 0, stream>>>(qkv, conv_state, conv_w, beta, alpha, ssm_a, ssm_dt);
+    deltanet_prep_kernel<<<kQKV / 128 + 1, 128, 0, stream>>>(qkv, conv_state, slot_stride, slot, row, conv_w, beta,
+                                                             alpha, ssm_a, ssm_dt);
 }
 
-void launch_deltanet_state(float *attn, float *delta_state, const float *qkv, const float *beta, const float *alpha,
-                           float query_scale, hipStream_t stream)
+void launch_deltanet_state(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int row,
+                           const float *qkv, const float *beta, const float *alpha, float query_scale,
+                           hipStream_t stream)
 {
-    deltanet_state_kernel<<<kVHeads * kHeadDim / 8, 256, 0, stream>>>(attn, delta_state, qkv, beta, alpha,
-                                                                     query_scale);
+    deltanet_state_kernel<<<kVHeads * kHeadDim / 8, 256, 0, stream>>>(attn, delta_state, slot_stride, slot, row, qkv,
+                                                                     beta, alpha, query_scale);
 }
 
 void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, const float *ssm_norm, int rows,
