@@ -21,6 +21,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <map>
 #include <unordered_map>
 #include <vector>
 
@@ -40,6 +41,11 @@ constexpr uint32_t kQGDim = 12288, kQDim = 6144, kKVDim = 1024, kAttnHeads = 24;
 constexpr uint32_t kVocab = 248320;
 constexpr uint32_t kBatch = 8;           /* rows per batched step (GEMM limit) */
 constexpr uint32_t kQ8KBytes = 292;
+
+/* device parameter blocks of kParamWords words: [0] position of row 0 of
+ * the step, [1 + r] current state slot of recurrent layer r */
+constexpr uint32_t kParamWords = 64;
+enum : uint32_t { kParamTarget = 0, kParamCatchup = 1, kParamDraft0 = 2, kParamSets = 2 + kBatch };
 
 enum : uint32_t { F32 = 0, Q4_K = 12, Q6_K = 14, IQ1_M = 29 };
 
@@ -319,8 +325,14 @@ struct Q38Model {
     /* host side */
     float *host_logits = nullptr;
     uint32_t *host_words = nullptr;
+    uint32_t *host_params = nullptr;   /* pinned staging of the device parameter blocks */
     float query_scale = 0.0f;
     bool pending_branch = false;   /* m->branch holds an FFN output not yet added to m->hidden */
+    /* instantiated HIP graphs of the step sequences, by key; `seen` marks
+     * keys that already ran once without capture */
+    std::map<uint64_t, hipGraphExec_t> graphs;
+    std::map<uint64_t, bool> seen;
+    bool graphs_enabled = true;
 };
 
 namespace {
@@ -512,6 +524,8 @@ void release(Q38Model *m)
     if (m->mtp_weights) (void)hipFree(m->mtp_weights);
     if (m->host_logits) (void)hipHostFree(m->host_logits);
     if (m->host_words) (void)hipHostFree(m->host_words);
+    if (m->host_params) (void)hipHostFree(m->host_params);
+    for (auto &g : m->graphs) (void)hipGraphExecDestroy(g.second);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
 }
@@ -532,12 +546,15 @@ bool allocate_state(Q38Model *m)
               dalloc(&m->alpha, (size_t)B * kVHeads) && dalloc(&m->scores, (size_t)B * kAttnHeads * ctx) &&
               dalloc(&m->logits, (size_t)B * kVocab) && dalloc(&m->target_norm, (size_t)B * kHidden) &&
               dalloc(&m->q8k, (size_t)B * (kFFN / 256) * kQ8KBytes) && dalloc(&m->tokens, B) &&
-              dalloc(&m->params, 64) && dalloc(&m->targets, B) && dalloc(&m->drafts, B) &&
+              dalloc(&m->params, (size_t)kParamSets * kParamWords) && dalloc(&m->targets, B) &&
+              dalloc(&m->drafts, B + 1) &&
               dalloc(&m->accept, B + 3) && dalloc(&m->argmax_pv, (size_t)B * q38::argmax_chunks(kVocab)) &&
               dalloc(&m->argmax_pi, (size_t)B * q38::argmax_chunks(kVocab)) &&
               hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_logits), kVocab * sizeof(float)),
                      "pinned logits") &&
-              hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_words), 128 * sizeof(uint32_t)), "pinned ids");
+              hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_words), 128 * sizeof(uint32_t)), "pinned ids") &&
+              hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_params),
+                                   (size_t)kParamSets * kParamWords * sizeof(uint32_t)), "pinned parameters");
     if (!ok) return false;
     /* RoPE table: theta starts at the position and is multiplied by
      * powf(1e7, -2/64) per pair; cosf/sinf of the host C library, exactly the
@@ -612,6 +629,17 @@ void trace(Q38Model *m, const char *name, int layer, const float *device, uint64
 
 /* ---- step building blocks -------------------------------------------------- */
 
+/* Where a step reads its parameter block and its input token ids (device). */
+struct Step {
+    const uint32_t *params;
+    const uint32_t *tokens;
+};
+
+Step step_of(Q38Model *m, uint32_t param_set, const uint32_t *tokens)
+{
+    return Step{m->params + (size_t)param_set * kParamWords, tokens};
+}
+
 /* GEMM over `count` Q8_K rows already in m->q8k (starting at block
  * `first_block`) */
 bool gemm_q(Q38Model *m, const DevTensor &w, uint32_t count, float *out, size_t first_block = 0)
@@ -622,16 +650,21 @@ bool gemm_q(Q38Model *m, const DevTensor &w, uint32_t count, float *out, size_t 
     return true;
 }
 
-/* step parameters: position of row 0 and the current state slot of every
- * recurrent layer */
-bool set_positions(Q38Model *m, uint32_t base)
+/* host staging of a parameter block: position of row 0 and the current
+ * state slot of every recurrent layer */
+void write_params(Q38Model *m, uint32_t set, uint32_t position)
 {
-    m->host_words[64] = base;
-    for (uint32_t r = 0; r < kRecurrent; ++r) m->host_words[65 + r] = m->slot_host[r];
-    return hip_ok(hipMemcpyAsync(m->params, &m->host_words[64], (1 + kRecurrent) * sizeof(uint32_t),
+    uint32_t *p = m->host_params + (size_t)set * kParamWords;
+    p[0] = position;
+    for (uint32_t r = 0; r < kRecurrent; ++r) p[1 + r] = m->slot_host[r];
+}
+
+/* copy all staged parameter blocks to the device (ordered on the stream) */
+bool flush_params(Q38Model *m)
+{
+    return hip_ok(hipMemcpyAsync(m->params, m->host_params, (size_t)kParamSets * kParamWords * sizeof(uint32_t),
                                  hipMemcpyHostToDevice, m->stream),
-                  "parameter upload") &&
-           hip_ok(hipStreamSynchronize(m->stream), "parameter upload");
+                  "parameter upload");
 }
 
 /* after `rows` rows ran through recurrent layers 0..layers-1 */
@@ -661,9 +694,9 @@ void norm_hidden(Q38Model *m, const DevTensor &weight, uint32_t count, float *no
 }
 
 /* attention mixer of a full-attention layer over `count` rows at positions
- * base.. (q38_batch_full_attention, qwen38_model.c:1089-1119); input Q8_K rows
- * in m->q8k, output rows in m->branch */
-bool full_attention_rows(Q38Model *m, int layer, uint32_t count)
+ * params[0] + t (q38_batch_full_attention, qwen38_model.c:1089-1119); input
+ * Q8_K rows in m->q8k, output rows in m->branch */
+bool full_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count)
 {
     const Layer &L = m->layers[layer];
     const int full_index = layer / 4;
@@ -672,10 +705,10 @@ bool full_attention_rows(Q38Model *m, int layer, uint32_t count)
         return false;
     q38::launch_attention(m->attn, m->q8k, m->qbuf, m->wide0, m->kbuf, m->vbuf, L.q_norm.f32(), L.k_norm.f32(),
                           m->rope, m->key_cache + kv_off, m->value_cache + kv_off, m->scores, (int)m->context_length,
-                          m->params, (int)count, m->stream);
+                          s.params, (int)count, m->stream);
     if (count == 1 && trace_enabled()) {
         uint32_t pos = 0;
-        (void)hipMemcpy(&pos, m->params, 4, hipMemcpyDeviceToHost);
+        (void)hipMemcpy(&pos, s.params, 4, hipMemcpyDeviceToHost);
         trace(m, "Qcur_full-", layer, m->wide0, kQGDim);
         trace(m, "Kcur-", layer, m->key_cache + kv_off + (size_t)pos * kKVDim, kKVDim);
         trace(m, "Vcur-", layer, m->vbuf, kKVDim);
@@ -687,7 +720,7 @@ bool full_attention_rows(Q38Model *m, int layer, uint32_t count)
 }
 
 /* DeltaNet mixer (q38_batch_linear_attention, qwen38_model.c:1062-1087) */
-bool linear_attention_rows(Q38Model *m, int layer, uint32_t count)
+bool linear_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count)
 {
     const Layer &L = m->layers[layer];
     const int r = layer - (layer + 1) / 4;
@@ -705,14 +738,14 @@ bool linear_attention_rows(Q38Model *m, int layer, uint32_t count)
         float *qkv = m->wide0 + (size_t)t * kQKV, *attn = m->attn + (size_t)t * kLinV;
         float *beta = m->beta + (size_t)t * kVHeads, *alpha = m->alpha + (size_t)t * kVHeads;
         q38::launch_deltanet_prep(qkv, beta, alpha, m->conv_state + (size_t)r * kQKV * 3, (long long)conv_count(),
-                                  m->params + 1 + r, (int)t, L.conv.f32(), L.a.f32(), L.dt.f32(), m->stream);
+                                  s.params + 1 + r, (int)t, L.conv.f32(), L.a.f32(), L.dt.f32(), m->stream);
         if (tr) {
             trace(m, "dn_qkv-", layer, qkv, kQKV);
             trace(m, "dn_beta-", layer, beta, kVHeads);
             trace(m, "dn_alpha-", layer, alpha, kVHeads);
         }
         q38::launch_deltanet_state(attn, m->delta_state + (size_t)r * kVHeads * kHeadDim * kHeadDim,
-                                   (long long)delta_count(), m->params + 1 + r, (int)t, qkv, beta, alpha,
+                                   (long long)delta_count(), s.params + 1 + r, (int)t, qkv, beta, alpha,
                                    m->query_scale, m->stream);
         if (tr) trace(m, "dn_core-", layer, attn, kLinV);
     }
@@ -725,11 +758,11 @@ bool linear_attention_rows(Q38Model *m, int layer, uint32_t count)
  * (q38_layer_forward / q38_batch_layer, qwen38_model.c:955-984, 1121-1155).
  * The FFN's residual add is left pending in m->branch and fused into the
  * next RMSNorm. */
-bool layer_rows(Q38Model *m, int layer, uint32_t count)
+bool layer_rows(Q38Model *m, const Step &s, int layer, uint32_t count)
 {
     const Layer &L = m->layers[layer];
     norm_hidden(m, L.attn_norm, count);
-    if (!(L.full ? full_attention_rows(m, layer, count) : linear_attention_rows(m, layer, count))) return false;
+    if (!(L.full ? full_attention_rows(m, s, layer, count) : linear_attention_rows(m, s, layer, count))) return false;
     if (count == 1) trace(m, "attention_branch-", layer, m->branch, kHidden);
     m->pending_branch = true;
     norm_hidden(m, L.post_norm, count);
@@ -746,56 +779,36 @@ bool layer_rows(Q38Model *m, int layer, uint32_t count)
     return true;
 }
 
-/* Target model over `count` (<= kBatch) tokens already in m->tokens at
- * positions base..base+count-1: all 64 blocks, the output norm into
- * m->target_norm and, if `logit_rows`, the LM head of the last `logit_rows`
- * rows into m->logits (q38_batch_target_eval, qwen38_model.c:1241-1266). */
-bool target_rows(Q38Model *m, uint32_t count, uint32_t base, uint32_t logit_rows)
+/* Target model over `count` (<= kBatch) tokens at positions params[0] + t:
+ * all 64 blocks, the output norm into m->target_norm and, if `logit_rows`,
+ * the LM head of the last `logit_rows` rows into m->logits
+ * (q38_batch_target_eval, qwen38_model.c:1241-1266).  Enqueue only: the
+ * caller advances the host-side state (slots, position). */
+bool target_rows(Q38Model *m, const Step &s, uint32_t count, uint32_t logit_rows)
 {
-    if (!set_positions(m, base)) return false;
-    q38::launch_embed_q4k(m->hidden, m->embedding.data, m->tokens, (int)count, kHidden, kVocab, m->stream);
+    q38::launch_embed_q4k(m->hidden, m->embedding.data, s.tokens, (int)count, kHidden, kVocab, m->stream);
     m->pending_branch = false;
     if (count == 1) trace(m, "model.input_embed", -1, m->hidden, kHidden);
     for (uint32_t layer = 0; layer < kLayers; ++layer)
-        if (!layer_rows(m, (int)layer, count)) return false;
+        if (!layer_rows(m, s, (int)layer, count)) return false;
     norm_hidden(m, m->output_norm, count, m->target_norm);
     if (logit_rows && !gemm_q(m, m->output, logit_rows, m->logits, (size_t)(count - logit_rows) * (kHidden / 256)))
         return false;
-    advance_slots(m, count);
     return true;
 }
 
-bool upload_tokens(Q38Model *m, const uint32_t *tokens, uint32_t count)
-{
-    for (uint32_t i = 0; i < count; ++i) {
-        if (tokens[i] >= kVocab) return report("token id out of range");
-        m->host_words[i] = tokens[i];
-    }
-    return hip_ok(hipMemcpyAsync(m->tokens, m->host_words, count * sizeof(uint32_t), hipMemcpyHostToDevice,
-                                 m->stream),
-                  "token upload");
-}
-
-bool logits_to_host(Q38Model *m, const float *device_row)
-{
-    return hip_ok(hipMemcpyAsync(m->host_logits, device_row, kVocab * sizeof(float), hipMemcpyDeviceToHost,
-                                 m->stream),
-                  "logits download") &&
-           hip_ok(hipStreamSynchronize(m->stream), "logits download");
-}
-
-/* KV-cache rows of the MTP block for the tokens in m->tokens: eh_proj over
- * [enorm(embedding) | hnorm(previous hidden)], attn_norm, K and V projections
- * and the k-norm / RoPE / cache write at positions base.. (q38_mtp_catchup,
- * qwen38_model.c:1268-1294).  The rest of the reference's catch-up block
+/* KV-cache rows of the MTP block for `count` tokens at positions
+ * params[0] + t: eh_proj over [enorm(embedding) | hnorm(previous hidden)],
+ * attn_norm, K and V projections and the k-norm / RoPE / cache write
+ * (q38_mtp_catchup, qwen38_model.c:1268-1294), then the MTP hidden becomes
+ * target_norm[count - 1].  The rest of the reference's catch-up block
  * (queries, attention output, FFN) is computed there and never read, so it
- * is not computed here. */
-bool mtp_catchup(Q38Model *m, uint32_t count, uint32_t base)
+ * is not computed here.  Enqueue only. */
+bool mtp_catchup(Q38Model *m, const Step &s, uint32_t count)
 {
     const Layer &L = m->layers[kLayers];
     constexpr int kHB = kHidden / 256;   /* Q8_K blocks per hidden row */
-    if (!set_positions(m, base)) return false;
-    q38::launch_embed_q4k(m->hidden, m->mtp_embedding.data, m->tokens, (int)count, kHidden, kVocab, m->stream);
+    q38::launch_embed_q4k(m->hidden, m->mtp_embedding.data, s.tokens, (int)count, kHidden, kVocab, m->stream);
     /* Q8_K rows of 2*kHidden: [enorm(e_t) | hnorm(prev_t)], prev_0 = MTP hidden,
      * prev_t = target_norm[t-1] */
     q38::launch_norm_quant(nullptr, 0, m->q8k, 2 * kHB, m->hidden, kHidden, nullptr, m->enorm.f32(), (int)count,
@@ -811,35 +824,86 @@ bool mtp_catchup(Q38Model *m, uint32_t count, uint32_t base)
     if (!gemm_q(m, L.k, count, m->kbuf) || !gemm_q(m, L.v, count, m->vbuf)) return false;
     const size_t kv_off = (size_t)(kLayers / 4) * m->context_length * kKVDim;
     q38::launch_kv_write(m->kbuf, m->vbuf, L.k_norm.f32(), m->rope, m->key_cache + kv_off, m->value_cache + kv_off,
-                         m->params, (int)count, m->stream);
-    if (!hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm + (size_t)(count - 1) * kHidden,
-                               kHidden * sizeof(float), hipMemcpyDeviceToDevice, m->stream),
-                "mtp hidden"))
-        return false;
-    m->mtp_position = base + count;
-    return true;
+                         s.params, (int)count, m->stream);
+    return hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm + (size_t)(count - 1) * kHidden,
+                                 kHidden * sizeof(float), hipMemcpyDeviceToDevice, m->stream),
+                  "mtp hidden");
 }
 
-/* one MTP draft step for the token in m->tokens[0] (q38_model_mtp_forward,
- * qwen38_model.c:1588-1612; the block is q38_mtp_layer_forward :932-953) */
-bool mtp_step(Q38Model *m)
+/* one MTP draft step for token s.tokens[0] at position params[0]
+ * (q38_model_mtp_forward, qwen38_model.c:1588-1612; the block is
+ * q38_mtp_layer_forward :932-953): logits into m->logits, MTP hidden updated.
+ * Enqueue only. */
+bool mtp_step(Q38Model *m, const Step &s)
 {
     constexpr int kHB = kHidden / 256;
-    if (!set_positions(m, m->mtp_position)) return false;
-    q38::launch_embed_q4k(m->hidden, m->mtp_embedding.data, m->tokens, 1, kHidden, kVocab, m->stream);
+    q38::launch_embed_q4k(m->hidden, m->mtp_embedding.data, s.tokens, 1, kHidden, kVocab, m->stream);
     q38::launch_norm_quant(nullptr, 0, m->q8k, 2 * kHB, m->hidden, kHidden, nullptr, m->enorm.f32(), 1, m->stream);
     q38::launch_norm_quant(nullptr, 0, m->q8k + kHB * kQ8KBytes, 2 * kHB, m->mtp_hidden, kHidden, nullptr,
                            m->hnorm.f32(), 1, m->stream);
     if (!gemm_q(m, m->eh_proj, 1, m->hidden)) return false;
     m->pending_branch = false;
-    if (!layer_rows(m, (int)kLayers, 1)) return false;
+    if (!layer_rows(m, s, (int)kLayers, 1)) return false;
     /* mtp hidden = shared_head_norm(hidden + branch), and its Q8_K rows */
     q38::launch_norm_quant(m->mtp_hidden, kHidden, m->q8k, kHB, m->hidden, kHidden,
                            m->pending_branch ? m->branch : nullptr, m->shared_head_norm.f32(), 1, m->stream);
     m->pending_branch = false;
-    if (!gemm_q(m, m->mtp_output, 1, m->logits)) return false;
-    ++m->mtp_position;
-    return true;
+    return gemm_q(m, m->mtp_output, 1, m->logits);
+}
+
+/* ---- graphs ------------------------------------------------------------------ */
+
+enum : uint32_t { kGraphTarget = 1, kGraphVerify = 2, kGraphDraft = 3, kGraphCatchup = 4 };
+
+uint64_t graph_key(uint32_t kind, uint32_t a, uint32_t b = 0) { return ((uint64_t)kind << 32) | (a << 16) | b; }
+
+/* Run the enqueue-only sequence `body` on the model's stream: the first
+ * time eagerly, from the second time on as a HIP graph captured then and
+ * replayed afterwards (the parameter blocks and token ids it reads are in
+ * device memory, so one graph serves every position).  Graphs are off while
+ * tracing or when QWEN38_NO_GRAPHS is set. */
+template <typename Body>
+bool run_step(Q38Model *m, uint64_t key, Body body)
+{
+    if (!m->graphs_enabled || trace_enabled()) return body();
+    auto it = m->graphs.find(key);
+    if (it != m->graphs.end()) return hip_ok(hipGraphLaunch(it->second, m->stream), "graph launch");
+    if (!m->seen[key]) {
+        m->seen[key] = true;
+        return body();
+    }
+    hipGraph_t graph = nullptr;
+    if (!hip_ok(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal), "graph capture")) return false;
+    const bool ok = body();
+    const bool ended = hip_ok(hipStreamEndCapture(m->stream, &graph), "graph capture");
+    if (!ok || !ended) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return false;
+    }
+    hipGraphExec_t exec = nullptr;
+    const bool inst = hip_ok(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "graph instantiate");
+    (void)hipGraphDestroy(graph);
+    if (!inst) return false;
+    m->graphs[key] = exec;
+    return hip_ok(hipGraphLaunch(exec, m->stream), "graph launch");
+}
+
+bool upload_tokens(Q38Model *m, const uint32_t *tokens, uint32_t count, uint32_t *device)
+{
+    for (uint32_t i = 0; i < count; ++i) {
+        if (tokens[i] >= kVocab) return report("token id out of range");
+        m->host_words[i] = tokens[i];
+    }
+    return hip_ok(hipMemcpyAsync(device, m->host_words, count * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream),
+                  "token upload");
+}
+
+bool logits_to_host(Q38Model *m, const float *device_row)
+{
+    return hip_ok(hipMemcpyAsync(m->host_logits, device_row, kVocab * sizeof(float), hipMemcpyDeviceToHost,
+                                 m->stream),
+                  "logits download") &&
+           hip_ok(hipStreamSynchronize(m->stream), "logits download");
 }
 
 /* q38_checkpoint_state (qwen38_model.c:1200-1210): the recurrent state is
@@ -898,6 +962,7 @@ Q38Model *q38_model_open_gguf(const char *path, uint32_t context_length)
         ok = bind_mtp(m, m->gguf, base);
     ok = ok && allocate_state(m) && clear_state(m);
     if (ok && !q38::configure_attention((int)context_length)) ok = report("attention kernel configuration failed");
+    if (const char *v = getenv("QWEN38_NO_GRAPHS")) m->graphs_enabled = !(v[0] && strcmp(v, "0") != 0);
     if (!ok) {
         release(m);
         return nullptr;
@@ -937,12 +1002,19 @@ void q38_model_reset(Q38Model *m)
 int q38_model_forward_token(Q38Model *m, uint32_t token, const float **logits)
 {
     if (!m || !logits || token >= kVocab || m->position >= m->context_length) return 0;
-    if (!upload_tokens(m, &token, 1) || !target_rows(m, 1, m->position, 1)) return 0;
-    if (m->mtp_enabled &&
-        !hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm, kHidden * sizeof(float), hipMemcpyDeviceToDevice,
-                               m->stream), "mtp hidden"))
-        return 0;
-    if (!logits_to_host(m, m->logits)) return 0;
+    write_params(m, kParamTarget, m->position);
+    if (!upload_tokens(m, &token, 1, m->tokens) || !flush_params(m)) return 0;
+    const Step s = step_of(m, kParamTarget, m->tokens);
+    const bool mtp = m->mtp_enabled;
+    const bool ok = run_step(m, graph_key(kGraphTarget, 1, mtp), [&] {
+        /* q38_model_forward_token (qwen38_model.c:1494-1517): the normed final
+         * hidden becomes the MTP input when MTP is enabled */
+        return target_rows(m, s, 1, 1) &&
+               (!mtp || hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm, kHidden * sizeof(float),
+                                              hipMemcpyDeviceToDevice, m->stream), "mtp hidden"));
+    });
+    if (!ok || !logits_to_host(m, m->logits)) return 0;
+    advance_slots(m, 1);
     ++m->position;
     *logits = m->host_logits;
     return 1;
@@ -951,18 +1023,20 @@ int q38_model_forward_token(Q38Model *m, uint32_t token, const float **logits)
 int q38_model_forward_token_layers(Q38Model *m, uint32_t token, uint32_t layer_count, float *hidden_out)
 {
     if (!m || !hidden_out || token >= kVocab || layer_count > kLayers || m->position >= m->context_length) return 0;
-    if (!upload_tokens(m, &token, 1) || !set_positions(m, m->position)) return 0;
-    q38::launch_embed_q4k(m->hidden, m->embedding.data, m->tokens, 1, kHidden, kVocab, m->stream);
+    write_params(m, kParamTarget, m->position);
+    if (!upload_tokens(m, &token, 1, m->tokens) || !flush_params(m)) return 0;
+    const Step s = step_of(m, kParamTarget, m->tokens);
+    q38::launch_embed_q4k(m->hidden, m->embedding.data, s.tokens, 1, kHidden, kVocab, m->stream);
     trace(m, "model.input_embed", -1, m->hidden, kHidden);
     m->pending_branch = false;
     for (uint32_t layer = 0; layer < layer_count; ++layer)
-        if (!layer_rows(m, (int)layer, 1)) return 0;
+        if (!layer_rows(m, s, (int)layer, 1)) return 0;
     flush_branch(m, 1);
-    advance_slots(m, 1, layer_count);
     if (!hip_ok(hipMemcpyAsync(hidden_out, m->hidden, kHidden * sizeof(float), hipMemcpyDeviceToHost, m->stream),
                 "hidden download") ||
         !hip_ok(hipStreamSynchronize(m->stream), "hidden download"))
         return 0;
+    advance_slots(m, 1, layer_count);
     ++m->position;
     return 1;
 }
@@ -973,13 +1047,22 @@ int q38_model_prefill(Q38Model *m, const uint32_t *tokens, uint32_t count, const
     for (uint32_t i = 0; i < count; ++i)
         if (tokens[i] >= kVocab) return 0;
     const uint32_t base = m->position;
-    /* chunks of kBatch tokens through all blocks: every row's arithmetic is
-     * independent of the chunking, and state advances in token order */
+    /* chunks of kBatch tokens through all blocks (q38_model_prefill,
+     * qwen38_model.c:1519-1560): every row's arithmetic is independent of
+     * the chunking, and state advances in token order */
     for (uint32_t done = 0; done < count; done += kBatch) {
         const uint32_t n = std::min(kBatch, count - done);
         const bool last = done + n == count;
-        if (!upload_tokens(m, tokens + done, n) || !target_rows(m, n, base + done, last ? 1 : 0)) return 0;
-        if (m->mtp_enabled && !mtp_catchup(m, n, base + done)) return 0;
+        write_params(m, kParamTarget, base + done);
+        write_params(m, kParamCatchup, base + done);
+        if (!upload_tokens(m, tokens + done, n, m->tokens) || !flush_params(m)) return 0;
+        const Step st = step_of(m, kParamTarget, m->tokens);
+        if (!target_rows(m, st, n, last ? 1 : 0)) return 0;
+        if (m->mtp_enabled && !mtp_catchup(m, step_of(m, kParamCatchup, m->tokens), n)) return 0;
+        /* the pinned staging is rewritten by the next chunk */
+        if (!hip_ok(hipStreamSynchronize(m->stream), "prefill")) return 0;
+        advance_slots(m, n);
+        if (m->mtp_enabled) m->mtp_position = base + done + n;
     }
     if (!logits_to_host(m, m->logits)) return 0;
     m->position = base + count;
@@ -1002,11 +1085,28 @@ int q38_model_enable_mtp(Q38Model *m)
 int q38_model_mtp_forward(Q38Model *m, uint32_t token, const float **logits)
 {
     if (!m || !m->mtp_enabled || !logits || token >= kVocab || m->mtp_position >= m->context_length) return 0;
-    if (!upload_tokens(m, &token, 1) || !mtp_step(m) || !logits_to_host(m, m->logits)) return 0;
+    write_params(m, kParamDraft0, m->mtp_position);
+    if (!upload_tokens(m, &token, 1, m->drafts) || !flush_params(m)) return 0;
+    const Step s = step_of(m, kParamDraft0, m->drafts);
+    if (!run_step(m, graph_key(kGraphDraft, 0, 1), [&] { return mtp_step(m, s); }) ||
+        !logits_to_host(m, m->logits))
+        return 0;
+    ++m->mtp_position;
     *logits = m->host_logits;
     return 1;
 }
 
+/* q38_model_speculative_greedy (qwen38_model.c:1614-1714).
+ *
+ * Device-side chain: m->drafts[0] = token; MTP step i embeds m->drafts[i]
+ * and its argmax becomes m->drafts[i + 1], so the verify rows
+ * [token, d0 .. d_{n-2}] are m->drafts[0 .. n) without a round trip.  All
+ * `draft_count` drafts run; if one equals stop_token the reference stops
+ * there (n = its index + 1), and the extra drafts only wrote MTP cache
+ * entries beyond the positions catch-up rewrites, which are overwritten
+ * before they are read.  The verify batch runs over all drafts too; the
+ * acceptance is decided over its first n rows exactly as the reference
+ * does over its n (rows are independent, row t only sees rows < t). */
 int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_token, uint32_t draft_count,
                                  uint32_t *accepted_tokens, uint32_t *accepted_count, const float **next_logits)
 {
@@ -1014,49 +1114,64 @@ int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_toke
         draft_count == 0 || m->position != m->mtp_position || draft_count > m->context_length - m->position)
         return 0;
     if (draft_count > kBatch) return report("draft_count above 8 is not supported"), 0;
+    const uint32_t k = draft_count;
     if (!checkpoint(m)) return 0;
+    for (uint32_t i = 0; i < k; ++i) write_params(m, kParamDraft0 + i, m->ck_mtp_position + i);
+    write_params(m, kParamTarget, m->ck_position);
+    if (!upload_tokens(m, &token, 1, m->drafts) || !flush_params(m)) return 0;
 
-    /* drafts: chained MTP steps, argmax on the device (qwen38_model.c:1638-1648) */
-    uint32_t drafts[kBatch];
-    uint32_t n = 0, input = token;
     bool ok = true;
-    while (ok && n < draft_count) {
-        if (m->mtp_position >= m->context_length) { ok = false; break; }
-        ok = upload_tokens(m, &input, 1) && mtp_step(m);
-        if (!ok) break;
-        q38::launch_argmax(m->logits, kVocab, 1, m->argmax_pv, m->argmax_pi, m->drafts + n, m->stream);
-        ok = hip_ok(hipMemcpyAsync(&m->host_words[40], m->drafts + n, 4, hipMemcpyDeviceToHost, m->stream), "draft") &&
-             hip_ok(hipStreamSynchronize(m->stream), "draft");
-        if (!ok) break;
-        input = m->host_words[40];
-        drafts[n++] = input;
-        if (input == stop_token) break;
+    for (uint32_t i = 0; ok && i < k; ++i) {
+        const Step s = step_of(m, kParamDraft0 + i, m->drafts + i);
+        ok = run_step(m, graph_key(kGraphDraft, i, 0), [&] {
+            if (!mtp_step(m, s)) return false;
+            q38::launch_argmax(m->logits, kVocab, 1, m->argmax_pv, m->argmax_pi, m->drafts + i + 1, m->stream);
+            return true;
+        });
     }
+    /* verify rows m->drafts[0 .. k), per-row argmax into m->targets and the
+     * device acceptance over all k rows */
+    const Step sv = step_of(m, kParamTarget, m->drafts);
+    ok = ok && run_step(m, graph_key(kGraphVerify, k), [&] {
+        if (!target_rows(m, sv, k, k)) return false;
+        q38::launch_argmax(m->logits, kVocab, k, m->argmax_pv, m->argmax_pi, m->targets, m->stream);
+        q38::launch_accept(m->accept, m->targets, m->drafts + 1, k, m->stream);
+        return true;
+    });
+    uint32_t *hw = m->host_words;   /* [64..) drafts, [80..) targets, [96..) acceptance */
+    ok = ok &&
+         hip_ok(hipMemcpyAsync(hw + 64, m->drafts + 1, k * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream),
+                "drafts") &&
+         hip_ok(hipMemcpyAsync(hw + 80, m->targets, k * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream),
+                "targets") &&
+         hip_ok(hipMemcpyAsync(hw + 96, m->accept, (k + 3) * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream),
+                "acceptance") &&
+         hip_ok(hipStreamSynchronize(m->stream), "acceptance");
     if (!ok) {
+        restore_target(m);
         (void)restore_mtp(m);
+        (void)hipStreamSynchronize(m->stream);
         return 0;
     }
-
-    /* verify rows [token, d0 .. d_{n-2}] in one batch, argmax per row and
-     * greedy acceptance on the device (qwen38_model.c:1655-1682) */
-    uint32_t inputs[kBatch];
-    inputs[0] = token;
-    for (uint32_t i = 1; i < n; ++i) inputs[i] = drafts[i - 1];
-    ok = upload_tokens(m, inputs, n) && target_rows(m, n, m->position, n);
-    if (ok) {
-        m->position = m->ck_position + n;
-        q38::launch_argmax(m->logits, kVocab, n, m->argmax_pv, m->argmax_pi, m->targets, m->stream);
-        q38::launch_accept(m->accept, m->targets, m->drafts, n, m->stream);
-        ok = hip_ok(hipMemcpyAsync(&m->host_words[44], m->accept, (n + 3) * sizeof(uint32_t), hipMemcpyDeviceToHost,
-                                   m->stream), "acceptance") &&
-             hip_ok(hipStreamSynchronize(m->stream), "acceptance");
-    }
-    uint32_t consumed = 0, matched = 0;
+    const uint32_t *drafts = hw + 64, *targets = hw + 80;
+    uint32_t n = k;
+    for (uint32_t i = 0; i < k; ++i)
+        if (drafts[i] == stop_token) { n = i + 1; break; }
+    uint32_t matched, consumed;
     uint32_t accepted[kBatch];
-    if (ok) {
-        consumed = m->host_words[44];
-        matched = m->host_words[45];
-        for (uint32_t i = 0; i < consumed; ++i) accepted[i] = m->host_words[47 + i];
+    if (n == k) {
+        consumed = hw[96];
+        matched = hw[97];
+        for (uint32_t i = 0; i < consumed; ++i) accepted[i] = hw[99 + i];
+    } else {
+        /* the reference's loop over its n rows (qwen38_model.c:1665-1682) */
+        matched = 0;
+        uint32_t next = 0;
+        while (matched < n && targets[matched] == drafts[matched]) ++matched;
+        if (matched < n) next = targets[matched];
+        consumed = matched < n ? matched + 1 : n;
+        for (uint32_t i = 0; i < matched; ++i) accepted[i] = drafts[i];
+        if (matched < n) accepted[matched] = next;
     }
     /* On a rejection the reference restores its checkpoint and replays the
      * consumed rows (qwen38_model.c:1684-1691).  Every row of the verify
@@ -1066,20 +1181,21 @@ int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_toke
      * K/V entries are in the caches, and the last consumed row's logits are
      * row consumed - 1 of the batch; entries of the rejected rows are never
      * read before being overwritten. */
-    const float *last_row = m->logits + (size_t)(consumed ? consumed - 1 : 0) * kVocab;
-    if (ok) restore_target(m, consumed);
-    if (ok) {
-        ok = logits_to_host(m, last_row) && restore_mtp(m) && upload_tokens(m, inputs, consumed) &&
-             mtp_catchup(m, consumed, m->ck_mtp_position);
-        ok = ok && hip_ok(hipStreamSynchronize(m->stream), "catch-up");
-    }
+    restore_target(m, consumed);
+    (void)restore_mtp(m);
+    write_params(m, kParamCatchup, m->ck_mtp_position);
+    const Step sc = step_of(m, kParamCatchup, m->drafts);
+    ok = hip_ok(hipMemcpyAsync(m->host_logits, m->logits + (size_t)(consumed - 1) * kVocab, kVocab * sizeof(float),
+                               hipMemcpyDeviceToHost, m->stream), "logits download") &&
+         flush_params(m) && run_step(m, graph_key(kGraphCatchup, consumed), [&] { return mtp_catchup(m, sc, consumed); }) &&
+         hip_ok(hipStreamSynchronize(m->stream), "catch-up");
     if (!ok) {
         restore_target(m);
         (void)restore_mtp(m);
         (void)hipStreamSynchronize(m->stream);
         return 0;
     }
-    (void)matched;
+    m->mtp_position = m->ck_mtp_position + consumed;
     for (uint32_t i = 0; i < consumed; ++i) accepted_tokens[i] = accepted[i];
     *accepted_count = consumed;
     *next_logits = m->host_logits;

@@ -836,10 +836,14 @@ static void launch_m(int m, const uint8_t *w, const uint8_t *x, float *y, uint32
 /* Enqueue y[t * rows + row] = W_row . x_t for t < m (all device pointers).
  * x is m * nblk Q8_K blocks, token-major.  grid is the IQ1_M codebook as
  * 2048 x 8 int8 (unused for the other types). */
+bool launch_gemv_lanes(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, uint32_t nb,
+                       hipStream_t stream);
+
 bool launch_gemm(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows,
                  uint32_t nblk, const void *grid, hipStream_t stream)
 {
     if (m < 1 || m > 8) return false;
+    if (launch_gemv_lanes(type, m, w, x, y, rows, nblk, stream)) return true;
     const uint2 *g = static_cast<const uint2 *>(grid);
     switch (type) {
     case kQ4K: launch_m<kQ4K>(m, w, x, y, rows, nblk, g, stream); return true;
