@@ -20,6 +20,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
+#include <initializer_list>
 #include <string>
 #include <map>
 #include <unordered_map>
@@ -103,6 +105,7 @@ struct TensorInfo {
     uint32_t type = 0;
     uint64_t offset = 0;
     uint64_t nbytes = 0;
+    uint64_t device_offset = 0;   /* placement in the HBM copy (plan_layout) */
 };
 
 struct MetaValue {
@@ -117,6 +120,7 @@ struct GGUFFile {
     uint64_t size = 0;
     uint64_t data_offset = 0;
     uint64_t data_bytes = 0;
+    uint64_t device_bytes = 0;   /* size of the HBM copy (plan_layout) */
     std::unordered_map<std::string, TensorInfo> tensors;
     std::unordered_map<std::string, MetaValue> meta;
 
@@ -283,12 +287,36 @@ struct DevTensor {
     const float *f32() const { return reinterpret_cast<const float *>(data); }
 };
 
+/* Projections of one input whose output rows are concatenated: row t of
+ * the result holds member i at columns first[i] .. first[i] + rows - 1, and
+ * rows are `width` floats apart.  Runs of members that sit back to back in
+ * HBM with one type and row width are computed by one GEMM. */
+struct Group {
+    DevTensor part[4];
+    uint32_t first[4] = {0};
+    int n = 0;
+    uint32_t width = 0;
+};
+
 struct Layer {
     bool full = false;
     DevTensor attn_norm, post_norm, ffn_gate, ffn_up, ffn_down;
     DevTensor qkv, z, alpha, beta, conv, dt, a, ssm_norm, ssm_out;   /* DeltaNet */
     DevTensor q, k, v, out, q_norm, k_norm;                          /* full attention */
+    Group ffn_in;   /* gate | up */
+    Group mix_in;   /* DeltaNet: qkv | z | beta | alpha; full attention: q+gate | k | v */
 };
+
+void make_group(Group *g, std::initializer_list<const DevTensor *> parts)
+{
+    g->n = 0;
+    g->width = 0;
+    for (const DevTensor *t : parts) {
+        g->part[g->n] = *t;
+        g->first[g->n++] = g->width;
+        g->width += (uint32_t)t->rows;
+    }
+}
 
 bool matrix_type_ok(uint32_t t) { return t == Q4_K || t == Q6_K || t == IQ1_M; }
 
@@ -314,8 +342,9 @@ struct Q38Model {
     uint32_t slot_host[kRecurrent] = {0}, ck_slot[kRecurrent] = {0};
     float *rope = nullptr;
     /* scratch, kBatch rows */
-    float *hidden = nullptr, *norm = nullptr, *branch = nullptr, *wide0 = nullptr, *wide1 = nullptr;
-    float *kbuf = nullptr, *vbuf = nullptr, *qbuf = nullptr, *attn = nullptr, *beta = nullptr, *alpha = nullptr;
+    /* wide0 holds a group's concatenated outputs: up to 2 * kFFN floats per row */
+    float *hidden = nullptr, *norm = nullptr, *branch = nullptr, *wide0 = nullptr;
+    float *qbuf = nullptr, *attn = nullptr;
     float *scores = nullptr, *logits = nullptr, *target_norm = nullptr;
     uint8_t *q8k = nullptr;
     /* params[0] = position of row 0 of the current step, params[1 + r] = slot of recurrent layer r */
@@ -349,7 +378,7 @@ bool bind_tensor(const GGUFFile &f, const uint8_t *base, const std::string &name
     out->n_dims = t.n_dims;
     out->width = t.shape[0];
     out->rows = t.n_dims > 1 ? t.shape[1] : 0;
-    out->data = base + t.offset;
+    out->data = base + t.device_offset;
     return true;
 }
 
@@ -410,14 +439,74 @@ bool bind_layer(Layer *L, const GGUFFile &f, const uint8_t *base, int layer)
               (int)expect(L->ssm_norm, p + "ssm_norm.weight", kHeadDim, 0, true) &
               (int)expect(L->ssm_out, p + "ssm_out.weight", kLinV, kHidden, false);
     }
+    make_group(&L->ffn_in, {&L->ffn_gate, &L->ffn_up});
+    if (L->full) make_group(&L->mix_in, {&L->q, &L->k, &L->v});
+    else make_group(&L->mix_in, {&L->qkv, &L->z, &L->beta, &L->alpha});
     return ok;
 }
 
-/* Copy the whole tensor-data region of a GGUF file to one HBM allocation
- * through two pinned staging buffers. */
-bool upload(const GGUFFile &f, void **device)
+/* Projections that read the same input.  Their tensors are placed back to
+ * back in HBM, so members of one type and width form a single matrix whose
+ * output rows are the members' rows in this order. */
+const char *const kFusionGroups[][4] = {
+    {"ffn_gate.weight", "ffn_up.weight", nullptr, nullptr},
+    {"attn_qkv.weight", "attn_gate.weight", "ssm_beta.weight", "ssm_alpha.weight"},
+    {"attn_q.weight", "attn_k.weight", "attn_v.weight", nullptr},
+};
+
+uint64_t align256(uint64_t v) { return (v + 255) & ~(uint64_t)255; }
+
+/* Device placement of every tensor: the fusion groups of each block first
+ * (a member directly after the previous one when both have the same type and
+ * row width, else 256-byte aligned), then all other tensors 256-byte aligned
+ * in file order. */
+void plan_layout(GGUFFile &f)
 {
-    if (!hip_ok(hipMalloc(device, f.data_bytes ? f.data_bytes : 1), "weight allocation")) return false;
+    uint64_t at = 0;
+    std::map<std::string, bool> placed;
+    for (uint32_t layer = 0; layer < kTotalLayers; ++layer) {
+        const std::string p = "blk." + std::to_string(layer) + ".";
+        for (const auto &group : kFusionGroups) {
+            const TensorInfo *prev = nullptr;
+            for (const char *member : group) {
+                if (!member) break;
+                auto it = f.tensors.find(p + member);
+                if (it == f.tensors.end()) continue;
+                TensorInfo &t = it->second;
+                if (!prev || prev->type != t.type || prev->shape[0] != t.shape[0]) at = align256(at);
+                t.device_offset = at;
+                at += t.nbytes;
+                placed[it->first] = true;
+                prev = &t;
+            }
+        }
+    }
+    std::vector<std::pair<uint64_t, TensorInfo *>> rest;
+    for (auto &kv : f.tensors)
+        if (!placed.count(kv.first)) rest.emplace_back(kv.second.offset, &kv.second);
+    std::sort(rest.begin(), rest.end(),
+              [](const std::pair<uint64_t, TensorInfo *> &a, const std::pair<uint64_t, TensorInfo *> &b) {
+                  return a.first < b.first;
+              });
+    for (auto &r : rest) {
+        at = align256(at);
+        r.second->device_offset = at;
+        at += r.second->nbytes;
+    }
+    f.device_bytes = at;
+}
+
+/* Read the tensor-data region of a GGUF file sequentially through two pinned
+ * staging buffers and copy each tensor's bytes to its planned place in one
+ * HBM allocation. */
+bool upload(GGUFFile &f, void **device)
+{
+    plan_layout(f);
+    if (!hip_ok(hipMalloc(device, f.device_bytes ? f.device_bytes : 1), "weight allocation")) return false;
+    std::vector<const TensorInfo *> order;
+    for (const auto &kv : f.tensors) order.push_back(&kv.second);
+    std::sort(order.begin(), order.end(),
+              [](const TensorInfo *a, const TensorInfo *b) { return a->offset < b->offset; });
     const size_t chunk = 256u << 20;
     void *stage[2] = {nullptr, nullptr};
     hipEvent_t done[2] = {nullptr, nullptr};
@@ -426,6 +515,7 @@ bool upload(const GGUFFile &f, void **device)
               hip_ok(hipHostMalloc(&stage[1], chunk), "pinned staging") &&
               hip_ok(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "upload stream") &&
               hip_ok(hipEventCreate(&done[0]), "event") && hip_ok(hipEventCreate(&done[1]), "event");
+    size_t first = 0;   /* first tensor that may overlap the current chunk */
     uint64_t off = 0;
     for (int i = 0; ok && off < f.data_bytes; ++i, off += chunk) {
         const size_t n = (size_t)std::min<uint64_t>(chunk, f.data_bytes - off);
@@ -438,9 +528,17 @@ bool upload(const GGUFFile &f, void **device)
             if (r <= 0) ok = report("reading GGUF tensor data failed");
             else got += (uint64_t)r;
         }
-        ok = ok && hip_ok(hipMemcpyAsync(static_cast<uint8_t *>(*device) + off, stage[b], n,
-                                         hipMemcpyHostToDevice, s), "weight upload") &&
-             hip_ok(hipEventRecord(done[b], s), "event");
+        while (first < order.size() && order[first]->offset + order[first]->nbytes <= off) ++first;
+        for (size_t k = first; ok && k < order.size() && order[k]->offset < off + n; ++k) {
+            const TensorInfo &t = *order[k];
+            const uint64_t lo = std::max<uint64_t>(t.offset, off), hi = std::min<uint64_t>(t.offset + t.nbytes, off + n);
+            if (lo >= hi) continue;
+            ok = hip_ok(hipMemcpyAsync(static_cast<uint8_t *>(*device) + t.device_offset + (lo - t.offset),
+                                       static_cast<uint8_t *>(stage[b]) + (lo - off), hi - lo,
+                                       hipMemcpyHostToDevice, s),
+                        "weight upload");
+        }
+        ok = ok && hip_ok(hipEventRecord(done[b], s), "event");
     }
     if (s) ok = hip_ok(hipStreamSynchronize(s), "upload") && ok;
     for (int b = 0; b < 2; ++b) {
@@ -514,8 +612,8 @@ void release(Q38Model *m)
     if (m->stream) (void)hipStreamSynchronize(m->stream);
     float **fbufs[] = {&m->conv_state, &m->delta_state, &m->key_cache, &m->value_cache, &m->mtp_hidden,
                        &m->ck_mtp_hidden, &m->rope, &m->hidden, &m->norm,
-                       &m->branch, &m->wide0, &m->wide1, &m->kbuf, &m->vbuf, &m->qbuf, &m->attn, &m->beta,
-                       &m->alpha, &m->scores, &m->logits, &m->target_norm, &m->argmax_pv};
+                       &m->branch, &m->wide0, &m->qbuf, &m->attn, &m->scores, &m->logits, &m->target_norm,
+                       &m->argmax_pv};
     for (float **p : fbufs) dfree(*p);
     uint32_t **ubufs[] = {&m->tokens, &m->params, &m->targets, &m->drafts, &m->accept, &m->argmax_pi};
     for (uint32_t **p : ubufs) dfree(*p);
@@ -539,11 +637,9 @@ bool allocate_state(Q38Model *m)
               dalloc(&m->key_cache, kv_count(ctx)) && dalloc(&m->value_cache, kv_count(ctx)) &&
               dalloc(&m->mtp_hidden, kHidden) && dalloc(&m->rope, (size_t)ctx * 64) &&
               dalloc(&m->hidden, (size_t)B * kHidden) && dalloc(&m->norm, (size_t)B * 2 * kHidden) &&
-              dalloc(&m->branch, (size_t)B * kHidden) && dalloc(&m->wide0, (size_t)B * kFFN) &&
-              dalloc(&m->wide1, (size_t)B * kFFN) && dalloc(&m->kbuf, (size_t)B * kKVDim) &&
-              dalloc(&m->vbuf, (size_t)B * kKVDim) && dalloc(&m->qbuf, (size_t)B * kQDim) &&
-              dalloc(&m->attn, (size_t)B * kLinV) && dalloc(&m->beta, (size_t)B * kVHeads) &&
-              dalloc(&m->alpha, (size_t)B * kVHeads) && dalloc(&m->scores, (size_t)B * kAttnHeads * ctx) &&
+              dalloc(&m->branch, (size_t)B * kHidden) && dalloc(&m->wide0, (size_t)B * 2 * kFFN) &&
+              dalloc(&m->qbuf, (size_t)B * kQDim) && dalloc(&m->attn, (size_t)B * kLinV) &&
+              dalloc(&m->scores, (size_t)B * kAttnHeads * ctx) &&
               dalloc(&m->logits, (size_t)B * kVocab) && dalloc(&m->target_norm, (size_t)B * kHidden) &&
               dalloc(&m->q8k, (size_t)B * (kFFN / 256) * kQ8KBytes) && dalloc(&m->tokens, B) &&
               dalloc(&m->params, (size_t)kParamSets * kParamWords) && dalloc(&m->targets, B) &&
@@ -650,6 +746,34 @@ bool gemm_q(Q38Model *m, const DevTensor &w, uint32_t count, float *out, size_t 
     return true;
 }
 
+uint64_t row_bytes(const DevTensor &t)
+{
+    uint32_t e = 0, b = 0;
+    ggml_block(t.type, &e, &b);
+    return t.width / e * b;
+}
+
+/* members [lo, hi) of group g over `count` Q8_K rows in m->q8k; row t of
+ * member i lands at out + t * ldy + first[i] - first[lo] */
+bool gemm_group(Q38Model *m, const Group &g, int lo, int hi, uint32_t count, float *out, uint32_t ldy)
+{
+    for (int i = lo; i < hi;) {
+        const DevTensor &a = g.part[i];
+        uint64_t rows = a.rows;
+        int j = i + 1;
+        while (j < hi && g.part[j].type == a.type && g.part[j].width == a.width &&
+               g.part[j].data == a.data + rows * row_bytes(a)) {
+            rows += g.part[j].rows;
+            ++j;
+        }
+        if (!q38::launch_gemm_ld((int)a.type, (int)count, a.data, m->q8k, out + (g.first[i] - g.first[lo]), ldy,
+                                 (uint32_t)rows, (uint32_t)(a.width / 256), m->grid, m->stream))
+            return report("unsupported GEMM configuration");
+        i = j;
+    }
+    return true;
+}
+
 /* host staging of a parameter block: position of row 0 and the current
  * state slot of every recurrent layer */
 void write_params(Q38Model *m, uint32_t set, uint32_t position)
@@ -701,17 +825,18 @@ bool full_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count)
     const Layer &L = m->layers[layer];
     const int full_index = layer / 4;
     const size_t kv_off = (size_t)full_index * m->context_length * kKVDim;
-    if (!gemm_q(m, L.q, count, m->wide0) || !gemm_q(m, L.k, count, m->kbuf) || !gemm_q(m, L.v, count, m->vbuf))
-        return false;
-    q38::launch_attention(m->attn, m->q8k, m->qbuf, m->wide0, m->kbuf, m->vbuf, L.q_norm.f32(), L.k_norm.f32(),
-                          m->rope, m->key_cache + kv_off, m->value_cache + kv_off, m->scores, (int)m->context_length,
-                          s.params, (int)count, m->stream);
+    /* per row: q+gate [12288] | k [1024] | v [1024] */
+    const Group &g = L.mix_in;
+    if (!gemm_group(m, g, 0, 3, count, m->wide0, g.width)) return false;
+    q38::launch_attention(m->attn, m->q8k, m->qbuf, m->wide0, m->wide0 + g.first[1], m->wide0 + g.first[2], g.width,
+                          L.q_norm.f32(), L.k_norm.f32(), m->rope, m->key_cache + kv_off, m->value_cache + kv_off,
+                          m->scores, (int)m->context_length, s.params, (int)count, m->stream);
     if (count == 1 && trace_enabled()) {
         uint32_t pos = 0;
         (void)hipMemcpy(&pos, s.params, 4, hipMemcpyDeviceToHost);
         trace(m, "Qcur_full-", layer, m->wide0, kQGDim);
         trace(m, "Kcur-", layer, m->key_cache + kv_off + (size_t)pos * kKVDim, kKVDim);
-        trace(m, "Vcur-", layer, m->vbuf, kKVDim);
+        trace(m, "Vcur-", layer, m->wide0 + g.first[2], kKVDim);
         trace(m, "attn_gated-", layer, m->attn, kQDim);
     }
     if (!gemm_q(m, L.out, count, m->branch)) return false;
@@ -724,19 +849,20 @@ bool linear_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count
 {
     const Layer &L = m->layers[layer];
     const int r = layer - (layer + 1) / 4;
-    if (!gemm_q(m, L.qkv, count, m->wide0) || !gemm_q(m, L.z, count, m->wide1) ||
-        !gemm_q(m, L.beta, count, m->beta) || !gemm_q(m, L.alpha, count, m->alpha))
-        return false;
+    /* per row: qkv [10240] | z [6144] | beta [48] | alpha [48] */
+    const Group &g = L.mix_in;
+    const uint32_t ld = g.width;
+    if (!gemm_group(m, g, 0, 4, count, m->wide0, ld)) return false;
     const bool tr = count == 1 && trace_enabled();
     if (tr) {
         trace(m, "dn_qkv_proj-", layer, m->wide0, kQKV);
-        trace(m, "dn_z-", layer, m->wide1, kLinV);
-        trace(m, "dn_beta_proj-", layer, m->beta, kVHeads);
-        trace(m, "dn_alpha_proj-", layer, m->alpha, kVHeads);
+        trace(m, "dn_z-", layer, m->wide0 + g.first[1], kLinV);
+        trace(m, "dn_beta_proj-", layer, m->wide0 + g.first[2], kVHeads);
+        trace(m, "dn_alpha_proj-", layer, m->wide0 + g.first[3], kVHeads);
     }
     for (uint32_t t = 0; t < count; ++t) {
-        float *qkv = m->wide0 + (size_t)t * kQKV, *attn = m->attn + (size_t)t * kLinV;
-        float *beta = m->beta + (size_t)t * kVHeads, *alpha = m->alpha + (size_t)t * kVHeads;
+        float *qkv = m->wide0 + (size_t)t * ld, *attn = m->attn + (size_t)t * kLinV;
+        float *beta = qkv + g.first[2], *alpha = qkv + g.first[3];
         q38::launch_deltanet_prep(qkv, beta, alpha, m->conv_state + (size_t)r * kQKV * 3, (long long)conv_count(),
                                   s.params + 1 + r, (int)t, L.conv.f32(), L.a.f32(), L.dt.f32(), m->stream);
         if (tr) {
@@ -749,7 +875,8 @@ bool linear_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count
                                    m->query_scale, m->stream);
         if (tr) trace(m, "dn_core-", layer, attn, kLinV);
     }
-    q38::launch_deltanet_out_quant(m->attn, m->q8k, m->wide1, L.ssm_norm.f32(), (int)count, m->stream);
+    q38::launch_deltanet_out_quant(m->attn, m->q8k, m->wide0 + g.first[1], ld, L.ssm_norm.f32(), (int)count,
+                                   m->stream);
     if (tr) trace(m, "dn_gated-", layer, m->attn, kLinV);
     return gemm_q(m, L.ssm_out, count, m->branch);
 }
@@ -767,8 +894,9 @@ bool layer_rows(Q38Model *m, const Step &s, int layer, uint32_t count)
     m->pending_branch = true;
     norm_hidden(m, L.post_norm, count);
     if (count == 1) trace(m, "attn_residual-", layer, m->hidden, kHidden);
-    if (!gemm_q(m, L.ffn_gate, count, m->wide0) || !gemm_q(m, L.ffn_up, count, m->wide1)) return false;
-    q38::launch_swiglu_quant(m->q8k, m->wide0, m->wide1, (int)count, m->stream);
+    const Group &g = L.ffn_in;   /* per row: gate [17408] | up [17408] */
+    if (!gemm_group(m, g, 0, 2, count, m->wide0, g.width)) return false;
+    q38::launch_swiglu_quant(m->q8k, m->wide0, m->wide0 + g.first[1], g.width, (int)count, m->stream);
     if (!gemm_q(m, L.ffn_down, count, m->branch)) return false;
     m->pending_branch = true;
     if (count == 1 && trace_enabled()) {
@@ -821,10 +949,13 @@ bool mtp_catchup(Q38Model *m, const Step &s, uint32_t count)
     if (!gemm_q(m, m->eh_proj, count, m->hidden)) return false;
     m->pending_branch = false;
     norm_hidden(m, L.attn_norm, count);
-    if (!gemm_q(m, L.k, count, m->kbuf) || !gemm_q(m, L.v, count, m->vbuf)) return false;
+    /* k | v members of the block's q+gate | k | v group, rows 2048 apart */
+    const Group &g = L.mix_in;
+    const uint32_t ld = g.first[2] + (uint32_t)g.part[2].rows - g.first[1];
+    if (!gemm_group(m, g, 1, 3, count, m->wide0, ld)) return false;
     const size_t kv_off = (size_t)(kLayers / 4) * m->context_length * kKVDim;
-    q38::launch_kv_write(m->kbuf, m->vbuf, L.k_norm.f32(), m->rope, m->key_cache + kv_off, m->value_cache + kv_off,
-                         s.params, (int)count, m->stream);
+    q38::launch_kv_write(m->wide0, m->wide0 + (g.first[2] - g.first[1]), ld, L.k_norm.f32(), m->rope,
+                         m->key_cache + kv_off, m->value_cache + kv_off, s.params, (int)count, m->stream);
     return hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm + (size_t)(count - 1) * kHidden,
                                  kHidden * sizeof(float), hipMemcpyDeviceToDevice, m->stream),
                   "mtp hidden");

@@ -27,6 +27,7 @@
  * token counts whose activations exceed LDS).
  */
 #include "q38_device.h"
+#include "q38_kernels.h"
 
 #include <map>
 #include <mutex>
@@ -460,7 +461,7 @@ __device__ __forceinline__ float chain_tree(float acc)
 /* All (row, token) chains of a tile: groups of F::group lanes over nthreads
  * lanes (a multiple of 64; every lane must call this). */
 template <int TYPE, int MT>
-__device__ __forceinline__ void tile_chains(const int *res, float *y, uint32_t rows, uint32_t row0, int tile_rows,
+__device__ __forceinline__ void tile_chains(const int *res, float *y, uint32_t ldy, uint32_t row0, int tile_rows,
                                             int nb, int tid, int nthreads)
 {
     using F = Format<TYPE>;
@@ -472,7 +473,7 @@ __device__ __forceinline__ void tile_chains(const int *res, float *y, uint32_t r
         const bool active = g < groups && k < F::chains;
         const float acc = active ? chain<TYPE, MT>(res, rc, tc, k, nb) : 0.0f;
         const float out = chain_tree<TYPE>(acc);
-        if (active && k == 0) y[static_cast<size_t>(tc) * rows + row0 + rc] = out;
+        if (active && k == 0) y[static_cast<size_t>(tc) * ldy + row0 + rc] = out;
     }
 }
 
@@ -511,7 +512,7 @@ __device__ __forceinline__ void wait_vmcnt()
  * the whole tile. */
 template <int TYPE, int MT, int NR, int WAVES, int LW>
 __global__ __launch_bounds__(64 * WAVES) void gemm_q8k_ring(
-    const uint8_t *__restrict__ w, const uint8_t *__restrict__ x, float *__restrict__ y,
+    const uint8_t *__restrict__ w, const uint8_t *__restrict__ x, float *__restrict__ y, uint32_t ldy,
     uint32_t rows, uint32_t nblk, uint32_t rw, uint32_t ntiles, const uint2 *__restrict__ grid_src)
 {
     using F = Format<TYPE>;
@@ -576,7 +577,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_q8k_ring(
             block_ints<TYPE, MT>(raw, act, bl, nb, pair_out<TYPE, MT>(res, r, bl, nb), j, grid);
         }
         __syncthreads();
-        tile_chains<TYPE, MT>(res, y, rows, row0, tile_rows, nb, threadIdx.x, 64 * WAVES);
+        tile_chains<TYPE, MT>(res, y, ldy, row0, tile_rows, nb, threadIdx.x, 64 * WAVES);
         slot = (slot + 1) % NR;
     }
     /* no copy may still be in flight into LDS when the workgroup retires */
@@ -590,7 +591,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_q8k_ring(
  * p = quad + 16 i (i < P) cover rw * nblk (row, block) pairs. */
 template <int TYPE, int MT>
 __global__ __launch_bounds__(256) void gemm_q8k_stream(
-    const uint8_t *__restrict__ w, const uint8_t *__restrict__ x, float *__restrict__ y,
+    const uint8_t *__restrict__ w, const uint8_t *__restrict__ x, float *__restrict__ y, uint32_t ldy,
     uint32_t rows, uint32_t nblk, uint32_t rw, uint32_t ntiles, const uint2 *__restrict__ grid_src)
 {
     using F = Format<TYPE>;
@@ -646,7 +647,7 @@ __global__ __launch_bounds__(256) void gemm_q8k_stream(
         /* LDS traffic of one wavefront completes in issue order; the fence
          * keeps the compiler from moving the chain reads above the writes. */
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        tile_chains<TYPE, MT>(res, y, rows, row0, tile_rows, nb, lane, 64);
+        tile_chains<TYPE, MT>(res, y, ldy, row0, tile_rows, nb, lane, 64);
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     }
 }
@@ -655,7 +656,7 @@ __global__ __launch_bounds__(256) void gemm_q8k_stream(
 
 template <int TYPE, int MT>
 __global__ __launch_bounds__(256) void gemm_q8k_chunked(
-    const uint8_t *__restrict__ w, const uint8_t *__restrict__ x, float *__restrict__ y,
+    const uint8_t *__restrict__ w, const uint8_t *__restrict__ x, float *__restrict__ y, uint32_t ldy,
     uint32_t rows, uint32_t nblk, uint32_t rw, uint32_t ch, const uint2 *__restrict__ grid_src)
 {
     using F = Format<TYPE>;
@@ -704,7 +705,7 @@ __global__ __launch_bounds__(256) void gemm_q8k_chunked(
         }
     }
     const float out = chain_tree<TYPE>(acc);
-    if (active && k == 0) y[static_cast<size_t>(tc) * rows + row0 + rc] = out;
+    if (active && k == 0) y[static_cast<size_t>(tc) * ldy + row0 + rc] = out;
 }
 
 /* ---- launch policy ---------------------------------------------------------- */
@@ -744,7 +745,7 @@ static int occupancy(const void *kernel, int threads, size_t lds)
 }
 
 template <int TYPE, int MT, int NR, int WAVES, int LW>
-static bool try_ring(const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, uint32_t nblk,
+static bool try_ring(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, uint32_t nblk,
                      const uint2 *grid, hipStream_t stream)
 {
     using F = Format<TYPE>;
@@ -770,19 +771,19 @@ static bool try_ring(const uint8_t *w, const uint8_t *x, float *y, uint32_t rows
     uint32_t groups = (uint32_t)device_cus();
     if (groups > tiles) groups = tiles;
     hipLaunchKernelGGL((gemm_q8k_ring<TYPE, MT, NR, WAVES, LW>), dim3(groups), dim3(64 * WAVES), lds, stream,
-                       w, x, y, rows, nblk, rw, tiles, grid);
+                       w, x, y, ldy, rows, nblk, rw, tiles, grid);
     return true;
 }
 
 template <int TYPE, int MT>
-static void launch_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, uint32_t nblk,
+static void launch_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, uint32_t nblk,
                          const uint2 *grid, hipStream_t stream)
 {
     using F = Format<TYPE>;
     /* Long rows (down projections) stream best through the LDS ring; short
      * rows through per-wave register prefetch.  Q6_K blocks (210 bytes) do
      * not sit on 16-byte boundaries in the ring and always stream. */
-    if (TYPE != kQ6K && MT <= 2 && nblk >= 40 && try_ring<TYPE, MT, 3, 16, 2>(w, x, y, rows, nblk, grid, stream))
+    if (TYPE != kQ6K && MT <= 2 && nblk >= 40 && try_ring<TYPE, MT, 3, 16, 2>(w, x, y, ldy, rows, nblk, grid, stream))
         return;
 
     const size_t grid_lds = TYPE == kIQ1M ? 16384 : 0;
@@ -801,7 +802,7 @@ static void launch_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t 
             const uint32_t per_wave = (tiles + capacity - 1) / capacity;
             const uint32_t waves = (tiles + per_wave - 1) / per_wave;
             hipLaunchKernelGGL((gemm_q8k_stream<TYPE, MT>), dim3((waves + 3) / 4), dim3(256), lds, stream,
-                               w, x, y, rows, nblk, rw, tiles, grid);
+                               w, x, y, ldy, rows, nblk, rw, tiles, grid);
             return;
         }
     }
@@ -814,43 +815,46 @@ static void launch_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t 
     };
     while (lds_of(ch) > 48 * 1024 && ch > 4) ch = (ch + 1) / 2;
     hipLaunchKernelGGL((gemm_q8k_chunked<TYPE, MT>), dim3((rows + rwc - 1) / rwc), dim3(256), lds_of(ch), stream,
-                       w, x, y, rows, nblk, rwc, ch, grid);
+                       w, x, y, ldy, rows, nblk, rwc, ch, grid);
 }
 
 template <int TYPE>
-static void launch_m(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, uint32_t nblk,
+static void launch_m(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, uint32_t nblk,
                      const uint2 *grid, hipStream_t stream)
 {
     switch (m) {
-    case 1: launch_typed<TYPE, 1>(w, x, y, rows, nblk, grid, stream); break;
-    case 2: launch_typed<TYPE, 2>(w, x, y, rows, nblk, grid, stream); break;
-    case 3: launch_typed<TYPE, 3>(w, x, y, rows, nblk, grid, stream); break;
-    case 4: launch_typed<TYPE, 4>(w, x, y, rows, nblk, grid, stream); break;
-    case 5: launch_typed<TYPE, 5>(w, x, y, rows, nblk, grid, stream); break;
-    case 6: launch_typed<TYPE, 6>(w, x, y, rows, nblk, grid, stream); break;
-    case 7: launch_typed<TYPE, 7>(w, x, y, rows, nblk, grid, stream); break;
-    default: launch_typed<TYPE, 8>(w, x, y, rows, nblk, grid, stream); break;
+    case 1: launch_typed<TYPE, 1>(w, x, y, ldy, rows, nblk, grid, stream); break;
+    case 2: launch_typed<TYPE, 2>(w, x, y, ldy, rows, nblk, grid, stream); break;
+    case 3: launch_typed<TYPE, 3>(w, x, y, ldy, rows, nblk, grid, stream); break;
+    case 4: launch_typed<TYPE, 4>(w, x, y, ldy, rows, nblk, grid, stream); break;
+    case 5: launch_typed<TYPE, 5>(w, x, y, ldy, rows, nblk, grid, stream); break;
+    case 6: launch_typed<TYPE, 6>(w, x, y, ldy, rows, nblk, grid, stream); break;
+    case 7: launch_typed<TYPE, 7>(w, x, y, ldy, rows, nblk, grid, stream); break;
+    default: launch_typed<TYPE, 8>(w, x, y, ldy, rows, nblk, grid, stream); break;
     }
 }
 
-/* Enqueue y[t * rows + row] = W_row . x_t for t < m (all device pointers).
+/* Enqueue y[t * ldy + row] = W_row . x_t for t < m (all device pointers).
  * x is m * nblk Q8_K blocks, token-major.  grid is the IQ1_M codebook as
  * 2048 x 8 int8 (unused for the other types). */
-bool launch_gemv_lanes(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, uint32_t nb,
-                       hipStream_t stream);
+bool launch_gemm_ld(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                    uint32_t nblk, const void *grid, hipStream_t stream)
+{
+    if (m < 1 || m > 8 || ldy < rows) return false;
+    if (launch_gemv_lanes(type, m, w, x, y, ldy, rows, nblk, stream)) return true;
+    const uint2 *g = static_cast<const uint2 *>(grid);
+    switch (type) {
+    case kQ4K: launch_m<kQ4K>(m, w, x, y, ldy, rows, nblk, g, stream); return true;
+    case kQ6K: launch_m<kQ6K>(m, w, x, y, ldy, rows, nblk, g, stream); return true;
+    case kIQ1M: launch_m<kIQ1M>(m, w, x, y, ldy, rows, nblk, g, stream); return true;
+    default: return false;
+    }
+}
 
 bool launch_gemm(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows,
                  uint32_t nblk, const void *grid, hipStream_t stream)
 {
-    if (m < 1 || m > 8) return false;
-    if (launch_gemv_lanes(type, m, w, x, y, rows, nblk, stream)) return true;
-    const uint2 *g = static_cast<const uint2 *>(grid);
-    switch (type) {
-    case kQ4K: launch_m<kQ4K>(m, w, x, y, rows, nblk, g, stream); return true;
-    case kQ6K: launch_m<kQ6K>(m, w, x, y, rows, nblk, g, stream); return true;
-    case kIQ1M: launch_m<kIQ1M>(m, w, x, y, rows, nblk, g, stream); return true;
-    default: return false;
-    }
+    return launch_gemm_ld(type, m, w, x, y, rows, rows, nblk, grid, stream);
 }
 
 }  // namespace q38

@@ -212,15 +212,11 @@ __device__ __forceinline__ int q6k_w(const Lane<kQ6K> &r, const uint8_t *a, int 
     return w - offset;
 }
 
-/* value of lane (base + k) for every lane (cross-lane read) */
-__device__ __forceinline__ float read_lane(float v, int src) { return __shfl(v, src, 64); }
-__device__ __forceinline__ int read_lane(int v, int src) { return __shfl(v, src, 64); }
-
 }  // namespace
 
 template <int TYPE, int MT, int G, int P>
 __global__ __launch_bounds__(256) void gemv_lanes(const uint8_t *__restrict__ w, const uint8_t *__restrict__ x,
-                                                  float *__restrict__ y, uint32_t rows, uint32_t nb)
+                                                  float *__restrict__ y, uint32_t ldy, uint32_t rows, uint32_t nb)
 {
     constexpr int RW = 8 / G;   /* rows per wavefront */
     constexpr int BB = TYPE == kQ4K ? 144 : 210;
@@ -330,7 +326,7 @@ __global__ __launch_bounds__(256) void gemv_lanes(const uint8_t *__restrict__ w,
             m = fadd_rn(m, __shfl_down(m, 1, 8));
             v = fadd_rn(v, m);
         }
-        if (row_ok && g == 0 && l == 0) y[(size_t)t * rows + row] = v;
+        if (row_ok && g == 0 && l == 0) y[(size_t)t * ldy + row] = v;
     }
 }
 
@@ -339,35 +335,35 @@ __global__ __launch_bounds__(256) void gemv_lanes(const uint8_t *__restrict__ w,
  * two-phase kernels of q38_gemm.hip are as fast or faster; from two tokens
  * on this kernel's per-token cost is lower).  Returns false otherwise. */
 template <int TYPE, int MT>
-static bool launch_lanes_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, uint32_t nb,
-                               hipStream_t stream)
+static bool launch_lanes_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                               uint32_t nb, hipStream_t stream)
 {
     const size_t lds = (size_t)MT * nb * kActStride;
     if (MT < 2 || lds > 64 * 1024) return false;
     /* one row per 8 lanes, 32 rows per workgroup; P = 4 blocks in flight per row */
     const dim3 grid((rows + 31) / 32);
-    hipLaunchKernelGGL((gemv_lanes<TYPE, MT, 1, 4>), grid, dim3(256), lds, stream, w, x, y, rows, nb);
+    hipLaunchKernelGGL((gemv_lanes<TYPE, MT, 1, 4>), grid, dim3(256), lds, stream, w, x, y, ldy, rows, nb);
     return true;
 }
 
 template <int TYPE>
-static bool launch_lanes_m(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, uint32_t nb,
-                           hipStream_t stream)
+static bool launch_lanes_m(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                           uint32_t nb, hipStream_t stream)
 {
     switch (m) {
-    case 1: return launch_lanes_typed<TYPE, 1>(w, x, y, rows, nb, stream);
-    case 2: return launch_lanes_typed<TYPE, 2>(w, x, y, rows, nb, stream);
-    case 3: return launch_lanes_typed<TYPE, 3>(w, x, y, rows, nb, stream);
-    case 4: return launch_lanes_typed<TYPE, 4>(w, x, y, rows, nb, stream);
+    case 1: return launch_lanes_typed<TYPE, 1>(w, x, y, ldy, rows, nb, stream);
+    case 2: return launch_lanes_typed<TYPE, 2>(w, x, y, ldy, rows, nb, stream);
+    case 3: return launch_lanes_typed<TYPE, 3>(w, x, y, ldy, rows, nb, stream);
+    case 4: return launch_lanes_typed<TYPE, 4>(w, x, y, ldy, rows, nb, stream);
     default: return false;
     }
 }
 
-bool launch_gemv_lanes(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, uint32_t nb,
-                       hipStream_t stream)
+bool launch_gemv_lanes(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                       uint32_t nb, hipStream_t stream)
 {
-    if (type == kQ4K) return launch_lanes_m<kQ4K>(m, w, x, y, rows, nb, stream);
-    if (type == kQ6K) return launch_lanes_m<kQ6K>(m, w, x, y, rows, nb, stream);
+    if (type == kQ4K) return launch_lanes_m<kQ4K>(m, w, x, y, ldy, rows, nb, stream);
+    if (type == kQ6K) return launch_lanes_m<kQ6K>(m, w, x, y, ldy, rows, nb, stream);
     return false;
 }
 

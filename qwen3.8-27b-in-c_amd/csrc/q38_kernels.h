@@ -13,6 +13,12 @@ constexpr uint32_t kRecurrentStateSlots = 9;
  * m <= 8.  `grid` is the device IQ1_M codebook (2048 x 8 int8). */
 bool launch_gemm(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, uint32_t nblk,
                  const void *grid, hipStream_t stream);
+/* lane-chain kernel for 2..4 tokens; false when it does not apply */
+bool launch_gemv_lanes(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                       uint32_t nb, hipStream_t stream);
+/* same with the token rows of y `ldy` floats apart (ldy >= rows) */
+bool launch_gemm_ld(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                    uint32_t nblk, const void *grid, hipStream_t stream);
 
 /* q38_misc.hip */
 void launch_quantize(const float *x, uint8_t *out, uint32_t nblocks, hipStream_t stream);
@@ -26,7 +32,9 @@ void launch_accept(uint32_t *result, const uint32_t *targets, const uint32_t *dr
 void launch_norm_quant(float *norm_out, long long norm_stride, uint8_t *q_out, int q_stride_blocks, float *hidden,
                        long long in_stride, const float *branch, const float *weight, int rows, hipStream_t stream);
 void launch_add(float *hidden, const float *branch, long long n, hipStream_t stream);
-void launch_swiglu_quant(uint8_t *q_out, const float *gate, const float *up, int rows, hipStream_t stream);
+/* row t of gate and up starts at t * stride floats */
+void launch_swiglu_quant(uint8_t *q_out, const float *gate, const float *up, long long stride, int rows,
+                         hipStream_t stream);
 void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int count, int width, uint32_t vocab,
                       hipStream_t stream);
 /* gated DeltaNet core of one row: conv + SiLU + q/k L2 norm + beta/alpha,
@@ -41,17 +49,18 @@ void launch_deltanet_prep(float *qkv, float *beta, float *alpha, float *conv_sta
 void launch_deltanet_state(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int row,
                            const float *qkv, const float *beta, const float *alpha, float query_scale,
                            hipStream_t stream);
-void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, const float *ssm_norm, int rows,
-                               hipStream_t stream);
+void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, long long z_stride, const float *ssm_norm,
+                               int rows, hipStream_t stream);
 /* full attention over `rows` rows at positions *position + t: prep (norms,
  * RoPE, K/V write), scores, softmax + V + gate + Q8_K of the output */
 bool configure_attention(int context);
 void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_and_gate, const float *key,
-                      const float *value, const float *q_norm, const float *k_norm, const float *rope,
-                      float *key_cache, float *value_cache, float *scores, int context, const uint32_t *position,
-                      int rows, hipStream_t stream);
+                      const float *value, long long in_stride, const float *q_norm, const float *k_norm,
+                      const float *rope, float *key_cache, float *value_cache, float *scores, int context,
+                      const uint32_t *position, int rows, hipStream_t stream);
 /* K-norm, RoPE and K/V cache write of `rows` rows without the query side */
-void launch_kv_write(const float *key, const float *value, const float *k_norm, const float *rope, float *key_cache,
-                     float *value_cache, const uint32_t *position, int rows, hipStream_t stream);
+void launch_kv_write(const float *key, const float *value, long long in_stride, const float *k_norm,
+                     const float *rope, float *key_cache, float *value_cache, const uint32_t *position, int rows,
+                     hipStream_t stream);
 
 }  // namespace q38

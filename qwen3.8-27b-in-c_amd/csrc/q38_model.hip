@@ -141,17 +141,21 @@ __global__ __launch_bounds__(256) void add_kernel(float *__restrict__ hidden, co
     if (i < n) hidden[i] = __fadd_rn(hidden[i], branch[i]);
 }
 
+constexpr int kFFNWidth = 17408;
+
 /* SwiGLU then Q8_K: y = silu(gate) * up (q38_swiglu scalar path,
- * qwen38_model.c:532-549), one wavefront per 256-element block of the
- * row-contiguous [rows][17408] vectors. */
+ * qwen38_model.c:532-549), one wavefront per 256-element block; row t of
+ * gate and up starts at t * stride (a multiple of 4). */
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(uint8_t *__restrict__ q_out, const float *__restrict__ gate,
-                                                           const float *__restrict__ up, int nblocks)
+                                                           const float *__restrict__ up, long long stride, int nblocks)
 {
     const int lane = threadIdx.x & 63;
     const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (b >= nblocks) return;
-    const float4 g = reinterpret_cast<const float4 *>(gate)[b * 64 + lane];
-    const float4 u = reinterpret_cast<const float4 *>(up)[b * 64 + lane];
+    const int t = b / (kFFNWidth / 256), j = b - t * (kFFNWidth / 256);
+    const size_t at = (size_t)t * stride + (size_t)j * 256 + 4 * lane;
+    const float4 g = *reinterpret_cast<const float4 *>(gate + at);
+    const float4 u = *reinterpret_cast<const float4 *>(up + at);
     const float v[4] = {__fmul_rn(siluf_exact(g.x), u.x), __fmul_rn(siluf_exact(g.y), u.y),
                         __fmul_rn(siluf_exact(g.z), u.z), __fmul_rn(siluf_exact(g.w), u.w)};
     wave_quantize_q8k(v, q_out + (size_t)b * kQ8KBytes, lane);
@@ -195,7 +199,7 @@ __global__ __launch_bounds__(256) void embed_q4k_kernel(float *__restrict__ out,
 
 /* ---- gated DeltaNet ------------------------------------------------------ */
 
-constexpr int kQKV = 10240, kQKDim = 2048, kVHeads = 48, kHeadDim = 128, kLinV = 6144, kFFNWidth = 17408;
+constexpr int kQKV = 10240, kQKDim = 2048, kVHeads = 48, kHeadDim = 128, kLinV = 6144;
 constexpr uint32_t kStateSlots = kRecurrentStateSlots;
 
 /* Causal conv (4 taps, state of 3 per channel), SiLU, per-head L2 norm of q
@@ -314,7 +318,7 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
  * ssm_out projection.  One block of 256 threads per pair of heads (one Q8_K
  * block) and row. */
 __global__ __launch_bounds__(256) void deltanet_out_quant_kernel(float *__restrict__ attn, uint8_t *__restrict__ q_out,
-                                                                 const float *__restrict__ z,
+                                                                 const float *__restrict__ z, long long z_stride,
                                                                  const float *__restrict__ norm_w)
 {
     __shared__ double partial[4];
@@ -344,7 +348,7 @@ __global__ __launch_bounds__(256) void deltanet_out_quant_kernel(float *__restri
     __syncthreads();
     const float scale = rms_scale(mean_s[half]);
     const float y = __fmul_rn(__fmul_rn(__fmul_rn(v, scale), norm_w[i]),
-                              siluf_exact(z[(size_t)t * kLinV + head * kHeadDim + i]));
+                              siluf_exact(z[(size_t)t * z_stride + head * kHeadDim + i]));
     x[i] = y;
     ybuf[tid] = y;
     __syncthreads();
@@ -356,7 +360,7 @@ __global__ __launch_bounds__(256) void deltanet_out_quant_kernel(float *__restri
 
 /* ---- full attention ------------------------------------------------------ */
 
-constexpr int kAttnHeads = 24, kKVHeads = 4, kAttnDim = 256, kKVDim = 1024, kQGDim = 12288, kQDim = 6144;
+constexpr int kAttnHeads = 24, kKVHeads = 4, kAttnDim = 256, kKVDim = 1024, kQDim = 6144;
 constexpr int kScoreChunk = 64;
 constexpr int kMaxLdsPositions = 32768;   /* softmax weights kept in LDS up to this many positions */
 
@@ -366,9 +370,11 @@ constexpr int kMaxLdsPositions = 32768;   /* softmax weights kept in LDS up to t
  * (blockIdx.y) at position *position_ptr + t.  Blocks 0..23 are q heads,
  * 24..27 k heads, 28 copies v.  `rope` holds cos (32) then sin (32) per
  * position, computed once on the host with the C library.  `block_base` =
- * 24 runs only the K/V part. */
+ * 24 runs only the K/V part.  Row t of q_and_gate, key and value starts at
+ * t * in_stride. */
 __global__ __launch_bounds__(256) void attn_prep_kernel(float *__restrict__ q_out, const float *__restrict__ q_and_gate,
                                                         const float *__restrict__ key, const float *__restrict__ value,
+                                                        long long in_stride,
                                                         const float *__restrict__ q_norm,
                                                         const float *__restrict__ k_norm,
                                                         const float *__restrict__ rope, float *__restrict__ key_cache,
@@ -381,13 +387,13 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float *__restrict__ q_ou
     const int block = blockIdx.x + block_base;
     float *kc = key_cache + (size_t)pos * kKVDim;
     if (block == kAttnHeads + kKVHeads) {
-        for (int e = i; e < kKVDim; e += 256) value_cache[(size_t)pos * kKVDim + e] = value[(size_t)t * kKVDim + e];
+        for (int e = i; e < kKVDim; e += 256) value_cache[(size_t)pos * kKVDim + e] = value[(size_t)t * in_stride + e];
         return;
     }
     const bool is_q = block < kAttnHeads;
     const int h = is_q ? block : block - kAttnHeads;
-    const float *src = is_q ? q_and_gate + (size_t)t * kQGDim + h * 2 * kAttnDim
-                            : key + (size_t)t * kKVDim + h * kAttnDim;
+    const float *src = is_q ? q_and_gate + (size_t)t * in_stride + h * 2 * kAttnDim
+                            : key + (size_t)t * in_stride + h * kAttnDim;
     const float *w = is_q ? q_norm : k_norm;
     const float x = src[i];
     const float mean = block_sum_finish<256>((double)__fmul_rn(x, x), src, kAttnDim, MeanPost{256.0});
@@ -453,7 +459,7 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(float *__restrict__ sco
 template <bool IN_LDS>
 __global__ __launch_bounds__(256) void attn_output_kernel(float *__restrict__ out, uint8_t *__restrict__ q_out,
                                                           float *__restrict__ scores,
-                                                          const float *__restrict__ q_and_gate,
+                                                          const float *__restrict__ q_and_gate, long long qg_stride,
                                                           const float *__restrict__ value_cache, int context,
                                                           const uint32_t *__restrict__ position_ptr)
 {
@@ -504,7 +510,7 @@ __global__ __launch_bounds__(256) void attn_output_kernel(float *__restrict__ ou
         for (int k = 0; k < 8; ++k) o = __builtin_fmaf(e[p + k], vv[k], o);
     }
     for (; p < n; ++p) o = __builtin_fmaf(e[p], vcol[(size_t)p * kKVDim], o);
-    const float g = q_and_gate[(size_t)t * kQGDim + h * 2 * kAttnDim + kAttnDim + tid];
+    const float g = q_and_gate[(size_t)t * qg_stride + h * 2 * kAttnDim + kAttnDim + tid];
     const float y = __fmul_rn(o, sigmoidf_exact(g));
     out[(size_t)t * kQDim + h * kAttnDim + tid] = y;
     ybuf[tid] = y;
@@ -533,10 +539,11 @@ void launch_add(float *hidden, const float *branch, long long n, hipStream_t str
     add_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(hidden, branch, n);
 }
 
-void launch_swiglu_quant(uint8_t *q_out, const float *gate, const float *up, int rows, hipStream_t stream)
+void launch_swiglu_quant(uint8_t *q_out, const float *gate, const float *up, long long stride, int rows,
+                         hipStream_t stream)
 {
     const int nblocks = rows * (kFFNWidth / 256);
-    swiglu_quant_kernel<<<(nblocks + 3) / 4, 256, 0, stream>>>(q_out, gate, up, nblocks);
+    swiglu_quant_kernel<<<(nblocks + 3) / 4, 256, 0, stream>>>(q_out, gate, up, stride, nblocks);
 }
 
 void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int count, int width, uint32_t vocab,
@@ -561,10 +568,10 @@ void launch_deltanet_state(float *attn, float *delta_state, long long slot_strid
                                                                      beta, alpha, query_scale);
 }
 
-void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, const float *ssm_norm, int rows,
-                               hipStream_t stream)
+void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, long long z_stride, const float *ssm_norm,
+                               int rows, hipStream_t stream)
 {
-    deltanet_out_quant_kernel<<<dim3(kVHeads / 2, rows), 256, 0, stream>>>(attn, q_out, z, ssm_norm);
+    deltanet_out_quant_kernel<<<dim3(kVHeads / 2, rows), 256, 0, stream>>>(attn, q_out, z, z_stride, ssm_norm);
 }
 
 bool configure_attention(int context)
@@ -575,27 +582,29 @@ bool configure_attention(int context)
 }
 
 void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_and_gate, const float *key,
-                      const float *value, const float *q_norm, const float *k_norm, const float *rope,
-                      float *key_cache, float *value_cache, float *scores, int context, const uint32_t *position,
-                      int rows, hipStream_t stream)
+                      const float *value, long long in_stride, const float *q_norm, const float *k_norm,
+                      const float *rope, float *key_cache, float *value_cache, float *scores, int context,
+                      const uint32_t *position, int rows, hipStream_t stream)
 {
     attn_prep_kernel<<<dim3(kAttnHeads + kKVHeads + 1, rows), 256, 0, stream>>>(
-        q_buf, q_and_gate, key, value, q_norm, k_norm, rope, key_cache, value_cache, position, 0);
+        q_buf, q_and_gate, key, value, in_stride, q_norm, k_norm, rope, key_cache, value_cache, position, 0);
     attn_scores_kernel<<<dim3(kKVHeads, (context + kScoreChunk - 1) / kScoreChunk, rows), 64, 0, stream>>>(
         scores, q_buf, key_cache, context, position);
     if (context <= kMaxLdsPositions)
         attn_output_kernel<true><<<dim3(kAttnHeads, rows), 256, (size_t)context * 4, stream>>>(
-            attn, q_out, scores, q_and_gate, value_cache, context, position);
+            attn, q_out, scores, q_and_gate, in_stride, value_cache, context, position);
     else
-        attn_output_kernel<false><<<dim3(kAttnHeads, rows), 256, 0, stream>>>(attn, q_out, scores, q_and_gate,
-                                                                             value_cache, context, position);
+        attn_output_kernel<false><<<dim3(kAttnHeads, rows), 256, 0, stream>>>(
+            attn, q_out, scores, q_and_gate, in_stride, value_cache, context, position);
 }
 
-void launch_kv_write(const float *key, const float *value, const float *k_norm, const float *rope, float *key_cache,
-                     float *value_cache, const uint32_t *position, int rows, hipStream_t stream)
+void launch_kv_write(const float *key, const float *value, long long in_stride, const float *k_norm,
+                     const float *rope, float *key_cache, float *value_cache, const uint32_t *position, int rows,
+                     hipStream_t stream)
 {
-    attn_prep_kernel<<<dim3(kKVHeads + 1, rows), 256, 0, stream>>>(nullptr, nullptr, key, value, nullptr, k_norm, rope,
-                                                                  key_cache, value_cache, position, kAttnHeads);
+    attn_prep_kernel<<<dim3(kKVHeads + 1, rows), 256, 0, stream>>>(nullptr, nullptr, key, value, in_stride, nullptr,
+                                                                  k_norm, rope, key_cache, value_cache, position,
+                                                                  kAttnHeads);
 }
 
 }  // namespace q38
