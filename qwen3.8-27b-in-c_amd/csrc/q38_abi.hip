@@ -10,17 +10,7 @@
 #include "q38hip.h"
 #include "q38_device.h"
 #include "q38_iq1m_grid.inc"
-
-namespace q38 {
-bool launch_gemm(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows,
-                 uint32_t nblk, const void *grid, hipStream_t stream);
-void launch_quantize(const float *x, uint8_t *out, uint32_t nblocks, hipStream_t stream);
-uint32_t argmax_chunks(uint32_t count);
-void launch_argmax(const float *values, uint32_t count, uint32_t rows, float *pv, uint32_t *pi,
-                   uint32_t *out, hipStream_t stream);
-void launch_accept(uint32_t *result, const uint32_t *targets, const uint32_t *drafts, uint32_t rows,
-                   hipStream_t stream);
-}  // namespace q38
+#include "q38_kernels.h"
 
 namespace {
 
@@ -179,6 +169,38 @@ int q38hip_gemm_q8_k(float *output, const Q38Q8KBlock *input, uint32_t batch_siz
                                      (uint32_t)tensor->shape[1], (uint32_t)(input_length / 256),
                                      state->grid, static_cast<hipStream_t>(stream));
     return ok ? 1 : fail("unsupported GEMM configuration");
+}
+
+uint64_t q38hip_tiled_q4k_bytes(uint32_t rows, uint64_t input_length)
+{
+    if (!rows || !input_length || input_length % Q38_Q8_K_BLOCK_SIZE || input_length / 256 > 0xffffffffull) return 0;
+    return q38::tiled_q4k_bytes(rows, (uint32_t)(input_length / 256));
+}
+
+int q38hip_repack_q4k_tiles(void *tiled, const void *q4k_rows, uint32_t rows, uint64_t input_length, void *stream)
+{
+    if (!tiled || !q4k_rows || !rows) return fail("null argument");
+    if (!input_length || input_length % Q38_Q8_K_BLOCK_SIZE || input_length / 256 > 0xffffffffull)
+        return fail("input length is not a positive multiple of 256");
+    if (!device_state()) return fail("device initialisation failed");
+    return q38::launch_repack_q4k_tiles(static_cast<uint8_t *>(tiled), static_cast<const uint8_t *>(q4k_rows), rows,
+                                        (uint32_t)(input_length / 256), static_cast<hipStream_t>(stream))
+               ? 1
+               : fail("repack launch failed (tiled copy must be 16-byte aligned)");
+}
+
+int q38hip_gemm_q8_k_tiled(float *output, const Q38Q8KBlock *input, uint32_t batch_size, uint64_t input_length,
+                           const void *tiled, uint32_t rows, void *stream)
+{
+    if (!output || !input || !tiled || !rows) return fail("null argument");
+    if (batch_size < 2 || batch_size > 8) return fail("batch_size must be 2..8");
+    if (!device_state()) return fail("device initialisation failed");
+    if (input_length % Q38_Q8_K_BLOCK_SIZE ||
+        !q38::launch_gemm_q4k_tiled((int)batch_size, static_cast<const uint8_t *>(tiled),
+                                    reinterpret_cast<const uint8_t *>(input), output, rows, rows,
+                                    (uint32_t)(input_length / 256), static_cast<hipStream_t>(stream)))
+        return fail("unsupported tiled GEMM shape (input_length 5120, 6144, 10240 or 17408)");
+    return 1;
 }
 
 int q38hip_argmax(uint32_t *index_out, const float *values, uint32_t count, uint32_t rows, void *stream)

@@ -284,6 +284,9 @@ struct DevTensor {
     uint32_t n_dims = 0;
     uint64_t width = 0, rows = 0;
     const uint8_t *data = nullptr;
+    /* Q4_K matrices: 16-row tiled copy used for 2..8-token GEMMs (may be
+     * null); for a group member, its rows inside its run's tiled copy */
+    const uint8_t *tiled = nullptr;
     const float *f32() const { return reinterpret_cast<const float *>(data); }
 };
 
@@ -325,6 +328,7 @@ bool matrix_type_ok(uint32_t t) { return t == Q4_K || t == Q6_K || t == IQ1_M; }
 struct Q38Model {
     GGUFFile gguf, mtp_gguf;
     void *weights = nullptr, *mtp_weights = nullptr;
+    void *tiled_weights = nullptr, *tiled_mtp = nullptr;   /* tiled copies (target layers, MTP block) */
     DevTensor embedding, output_norm, output, mtp_embedding, mtp_output;
     DevTensor eh_proj, enorm, hnorm, shared_head_norm;
     Layer layers[kTotalLayers];
@@ -620,6 +624,8 @@ void release(Q38Model *m)
     dfree(m->q8k);
     if (m->weights) (void)hipFree(m->weights);
     if (m->mtp_weights) (void)hipFree(m->mtp_weights);
+    if (m->tiled_weights) (void)hipFree(m->tiled_weights);
+    if (m->tiled_mtp) (void)hipFree(m->tiled_mtp);
     if (m->host_logits) (void)hipHostFree(m->host_logits);
     if (m->host_words) (void)hipHostFree(m->host_words);
     if (m->host_params) (void)hipHostFree(m->host_params);
@@ -740,6 +746,10 @@ Step step_of(Q38Model *m, uint32_t param_set, const uint32_t *tokens)
  * `first_block`) */
 bool gemm_q(Q38Model *m, const DevTensor &w, uint32_t count, float *out, size_t first_block = 0)
 {
+    if (count >= 2 && w.tiled &&
+        q38::launch_gemm_q4k_tiled((int)count, w.tiled, m->q8k + first_block * kQ8KBytes, out, (uint32_t)w.rows,
+                                   (uint32_t)w.rows, (uint32_t)(w.width / 256), m->stream))
+        return true;
     if (!q38::launch_gemm((int)w.type, (int)count, w.data, m->q8k + first_block * kQ8KBytes, out, (uint32_t)w.rows,
                           (uint32_t)(w.width / 256), m->grid, m->stream))
         return report("unsupported GEMM configuration");
@@ -753,9 +763,10 @@ uint64_t row_bytes(const DevTensor &t)
     return t.width / e * b;
 }
 
-/* members [lo, hi) of group g over `count` Q8_K rows in m->q8k; row t of
- * member i lands at out + t * ldy + first[i] - first[lo] */
-bool gemm_group(Q38Model *m, const Group &g, int lo, int hi, uint32_t count, float *out, uint32_t ldy)
+/* runs of members [lo, hi) of g that form one matrix (same type and width,
+ * back to back in HBM): f(first member, end member, total rows) */
+template <typename F>
+void for_runs(const Group &g, int lo, int hi, F f)
 {
     for (int i = lo; i < hi;) {
         const DevTensor &a = g.part[i];
@@ -766,12 +777,87 @@ bool gemm_group(Q38Model *m, const Group &g, int lo, int hi, uint32_t count, flo
             rows += g.part[j].rows;
             ++j;
         }
-        if (!q38::launch_gemm_ld((int)a.type, (int)count, a.data, m->q8k, out + (g.first[i] - g.first[lo]), ldy,
-                                 (uint32_t)rows, (uint32_t)(a.width / 256), m->grid, m->stream))
-            return report("unsupported GEMM configuration");
+        f(i, j, rows);
         i = j;
     }
-    return true;
+}
+
+/* Build 16-row tiled copies of the Q4_K GEMM matrices of blocks
+ * [first, last) (plus eh_proj when `with_eh`) in one allocation: every run
+ * of a fusion group, the down projection and the attention / DeltaNet
+ * output projection.  A group member whose first row inside its run is a
+ * multiple of 16 gets a pointer to its own tiles. */
+bool build_tiled(Q38Model *m, uint32_t first, uint32_t last, bool with_eh, void **mem)
+{
+    struct Job {
+        const uint8_t *src;
+        uint32_t rows, nb;
+        std::vector<std::pair<DevTensor *, uint64_t>> targets;   /* tensor, first tile */
+    };
+    std::vector<Job> jobs;
+    auto supported = [](const DevTensor &t) {
+        const uint64_t nb = t.width / 256;
+        return t.type == Q4_K && t.data && (nb == 20 || nb == 24 || nb == 40 || nb == 68);
+    };
+    auto add_group = [&](Group &g) {
+        for_runs(g, 0, g.n, [&](int i, int j, uint64_t rows) {
+            if (!supported(g.part[i])) return;
+            Job job{g.part[i].data, (uint32_t)rows, (uint32_t)(g.part[i].width / 256), {}};
+            uint64_t row = 0;
+            for (int k = i; k < j; ++k) {
+                if (row % 16 == 0) job.targets.emplace_back(&g.part[k], row / 16);
+                row += g.part[k].rows;
+            }
+            jobs.push_back(job);
+        });
+    };
+    auto add_one = [&](DevTensor &t) {
+        if (supported(t)) jobs.push_back(Job{t.data, (uint32_t)t.rows, (uint32_t)(t.width / 256), {{&t, 0}}});
+    };
+    for (uint32_t l = first; l < last; ++l) {
+        Layer &L = m->layers[l];
+        add_group(L.ffn_in);
+        add_group(L.mix_in);
+        add_one(L.ffn_down);
+        add_one(L.full ? L.out : L.ssm_out);
+    }
+    if (with_eh) add_one(m->eh_proj);
+    size_t total = 0;
+    std::vector<size_t> offsets;
+    for (const Job &j : jobs) {
+        offsets.push_back(total);
+        total += align256(q38::tiled_q4k_bytes(j.rows, j.nb));
+    }
+    if (!total) return true;
+    if (!hip_ok(hipMalloc(mem, total), "tiled weight allocation")) return false;
+    uint8_t *base = static_cast<uint8_t *>(*mem);
+    for (size_t k = 0; k < jobs.size(); ++k) {
+        const Job &j = jobs[k];
+        uint8_t *dst = base + offsets[k];
+        if (!q38::launch_repack_q4k_tiles(dst, j.src, j.rows, j.nb, m->stream)) return report("tiled repack failed");
+        for (const auto &t : j.targets) t.first->tiled = dst + t.second * j.nb * 2304;
+    }
+    return hip_ok(hipStreamSynchronize(m->stream), "tiled repack");
+}
+
+/* members [lo, hi) of group g over `count` Q8_K rows in m->q8k; row t of
+ * member i lands at out + t * ldy + first[i] - first[lo].  Two or more rows
+ * use the tiled copy where there is one. */
+bool gemm_group(Q38Model *m, const Group &g, int lo, int hi, uint32_t count, float *out, uint32_t ldy)
+{
+    bool ok = true;
+    for_runs(g, lo, hi, [&](int i, int, uint64_t rows) {
+        const DevTensor &a = g.part[i];
+        float *y = out + (g.first[i] - g.first[lo]);
+        const uint32_t nb = (uint32_t)(a.width / 256);
+        if (count >= 2 && a.tiled &&
+            q38::launch_gemm_q4k_tiled((int)count, a.tiled, m->q8k, y, ldy, (uint32_t)rows, nb, m->stream))
+            return;
+        if (!q38::launch_gemm_ld((int)a.type, (int)count, a.data, m->q8k, y, ldy, (uint32_t)rows, nb, m->grid,
+                                 m->stream))
+            ok = report("unsupported GEMM configuration");
+    });
+    return ok;
 }
 
 /* host staging of a parameter block: position of row 0 and the current
@@ -1091,6 +1177,8 @@ Q38Model *q38_model_open_gguf(const char *path, uint32_t context_length)
     uint32_t blocks = 0;
     if (ok && m->gguf.get_u32("qwen35.block_count", &blocks) && blocks == kTotalLayers)
         ok = bind_mtp(m, m->gguf, base);
+    ok = ok && build_tiled(m, 0, kLayers, false, &m->tiled_weights) &&
+         (!m->mtp_weights_loaded || build_tiled(m, kLayers, kLayers + 1, true, &m->tiled_mtp));
     ok = ok && allocate_state(m) && clear_state(m);
     if (ok && !q38::configure_attention((int)context_length)) ok = report("attention kernel configuration failed");
     if (const char *v = getenv("QWEN38_NO_GRAPHS")) m->graphs_enabled = !(v[0] && strcmp(v, "0") != 0);
@@ -1107,13 +1195,16 @@ int q38_model_attach_mtp_gguf(Q38Model *m, const char *path)
         m->mtp_gguf.fd >= 0)
         return 0;
     const bool ok = m->mtp_gguf.open(path) && upload(m->mtp_gguf, &m->mtp_weights) &&
-                    bind_mtp(m, m->mtp_gguf, static_cast<const uint8_t *>(m->mtp_weights));
+                    bind_mtp(m, m->mtp_gguf, static_cast<const uint8_t *>(m->mtp_weights)) &&
+                    build_tiled(m, kLayers, kLayers + 1, true, &m->tiled_mtp);
     if (!ok) {
         m->layers[kLayers] = Layer();
         m->mtp_embedding = m->mtp_output = m->eh_proj = m->enorm = m->hnorm = m->shared_head_norm = DevTensor();
         m->mtp_weights_loaded = false;
         if (m->mtp_weights) (void)hipFree(m->mtp_weights);
         m->mtp_weights = nullptr;
+        if (m->tiled_mtp) (void)hipFree(m->tiled_mtp);
+        m->tiled_mtp = nullptr;
         m->mtp_gguf.close();
         return 0;
     }

@@ -16,6 +16,13 @@ bool launch_gemm(int type, int m, const uint8_t *w, const uint8_t *x, float *y, 
 /* lane-chain kernel for 2..4 tokens; false when it does not apply */
 bool launch_gemv_lanes(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                        uint32_t nb, hipStream_t stream);
+/* Q4_K matrices in the 16-row tiled layout (q38_tiled.hip): bytes of the
+ * tiled copy, the repack from row-major, and the matrix-core GEMM for 2..8
+ * tokens (false when the width or token count is not supported) */
+size_t tiled_q4k_bytes(uint32_t rows, uint32_t nb);
+bool launch_repack_q4k_tiles(uint8_t *dst, const uint8_t *src, uint32_t rows, uint32_t nb, hipStream_t stream);
+bool launch_gemm_q4k_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                           uint32_t nb, hipStream_t stream);
 /* same with the token rows of y `ldy` floats apart (ldy >= rows) */
 bool launch_gemm_ld(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                     uint32_t nblk, const void *grid, hipStream_t stream);

@@ -1,0 +1,326 @@
+/* Q4_K x Q8_K for 2..8 tokens on the gfx950 matrix cores, over a 16-row
+ * tiled copy of the weights (the speculative verify batch and prefill).
+ *
+ * Layout.  The tiled copy of a Q4_K matrix of R rows x NB super-blocks is
+ * [tile = row / 16][block][row % 16][144 bytes]: the 16 rows' blocks b sit
+ * together (2304 contiguous bytes), so a wavefront walking a tile reads one
+ * contiguous stretch per step.  The last tile is zero-padded.
+ *
+ * Arithmetic.  The reference's AVX2 kernel (src/qwen38/qwen38_quant.c:
+ * 1546-1634) keeps, per row and token, eight fp32 accumulator lanes and four
+ * min lanes; for every super-block b in order, lane l adds d_b * W[b][l] and
+ * min lane i adds -dmin_b * M[b][i], with
+ *   W[b][l] = sum_c sc[2c] * sum_u lo(q[32c+4l+u]) * a[64c+4l+u]
+ *           + sc[2c+1] * sum_u hi(q[32c+4l+u]) * a[64c+32+4l+u]
+ *   M[b][i] = m[2i] * (s[4i] + s[4i+1]) + m[2i+1] * (s[4i+2] + s[4i+3]).
+ * W[b][l] is a 32-term integer dot product of sc * q (<= 945, exact in
+ * fp16) with the int8 activations (exact in fp16); every product and every
+ * partial sum is an integer below 2^22, so v_mfma_f32_16x16x32_f16 returns
+ * it exactly whatever its internal order.  The fp32 chains then run in the
+ * reference's order with its fmaf and product roundings.
+ *
+ * Mapping.  Two wavefronts share a tile: wavefront G owns AVX2 lanes
+ * 4G..4G+3.  Lane i: row r = i % 16, chunk q = i / 16 (elements 64q..64q+63),
+ * and as an A row m = (g, t) = (i / 4 % 4, i % 4).  For each p = 0..3:
+ *   B_p (weights): K-slot q, column r = the 8 quants of AVX2 lane 4G + p in
+ *     chunk q as fp16 sc * q (one dword: masks, then a packed fma per pair,
+ *     (1024 + n) * sc - 1024 * sc);
+ *   A (activations): row (g, t), K-slot q = token t's 8 activations of AVX2
+ *     lane 4G + g in chunk q;
+ *   D_p[(g, t)][r] = sum over chunks of act(4G + g) . w(4G + p), which for
+ *     g == p is W[b][4G + p] for token t.
+ * Lane (r, q) reads that diagonal from D_q: it runs the chains of AVX2 lane
+ * 4G + q (tokens t = 0..MT-1, four per MFMA token set) and, in wavefront 0,
+ * of min lane q.  Wavefront 1 hands its lanes to wavefront 0 through LDS for
+ * the reference's final tree.
+ *
+ * Memory.  Weights and activations are read with buffer loads whose block
+ * offset is a scalar, four blocks ahead of use; each ring slot is refilled
+ * only after its last use so the loop-carried registers stay in place and
+ * the waits count only the loads still needed.  Scales and min pair sums of
+ * the activations are staged in LDS once per workgroup.
+ */
+#include "q38_device.h"
+#include "q38_kernels.h"
+
+namespace q38 {
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+constexpr int kTileRows = 16;
+constexpr int kQ4KBytes = 144;
+constexpr int kTileBlockBytes = kTileRows * kQ4KBytes;   /* 2304 */
+constexpr uint32_t kBufferFlags = 0x00020000u;           /* raw 32-bit buffer resource (gfx9) */
+
+__device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
+
+/* fp16 pair (n, n) for an integer n < 1024: (1024 + n) - 1024 */
+__device__ __forceinline__ half2v pair_of(uint32_t n)
+{
+    const half2v x = as_h2((n | (n << 16)) | 0x64006400u);
+    return x - (half2v){(_Float16)1024.0f, (_Float16)1024.0f};
+}
+
+struct Slot {
+    uint4 h;        /* block header: d, dmin, 12 scale/min bytes */
+    uint4 qd;       /* quant dwords 4G .. 4G+3 of chunk q */
+    uint32_t alo[2], ahi[2];   /* per token set: 4 activations of half 0 and of half 1 */
+};
+
+}  // namespace
+
+/* 4 / 2 tiles per workgroup of 256 threads; P blocks in flight per wave. */
+template <int MT, int NB, int P>
+__global__ __launch_bounds__(256) void gemm_q4k_tiled(const uint8_t *__restrict__ w, const uint8_t *__restrict__ x,
+                                                       float *__restrict__ y, uint32_t ldy, uint32_t rows)
+{
+    constexpr int TS = (MT + 3) / 4;   /* MFMA token sets of four */
+    __shared__ int2 pairs_s[MT * NB * 4];
+    __shared__ float xs_s[MT * NB];
+    __shared__ float xch[2][MT][64];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int tl = wave >> 1, G = wave & 1;
+    const int r = lane & 15, q = lane >> 4, g = (lane >> 2) & 3, tk = lane & 3;
+    const uint32_t ntiles = (rows + kTileRows - 1) / kTileRows;
+    const uint32_t tile = blockIdx.x * 2u + (uint32_t)tl;
+    const uint32_t tc = tile < ntiles ? tile : ntiles - 1;   /* idle waves re-read the last tile */
+
+    /* uniform bases plus 32-bit per-lane offsets */
+    const uint8_t *tb = w + (size_t)tc * NB * kTileBlockBytes;
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(tb), 0, NB * kTileBlockBytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(x), 0, MT * NB * kQ8KBytes, kBufferFlags);
+    const uint32_t hoff = (uint32_t)(r * kQ4KBytes), qoff = hoff + 16 + 32 * q + 16 * G;
+    uint32_t xoff[TS];   /* token tk + 4s (clamped), AVX2 lane 4G + g, chunk q, half 0 */
+#pragma unroll
+    for (int s = 0; s < TS; ++s) {
+        const int t = tk + 4 * s < MT ? tk + 4 * s : MT - 1;
+        xoff[s] = (uint32_t)(t * NB * kQ8KBytes + 4 + 64 * q + 4 * (4 * G + g));
+    }
+    auto load = [&](int b) {
+        Slot sl;
+        const int4v h = __builtin_amdgcn_raw_buffer_load_b128(wr, hoff, b * kTileBlockBytes, 0);
+        const int4v qv = __builtin_amdgcn_raw_buffer_load_b128(wr, qoff, b * kTileBlockBytes, 0);
+        sl.h = make_uint4(h[0], h[1], h[2], h[3]);
+        sl.qd = make_uint4(qv[0], qv[1], qv[2], qv[3]);
+#pragma unroll
+        for (int s = 0; s < TS; ++s) {
+            sl.alo[s] = __builtin_amdgcn_raw_buffer_load_b32(xr, xoff[s], b * kQ8KBytes, 0);
+            sl.ahi[s] = __builtin_amdgcn_raw_buffer_load_b32(xr, xoff[s] + 32, b * kQ8KBytes, 0);
+        }
+        return sl;
+    };
+    Slot ring[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) ring[i] = load(i < NB ? i : NB - 1);
+
+    /* activation scales and min pair sums: Q8_K dword 0 and bsum dwords 65..72 */
+    {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(x);
+        for (int i = threadIdx.x; i < MT * NB * 9; i += 256) {
+            const int blk = i / 9, k = i - blk * 9;
+            const uint32_t v = src[(size_t)blk * 73 + (k == 0 ? 0 : 64 + k)];
+            if (k == 0) xs_s[blk] = __uint_as_float(v);
+            else reinterpret_cast<int *>(pairs_s)[blk * 8 + (k - 1)] = (int)(int16_t)(v & 0xffffu) + ((int)v >> 16);
+        }
+    }
+    __syncthreads();
+
+    float acc[MT], accm[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = accm[t] = 0.0f;
+
+    /* loop-invariant per-lane values (the masks live in registers: VOP3
+     * forms cannot take two literals) */
+    uint32_t kMask = 0x000f000fu, kMagic = 0x64006400u;
+    asm volatile("" : "+v"(kMask), "+v"(kMagic));
+    const int sh = (q & 1) * 16;
+    const bool hi_chunk = q >= 2, q_odd = (q & 1) != 0;
+    const uint32_t kLow = hi_chunk ? 0x0f0f0f0fu : 0x3f3f3f3fu, kHigh = hi_chunk ? 0x30303030u : 0u;
+
+    auto step = [&](const Slot &c, int b) {
+        const uint32_t Y = c.h.y, Z = c.h.z, Wd = c.h.w;
+        /* 6-bit scales of sub-blocks 2q, 2q+1 (src/qwen38/qwen38_quant.c:131-143) */
+        const uint32_t scw = ((hi_chunk ? Wd : Y) & kLow) | ((Y >> 2) & kHigh);
+        const half2v SL = pair_of((scw >> sh) & 0xffu), SH = pair_of((scw >> (sh + 8)) & 0xffu);
+        const half2v k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+        const half2v NL = SL * k1024, NH = SH * k1024;
+        const float d = f16_to_f32(c.h.x), dmin = f16_to_f32(c.h.x >> 16);
+        float dw[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) dw[t] = fmul_rn(d, xs_s[t * NB + b]);
+        half8 bv[4];
+        const uint32_t qw[4] = {c.qd.x, c.qd.y, c.qd.z, c.qd.w};
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            /* element order per half: u = 0, 2, 1, 3 (the activations use the same) */
+            const uint32_t wd = qw[p];
+            const half2v b0 = __builtin_elementwise_fma(as_h2((wd & kMask) | kMagic), SL, NL);
+            const half2v b1 = __builtin_elementwise_fma(as_h2(((wd >> 8) & kMask) | kMagic), SL, NL);
+            const half2v b2 = __builtin_elementwise_fma(as_h2(((wd >> 4) & kMask) | kMagic), SH, NH);
+            const half2v b3 = __builtin_elementwise_fma(as_h2(((wd >> 12) & kMask) | kMagic), SH, NH);
+            bv[p][0] = b0[0]; bv[p][1] = b0[1]; bv[p][2] = b1[0]; bv[p][3] = b1[1];
+            bv[p][4] = b2[0]; bv[p][5] = b2[1]; bv[p][6] = b3[0]; bv[p][7] = b3[1];
+        }
+#pragma unroll
+        for (int s = 0; s < TS; ++s) {
+            /* int8 -> fp16: bytes biased by 128 under 0x64 are 1024 + 128 + a */
+            const half2v k1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+            const uint32_t ua = c.alo[s] ^ 0x80808080u, ub = c.ahi[s] ^ 0x80808080u;
+            const half2v a02 = as_h2(__builtin_amdgcn_perm(0x64646464u, ua, 0x04020400u)) + k1152;
+            const half2v a13 = as_h2(__builtin_amdgcn_perm(0x64646464u, ua, 0x04030401u)) + k1152;
+            const half2v b02 = as_h2(__builtin_amdgcn_perm(0x64646464u, ub, 0x04020400u)) + k1152;
+            const half2v b13 = as_h2(__builtin_amdgcn_perm(0x64646464u, ub, 0x04030401u)) + k1152;
+            half8 av;
+            av[0] = a02[0]; av[1] = a02[1]; av[2] = a13[0]; av[3] = a13[1];
+            av[4] = b02[0]; av[5] = b02[1]; av[6] = b13[0]; av[7] = b13[1];
+            float4v D[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+                D[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[p], (float4v){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int t = 4 * s + j;
+                if (t >= MT) break;
+                /* the diagonal: lane (r, q) takes D_q */
+                const float w01 = q_odd ? D[1][j] : D[0][j], w23 = q_odd ? D[3][j] : D[2][j];
+                acc[t] = __builtin_fmaf(dw[t], hi_chunk ? w23 : w01, acc[t]);
+            }
+        }
+        if (G == 0) {
+            /* 6-bit mins of sub-blocks 2q, 2q+1 */
+            const uint32_t mw = ((hi_chunk ? (Wd >> 4) : Z) & kLow) | ((Z >> 2) & kHigh);
+            const int m0 = (int)((mw >> sh) & 0xffu), m1 = (int)((mw >> (sh + 8)) & 0xffu);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const int2 pr = pairs_s[(t * NB + b) * 4 + q];
+                const int M = mad24(m0, pr.x, mul24(m1, pr.y));
+                accm[t] = __builtin_fmaf(-fmul_rn(dmin, xs_s[t * NB + b]), (float)M, accm[t]);
+            }
+        }
+    };
+
+    constexpr int kFull = NB / P, kRem = NB % P;
+#pragma unroll 1
+    for (int it = 0; it < kFull; ++it) {
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int b = it * P + i;
+            step(ring[i], b);
+            /* refill the slot after its last use (loads past the end re-read
+             * the last block and are never used) */
+            ring[i] = load(b + P < NB ? b + P : NB - 1);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kRem; ++i) step(ring[i], NB - kRem + i);
+
+    /* wavefront 1 hands AVX2 lanes 4..7 to wavefront 0, which applies the
+     * reference's trees: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)), then
+     * ((m0+m2)+(m1+m3)) (qwen38_quant.c:303-310, 1626-1630) */
+    if (G == 1) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) xch[tl][t][lane] = acc[t];
+    }
+    __syncthreads();
+    if (G == 0) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            float v = fadd_rn(acc[t], xch[tl][t][lane]);
+            v = fadd_rn(v, __shfl_xor(v, 32, 64));
+            v = fadd_rn(v, __shfl_xor(v, 16, 64));
+            float m = accm[t];
+            m = fadd_rn(m, __shfl_xor(m, 32, 64));
+            m = fadd_rn(m, __shfl_xor(m, 16, 64));
+            const uint32_t row = tile * kTileRows + (uint32_t)r;
+            if (q == 0 && tile < ntiles && row < rows) y[(size_t)t * ldy + row] = fadd_rn(v, m);
+        }
+    }
+}
+
+/* Row-major Q4_K (rows x nb blocks) -> tiled copy; one thread per 16-byte
+ * piece of the destination, pad rows of the last tile are zero. */
+__global__ __launch_bounds__(256) void repack_q4k_tiles(uint4 *__restrict__ dst, const uint8_t *__restrict__ src,
+                                                        uint32_t rows, uint32_t nb, size_t pieces)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= pieces) return;
+    const size_t block_index = i / 9, k = i - block_index * 9;   /* 9 pieces per 144-byte block */
+    const size_t per_tile = (size_t)nb * kTileRows;
+    const size_t tile = block_index / per_tile, rem = block_index - tile * per_tile;
+    const size_t b = rem / kTileRows, rr = rem - b * kTileRows;
+    const size_t row = tile * kTileRows + rr;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row < rows) {
+        const uint8_t *p = src + (row * nb + b) * kQ4KBytes + k * 16;
+        __builtin_memcpy(&v, p, 16);
+    }
+    dst[i] = v;
+}
+
+size_t tiled_q4k_bytes(uint32_t rows, uint32_t nb)
+{
+    return (size_t)((rows + kTileRows - 1) / kTileRows) * nb * kTileBlockBytes;
+}
+
+bool launch_repack_q4k_tiles(uint8_t *dst, const uint8_t *src, uint32_t rows, uint32_t nb, hipStream_t stream)
+{
+    if (!rows || !nb || (reinterpret_cast<uintptr_t>(dst) & 15)) return false;
+    const size_t pieces = tiled_q4k_bytes(rows, nb) / 16;
+    hipLaunchKernelGGL(repack_q4k_tiles, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream,
+                       reinterpret_cast<uint4 *>(dst), src, rows, nb, pieces);
+    return hipGetLastError() == hipSuccess;
+}
+
+namespace {
+
+template <int MT, int NB>
+void launch_tiled_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, hipStream_t stream)
+{
+    const uint32_t tiles = (rows + kTileRows - 1) / kTileRows;
+    hipLaunchKernelGGL((gemm_q4k_tiled<MT, NB, 4>), dim3((tiles + 1) / 2), dim3(256), 0, stream, w, x, y, ldy, rows);
+}
+
+template <int NB>
+bool launch_tiled_nb(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                     hipStream_t stream)
+{
+    switch (m) {
+    case 2: launch_tiled_typed<2, NB>(w, x, y, ldy, rows, stream); return true;
+    case 3: launch_tiled_typed<3, NB>(w, x, y, ldy, rows, stream); return true;
+    case 4: launch_tiled_typed<4, NB>(w, x, y, ldy, rows, stream); return true;
+    case 5: launch_tiled_typed<5, NB>(w, x, y, ldy, rows, stream); return true;
+    case 6: launch_tiled_typed<6, NB>(w, x, y, ldy, rows, stream); return true;
+    case 7: launch_tiled_typed<7, NB>(w, x, y, ldy, rows, stream); return true;
+    case 8: launch_tiled_typed<8, NB>(w, x, y, ldy, rows, stream); return true;
+    default: return false;
+    }
+}
+
+}  // namespace
+
+/* Enqueue y[t * ldy + row] = W_row . x_t (t < m) from the tiled copy; the
+ * row widths of the Qwen3.8 matrices (5120, 6144, 10240, 17408) and 2..8
+ * tokens are supported, false otherwise. */
+bool launch_gemm_q4k_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                           uint32_t nb, hipStream_t stream)
+{
+    if (!rows || ldy < rows) return false;
+    switch (nb) {
+    case 20: return launch_tiled_nb<20>(m, w_tiled, x, y, ldy, rows, stream);
+    case 24: return launch_tiled_nb<24>(m, w_tiled, x, y, ldy, rows, stream);
+    case 40: return launch_tiled_nb<40>(m, w_tiled, x, y, ldy, rows, stream);
+    case 68: return launch_tiled_nb<68>(m, w_tiled, x, y, ldy, rows, stream);
+    default: return false;
+    }
+}
+
+}  // namespace q38

@@ -49,6 +49,7 @@ def make_tensor(data_ptr, qtype, width, rows, nbytes=0):
 # Every symbol the C header declares (tests check the library exports them).
 EXPORTS = ("q38_f16_to_f32", "q38_quantize_q8_k", "q38_tensor_gemv_q8_k", "q38_tensor_gemm_q8_k",
            "q38hip_quantize_q8_k", "q38hip_gemm_q8_k", "q38hip_argmax", "q38hip_accept",
+           "q38hip_tiled_q4k_bytes", "q38hip_repack_q4k_tiles", "q38hip_gemm_q8_k_tiled",
            "q38hip_last_error", "q38hip_synchronize",
            "q38_model_open_gguf", "q38_model_attach_mtp_gguf", "q38_model_close", "q38_model_reset",
            "q38_model_forward_token", "q38_model_prefill", "q38_model_enable_mtp", "q38_model_mtp_forward",
@@ -69,6 +70,10 @@ def load_library(path=LIB_PATH):
     lib.q38_tensor_gemm_q8_k.argtypes = [vp, vp, u32, u64, ctypes.POINTER(GGUFTensor)]
     lib.q38hip_quantize_q8_k.argtypes = [vp, vp, u64, u32, vp]
     lib.q38hip_gemm_q8_k.argtypes = [vp, vp, u32, u64, ctypes.POINTER(GGUFTensor), vp]
+    lib.q38hip_tiled_q4k_bytes.restype = u64
+    lib.q38hip_tiled_q4k_bytes.argtypes = [u32, u64]
+    lib.q38hip_repack_q4k_tiles.argtypes = [vp, vp, u32, u64, vp]
+    lib.q38hip_gemm_q8_k_tiled.argtypes = [vp, vp, u32, u64, vp, u32, vp]
     lib.q38hip_argmax.argtypes = [vp, vp, u32, u32, vp]
     lib.q38hip_accept.argtypes = [vp, vp, vp, u32, vp]
     lib.q38hip_last_error.restype = ctypes.c_char_p
@@ -133,6 +138,28 @@ def gemm_q8_k(weights, qtype, width, rows, xq, batch, out=None):
     tensor = make_tensor(weights.data_ptr(), qtype, width, rows, weights.numel())
     _check(lib().q38hip_gemm_q8_k(_dev_ptr(out), _dev_ptr(xq), batch, width, ctypes.byref(tensor),
                                   _stream()), "q38hip_gemm_q8_k")
+    return out
+
+
+def repack_q4k_tiles(weights, width, rows):
+    """weights: uint8 row-major Q4_K rows on the GPU -> uint8 tiled copy."""
+    import torch
+    nbytes = int(lib().q38hip_tiled_q4k_bytes(rows, width))
+    if nbytes == 0:
+        raise ValueError("bad tiled shape")
+    out = torch.empty(nbytes, dtype=torch.uint8, device=weights.device)
+    _check(lib().q38hip_repack_q4k_tiles(_dev_ptr(out), _dev_ptr(weights), rows, width, _stream()),
+           "q38hip_repack_q4k_tiles")
+    return out
+
+
+def gemm_q8_k_tiled(tiled, width, rows, xq, batch, out=None):
+    """tiled: uint8 tiled Q4_K copy on the GPU; returns float32 [batch, rows]."""
+    import torch
+    if out is None:
+        out = torch.empty((batch, rows), dtype=torch.float32, device=tiled.device)
+    _check(lib().q38hip_gemm_q8_k_tiled(_dev_ptr(out), _dev_ptr(xq), batch, width, _dev_ptr(tiled), rows,
+                                        _stream()), "q38hip_gemm_q8_k_tiled")
     return out
 
 

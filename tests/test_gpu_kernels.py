@@ -151,3 +151,43 @@ def test_accept_matches_oracle(hip, oracle, device):
             assert (res[0], res[1], res[2]) == (consumed, matched, nxt)
             assert list(res[3:3 + consumed]) == list(accepted)
     torch.cuda.synchronize()
+
+
+def tiled_numpy(w, rows, width):
+    """Host restatement of the 16-row tiled layout: [tile][block][row % 16][144]."""
+    nb = width // 256
+    tiles = (rows + 15) // 16
+    padded = np.zeros((tiles * 16, nb, 144), dtype=np.uint8)
+    padded[:rows] = w.reshape(rows, nb, 144)
+    return np.ascontiguousarray(padded.reshape(tiles, 16, nb, 144).transpose(0, 2, 1, 3)).reshape(-1)
+
+
+@pytest.mark.parametrize("rows,width", [(1000, 5120), (48, 5120), (2064, 6144), (520, 10240), (1040, 17408)])
+def test_tiled_repack_and_gemm_bit_exact(hip, oracle, device, rows, width):
+    """Tiled Q4_K copy (2..8 tokens, matrix cores) equals the oracle bit for bit;
+    the repack equals the host restatement of the layout (zero-padded tail)."""
+    w = synth.matrix(Q4_K, rows, width, seed=rows + width)
+    wd = to_dev(w, device)
+    tiled = hip.repack_q4k_tiles(wd, width, rows)
+    assert tiled.cpu().numpy().tobytes() == tiled_numpy(w, rows, width).tobytes()
+    x = synth.activations(width, seed=rows * 3 + 1, count=8)
+    q = oracle.quantize(x.reshape(-1))
+    xq = hip.quantize_q8_k(to_dev(x, device))
+    nb = width // 256
+    for m in range(2, 9):
+        want = oracle.gemm(Q4_K, w, rows, q[:m * nb], m)
+        got = hip.gemm_q8_k_tiled(tiled, width, rows, xq[:m * nb * 292], m).cpu().numpy()
+        assert np.array_equal(bits(got), bits(want)), "M=%d" % m
+
+
+@pytest.mark.parametrize("m", [2, 3, 4, 8])
+def test_tiled_gemm_full_shape_matches_row_major(hip, device, m):
+    """34816x5120 (fused gate|up) and 5120x17408 (down): tiled = row-major kernels."""
+    for rows, width in ((34816, 5120), (5120, 17408)):
+        w = synth.matrix(Q4_K, rows, width, seed=m + rows)
+        wd = to_dev(w, device)
+        x = synth.activations(width, seed=m * 7 + width, count=m)
+        xq = hip.quantize_q8_k(to_dev(x, device))
+        want = hip.gemm_q8_k(wd, Q4_K, width, rows, xq, m).cpu().numpy()
+        got = hip.gemm_q8_k_tiled(hip.repack_q4k_tiles(wd, width, rows), width, rows, xq, m).cpu().numpy()
+        assert np.array_equal(bits(got), bits(want)), (rows, width)
