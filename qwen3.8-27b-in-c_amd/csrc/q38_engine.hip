@@ -946,21 +946,18 @@ bool linear_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count
         trace(m, "dn_beta_proj-", layer, m->wide0 + g.first[2], kVHeads);
         trace(m, "dn_alpha_proj-", layer, m->wide0 + g.first[3], kVHeads);
     }
-    for (uint32_t t = 0; t < count; ++t) {
-        float *qkv = m->wide0 + (size_t)t * ld, *attn = m->attn + (size_t)t * kLinV;
-        float *beta = qkv + g.first[2], *alpha = qkv + g.first[3];
-        q38::launch_deltanet_prep(qkv, beta, alpha, m->conv_state + (size_t)r * kQKV * 3, (long long)conv_count(),
-                                  s.params + 1 + r, (int)t, L.conv.f32(), L.a.f32(), L.dt.f32(), m->stream);
-        if (tr) {
-            trace(m, "dn_qkv-", layer, qkv, kQKV);
-            trace(m, "dn_beta-", layer, beta, kVHeads);
-            trace(m, "dn_alpha-", layer, alpha, kVHeads);
-        }
-        q38::launch_deltanet_state(attn, m->delta_state + (size_t)r * kVHeads * kHeadDim * kHeadDim,
-                                   (long long)delta_count(), s.params + 1 + r, (int)t, qkv, beta, alpha,
-                                   m->query_scale, m->stream);
-        if (tr) trace(m, "dn_core-", layer, attn, kLinV);
+    float *conv = m->conv_state + (size_t)r * kQKV * 3;
+    float *delta = m->delta_state + (size_t)r * kVHeads * kHeadDim * kHeadDim;
+    q38::launch_deltanet_prep(m->wide0, ld, (int)g.first[2], (int)g.first[3], conv, (long long)conv_count(),
+                              s.params + 1 + r, (int)count, L.conv.f32(), L.a.f32(), L.dt.f32(), m->stream);
+    if (tr) {
+        trace(m, "dn_qkv-", layer, m->wide0, kQKV);
+        trace(m, "dn_beta-", layer, m->wide0 + g.first[2], kVHeads);
+        trace(m, "dn_alpha-", layer, m->wide0 + g.first[3], kVHeads);
     }
+    q38::launch_deltanet_state(m->attn, delta, (long long)delta_count(), s.params + 1 + r, (int)count, m->wide0, ld,
+                               (int)g.first[2], (int)g.first[3], m->query_scale, m->stream);
+    if (tr) trace(m, "dn_core-", layer, m->attn, kLinV);
     q38::launch_deltanet_out_quant(m->attn, m->q8k, m->wide0 + g.first[1], ld, L.ssm_norm.f32(), (int)count,
                                    m->stream);
     if (tr) trace(m, "dn_gated-", layer, m->attn, kLinV);

@@ -50,11 +50,11 @@ void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int 
  * floats apart: row t of a batch reads slot (*slot + t) and writes slot
  * (*slot + t + 1), both mod kRecurrentStateSlots, so the state after any
  * prefix of the batch stays available. */
-void launch_deltanet_prep(float *qkv, float *beta, float *alpha, float *conv_state, long long slot_stride,
-                          const uint32_t *slot, int row, const float *conv_w, const float *ssm_a, const float *ssm_dt,
-                          hipStream_t stream);
-void launch_deltanet_state(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int row,
-                           const float *qkv, const float *beta, const float *alpha, float query_scale,
+void launch_deltanet_prep(float *qkv, long long ld, int beta_off, int alpha_off, float *conv_state,
+                          long long slot_stride, const uint32_t *slot, int rows, const float *conv_w,
+                          const float *ssm_a, const float *ssm_dt, hipStream_t stream);
+void launch_deltanet_state(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,
+                           const float *qkv, long long ld, int beta_off, int alpha_off, float query_scale,
                            hipStream_t stream);
 void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, long long z_stride, const float *ssm_norm,
                                int rows, hipStream_t stream);

@@ -96,7 +96,10 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float *__restrict__ nor
     constexpr int N = 1024 * NV;
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float *h = hidden + (long long)row * in_stride;
-    float4 x[NV];
+    /* the weights do not depend on the row: load them with the row */
+    const float4 *w4 = reinterpret_cast<const float4 *>(weight);
+    float4 w[NV], x[NV];
+    for (int j = 0; j < NV; ++j) w[j] = w4[tid + 256 * j];
     for (int j = 0; j < NV; ++j) x[j] = reinterpret_cast<const float4 *>(h)[tid + 256 * j];
     if (ADD) {
         const float4 *b = reinterpret_cast<const float4 *>(branch + (long long)row * in_stride);
@@ -118,14 +121,12 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float *__restrict__ nor
     }
     const float mean = block_sum_finish<256>(s, h, N, MeanPost{(double)N});
     const float scale = rms_scale(mean);
-    const float4 *w4 = reinterpret_cast<const float4 *>(weight);
     for (int j = 0; j < NV; ++j) {
-        const float4 w = w4[tid + 256 * j];
         float v[4];
-        v[0] = __fmul_rn(__fmul_rn(x[j].x, scale), w.x);
-        v[1] = __fmul_rn(__fmul_rn(x[j].y, scale), w.y);
-        v[2] = __fmul_rn(__fmul_rn(x[j].z, scale), w.z);
-        v[3] = __fmul_rn(__fmul_rn(x[j].w, scale), w.w);
+        v[0] = __fmul_rn(__fmul_rn(x[j].x, scale), w[j].x);
+        v[1] = __fmul_rn(__fmul_rn(x[j].y, scale), w[j].y);
+        v[2] = __fmul_rn(__fmul_rn(x[j].z, scale), w[j].z);
+        v[3] = __fmul_rn(__fmul_rn(x[j].w, scale), w[j].w);
         if (norm_out)
             reinterpret_cast<float4 *>(norm_out + (long long)row * norm_stride)[tid + 256 * j] =
                 make_float4(v[0], v[1], v[2], v[3]);
@@ -204,52 +205,64 @@ constexpr uint32_t kStateSlots = kRecurrentStateSlots;
 
 /* Causal conv (4 taps, state of 3 per channel), SiLU, per-head L2 norm of q
  * and k, and the beta / alpha transforms (q38_linear_core,
- * qwen38_model.c:720-757).  Blocks 0..79 each own 128 channels (blocks 0..31
- * are the 16 q heads and 16 k heads); block 80 does beta/alpha.
- * The conv state of row `row` is read from slot (*slot_ptr + row) and the
- * shifted state written to the next slot (mod kStateSlots). */
-__global__ __launch_bounds__(128) void deltanet_prep_kernel(float *__restrict__ qkv, float *__restrict__ conv_state,
+ * qwen38_model.c:720-757) for `rows` consecutive tokens.  Row t's
+ * projections are at qkv + t * ld (q, k, v, then beta at + beta_off and
+ * alpha at + alpha_off) and are transformed in place.  Blocks 0..79 each own
+ * 128 channels (blocks 0..31 are the 16 q heads and 16 k heads); block 80
+ * does beta/alpha.  The conv state before row t is slot (*slot_ptr + t) (mod
+ * kStateSlots); each row's shifted state is written to the next slot, and
+ * the chain between rows stays in registers. */
+__global__ __launch_bounds__(128) void deltanet_prep_kernel(float *__restrict__ qkv, long long ld, int beta_off,
+                                                            int alpha_off, float *__restrict__ conv_state,
                                                             long long slot_stride,
-                                                            const uint32_t *__restrict__ slot_ptr, int row,
+                                                            const uint32_t *__restrict__ slot_ptr, int rows,
                                                             const float *__restrict__ conv_w,
-                                                            float *__restrict__ beta, float *__restrict__ alpha,
                                                             const float *__restrict__ ssm_a,
                                                             const float *__restrict__ ssm_dt)
 {
     const int tid = threadIdx.x;
     if (blockIdx.x == kQKV / 128) {
         if (tid < kVHeads) {
-            beta[tid] = sigmoidf_exact(beta[tid]);
-            alpha[tid] = __fmul_rn(ssm_a[tid], softplusf_exact(__fadd_rn(alpha[tid], ssm_dt[tid])));
+            for (int t = 0; t < rows; ++t) {
+                float *beta = qkv + (long long)t * ld + beta_off, *alpha = qkv + (long long)t * ld + alpha_off;
+                beta[tid] = sigmoidf_exact(beta[tid]);
+                alpha[tid] = __fmul_rn(ssm_a[tid], softplusf_exact(__fadd_rn(alpha[tid], ssm_dt[tid])));
+            }
         }
         return;
     }
     const int ch = blockIdx.x * 128 + tid;
-    const uint32_t slot = *slot_ptr + row;
-    const float *st = conv_state + (size_t)(slot % kStateSlots) * slot_stride + (size_t)ch * 3;
-    float *st_out = conv_state + (size_t)((slot + 1) % kStateSlots) * slot_stride + (size_t)ch * 3;
-    const float *k = conv_w + (size_t)ch * 4;
-    const float x = qkv[ch];
-    const float s0 = st[0], s1 = st[1], s2 = st[2];
-    float value = 0.0f;
-    value = __fadd_rn(value, __fmul_rn(s0, k[0]));
-    value = __fadd_rn(value, __fmul_rn(s1, k[1]));
-    value = __fadd_rn(value, __fmul_rn(s2, k[2]));
-    value = __fadd_rn(value, __fmul_rn(x, k[3]));
-    st_out[0] = s1;
-    st_out[1] = s2;
-    st_out[2] = x;
-    const float y = siluf_exact(value);
-    if (ch >= 2 * kQKDim) {
-        qkv[ch] = y;
-        return;
-    }
+    const uint32_t slot0 = *slot_ptr;
+    const float *st = conv_state + (size_t)(slot0 % kStateSlots) * slot_stride + (size_t)ch * 3;
+    const float4 k = reinterpret_cast<const float4 *>(conv_w)[ch];
+    float s0 = st[0], s1 = st[1], s2 = st[2];
     __shared__ float head[128];
-    head[tid] = y;
-    __syncthreads();
-    const float sum = block_sum_squares<128>(head, 128, FloatPost{});
-    const float scale = div_rn(1.0f, fmaxf(sqrt_rn(sum), 1e-6f));
-    qkv[ch] = __fmul_rn(y, scale);
+    for (int t = 0; t < rows; ++t) {
+        float *row = qkv + (long long)t * ld;
+        const float x = row[ch];
+        float value = 0.0f;
+        value = __fadd_rn(value, __fmul_rn(s0, k.x));
+        value = __fadd_rn(value, __fmul_rn(s1, k.y));
+        value = __fadd_rn(value, __fmul_rn(s2, k.z));
+        value = __fadd_rn(value, __fmul_rn(x, k.w));
+        s0 = s1;
+        s1 = s2;
+        s2 = x;
+        float *st_out = conv_state + (size_t)((slot0 + t + 1) % kStateSlots) * slot_stride + (size_t)ch * 3;
+        st_out[0] = s0;
+        st_out[1] = s1;
+        st_out[2] = s2;
+        const float y = siluf_exact(value);
+        if (blockIdx.x >= 2 * kQKDim / 128) {
+            row[ch] = y;
+            continue;
+        }
+        head[tid] = y;
+        __syncthreads();
+        const float sum = block_sum_squares<128>(head, 128, FloatPost{});
+        const float scale = div_rn(1.0f, fmaxf(sqrt_rn(sum), 1e-6f));
+        row[ch] = __fmul_rn(y, scale);
+    }
 }
 
 /* Sum of 32 per-lane values in the reference's AVX2 reduction order
@@ -272,45 +285,53 @@ __device__ __forceinline__ float avx2_tree32(float v)
  * S_c = fma(k, delta, S_c); out[c] = dot(S_c, q) * (1/sqrt(128)).
  * Columns are independent: 32 lanes per column (lane l owns elements
  * l, l+32, l+64, l+96, the reference's fixed 4 x 8-lane accumulators), two
- * columns per wavefront, eight per block of 256.  The state of row `row` is
- * read from slot (*slot_ptr + row) and written to the next slot. */
+ * columns per wavefront, eight per block of 256.  The column runs through
+ * `rows` consecutive tokens (row t's prepared q|k|v at qkv + t * ld, beta
+ * and alpha at + beta_off / alpha_off, output at out + t * kLinV): the
+ * state before row t is slot (*slot_ptr + t), read once, kept in registers,
+ * and each row's result is written to the next slot. */
 __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__ out, float *__restrict__ state,
                                                              long long slot_stride,
-                                                             const uint32_t *__restrict__ slot_ptr, int row,
-                                                             const float *__restrict__ qkv,
-                                                             const float *__restrict__ beta,
-                                                             const float *__restrict__ alpha, float query_scale)
+                                                             const uint32_t *__restrict__ slot_ptr, int rows,
+                                                             const float *__restrict__ qkv, long long ld,
+                                                             int beta_off, int alpha_off, float query_scale)
 {
     const int column_global = blockIdx.x * 8 + (threadIdx.x >> 5);   /* 0 .. 48*128-1 */
     const int h = column_global >> 7;
     const int c = column_global & 127;
     const int l = threadIdx.x & 31;
     const int kh = h % 16;
-    const float *q = qkv + kh * kHeadDim;
-    const float *k = qkv + kQKDim + kh * kHeadDim;
-    const float *v = qkv + 2 * kQKDim + h * kHeadDim;
-    const uint32_t slot = *slot_ptr + row;
-    const float *s = state + (size_t)(slot % kStateSlots) * slot_stride + ((size_t)h * kHeadDim + c) * kHeadDim;
-    float *s_out = state + (size_t)((slot + 1) % kStateSlots) * slot_stride + ((size_t)h * kHeadDim + c) * kHeadDim;
-    const float decay = q38_expf(alpha[h]);
-    float sv[4], kv[4], qv[4];
-    for (int a = 0; a < 4; ++a) {
-        sv[a] = __fmul_rn(s[32 * a + l], decay);
-        kv[a] = k[32 * a + l];
-        qv[a] = q[32 * a + l];
+    const uint32_t slot0 = *slot_ptr;
+    const size_t col_off = ((size_t)h * kHeadDim + c) * kHeadDim;
+    const float *s = state + (size_t)(slot0 % kStateSlots) * slot_stride + col_off;
+    float sv[4];
+    for (int a = 0; a < 4; ++a) sv[a] = s[32 * a + l];
+    for (int t = 0; t < rows; ++t) {
+        const float *row = qkv + (long long)t * ld;
+        const float *q = row + kh * kHeadDim;
+        const float *k = row + kQKDim + kh * kHeadDim;
+        const float *v = row + 2 * kQKDim + h * kHeadDim;
+        const float decay = q38_expf(row[alpha_off + h]);
+        float kv[4], qv[4];
+        for (int a = 0; a < 4; ++a) {
+            sv[a] = __fmul_rn(sv[a], decay);
+            kv[a] = k[32 * a + l];
+            qv[a] = q[32 * a + l];
+        }
+        float p = 0.0f;
+        for (int a = 0; a < 4; ++a) p = __builtin_fmaf(sv[a], kv[a], p);
+        const float pred = avx2_tree32(p);
+        const float delta = __fmul_rn(__fsub_rn(v[c], pred), row[beta_off + h]);
+        float *s_out = state + (size_t)((slot0 + t + 1) % kStateSlots) * slot_stride + col_off;
+        float r = 0.0f;
+        for (int a = 0; a < 4; ++a) {
+            sv[a] = __builtin_fmaf(kv[a], delta, sv[a]);
+            s_out[32 * a + l] = sv[a];
+            r = __builtin_fmaf(sv[a], qv[a], r);
+        }
+        const float result = avx2_tree32(r);
+        if (l == 0) out[(size_t)t * kLinV + h * kHeadDim + c] = __fmul_rn(result, query_scale);
     }
-    float p = 0.0f;
-    for (int a = 0; a < 4; ++a) p = __builtin_fmaf(sv[a], kv[a], p);
-    const float pred = avx2_tree32(p);
-    const float delta = __fmul_rn(__fsub_rn(v[c], pred), beta[h]);
-    float r = 0.0f;
-    for (int a = 0; a < 4; ++a) {
-        sv[a] = __builtin_fmaf(kv[a], delta, sv[a]);
-        s_out[32 * a + l] = sv[a];
-        r = __builtin_fmaf(sv[a], qv[a], r);
-    }
-    const float result = avx2_tree32(r);
-    if (l == 0) out[h * kHeadDim + c] = __fmul_rn(result, query_scale);
 }
 
 /* Per value head: RMSNorm over 128 (ssm_norm weight), then out *= silu(z)
@@ -552,20 +573,20 @@ void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int 
     embed_q4k_kernel<<<dim3(width / 256, count), 256, 0, stream>>>(out, w, tokens, width / 256, vocab);
 }
 
-void launch_deltanet_prep(float *qkv, float *beta, float *alpha, float *conv_state, long long slot_stride,
-                          const uint32_t *slot, int row, const float *conv_w, const float *ssm_a, const float *ssm_dt,
-                          hipStream_t stream)
+void launch_deltanet_prep(float *qkv, long long ld, int beta_off, int alpha_off, float *conv_state,
+                          long long slot_stride, const uint32_t *slot, int rows, const float *conv_w,
+                          const float *ssm_a, const float *ssm_dt, hipStream_t stream)
 {
-    deltanet_prep_kernel<<<kQKV / 128 + 1, 128, 0, stream>>>(qkv, conv_state, slot_stride, slot, row, conv_w, beta,
-                                                             alpha, ssm_a, ssm_dt);
+    deltanet_prep_kernel<<<kQKV / 128 + 1, 128, 0, stream>>>(qkv, ld, beta_off, alpha_off, conv_state, slot_stride,
+                                                             slot, rows, conv_w, ssm_a, ssm_dt);
 }
 
-void launch_deltanet_state(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int row,
-                           const float *qkv, const float *beta, const float *alpha, float query_scale,
+void launch_deltanet_state(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,
+                           const float *qkv, long long ld, int beta_off, int alpha_off, float query_scale,
                            hipStream_t stream)
 {
-    deltanet_state_kernel<<<kVHeads * kHeadDim / 8, 256, 0, stream>>>(attn, delta_state, slot_stride, slot, row, qkv,
-                                                                     beta, alpha, query_scale);
+    deltanet_state_kernel<<<kVHeads * kHeadDim / 8, 256, 0, stream>>>(attn, delta_state, slot_stride, slot, rows,
+                                                                     qkv, ld, beta_off, alpha_off, query_scale);
 }
 
 void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, long long z_stride, const float *ssm_norm,
