@@ -43,6 +43,8 @@
 #include "q38_device.h"
 #include "q38_kernels.h"
 
+#include <cstdlib>
+
 namespace q38 {
 
 namespace {
@@ -74,26 +76,41 @@ struct Slot {
 
 }  // namespace
 
-/* 4 / 2 tiles per workgroup of 256 threads; P blocks in flight per wave. */
-template <int MT, int NB, int P>
-__global__ __launch_bounds__(256) void gemm_q4k_tiled(const uint8_t *__restrict__ w, const uint8_t *__restrict__ x,
-                                                       float *__restrict__ y, uint32_t ldy, uint32_t rows)
+/* TPW tiles per workgroup, 2 * S wavefronts per tile: wavefront (G, phase)
+ * owns AVX2 lanes 4G..4G+3 and the blocks b = phase (mod S), P of them in
+ * flight.
+ * With S > 1 every round of S blocks passes through a double-buffered LDS
+ * ring: each wavefront leaves its block's integer sums (and, in wavefront
+ * G = 0, the min sums and the block's d/dmin), and after a barrier the
+ * wavefronts (G, t mod S) advance token t's chains over the round's blocks
+ * in block order. */
+template <int MT, int NB, int S, int P, int TPW>
+__global__ __launch_bounds__(128 * S * TPW) void gemm_q4k_tiled(const uint8_t *__restrict__ w, const uint8_t *__restrict__ x,
+                                                           float *__restrict__ y, uint32_t ldy, uint32_t rows)
 {
-    constexpr int TS = (MT + 3) / 4;   /* MFMA token sets of four */
+    static_assert(NB % S == 0, "the blocks must split evenly over the wavefronts of a tile");
+    constexpr int TS = (MT + 3) / 4;            /* MFMA token sets of four */
+    constexpr int KB = NB / S;                  /* rounds */
+    constexpr int NT = (MT + S - 1) / S;        /* tokens whose chains a wavefront owns */
+    constexpr int RP = S > 1 ? 2 : 1;           /* ring parities */
     __shared__ int2 pairs_s[MT * NB * 4];
     __shared__ float xs_s[MT * NB];
-    __shared__ float xch[2][MT][64];
+    /* ring record of wavefront (G, phase): W per token, M per token, d|dmin */
+    __shared__ float ring_w[TPW][RP][S][2][MT][64];
+    __shared__ int ring_m[TPW][RP][S][2][MT][64];
+    __shared__ uint32_t ring_d[TPW][RP][S][2][64];
+    __shared__ float xch[TPW][MT][64];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    const int tl = wave >> 1, G = wave & 1;
+    const int G = wave & 1, phase = (wave >> 1) % S, tl = wave / (2 * S);
     const int r = lane & 15, q = lane >> 4, g = (lane >> 2) & 3, tk = lane & 3;
     const uint32_t ntiles = (rows + kTileRows - 1) / kTileRows;
-    const uint32_t tile = blockIdx.x * 2u + (uint32_t)tl;
-    const uint32_t tc = tile < ntiles ? tile : ntiles - 1;   /* idle waves re-read the last tile */
+    const uint32_t tile_raw = blockIdx.x * TPW + (uint32_t)tl;
+    const uint32_t tile = tile_raw < ntiles ? tile_raw : ntiles - 1;   /* idle waves re-read the last tile */
 
     /* uniform bases plus 32-bit per-lane offsets */
-    const uint8_t *tb = w + (size_t)tc * NB * kTileBlockBytes;
+    const uint8_t *tb = w + (size_t)tile * NB * kTileBlockBytes;
     const __amdgpu_buffer_rsrc_t wr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(tb), 0, NB * kTileBlockBytes, kBufferFlags);
     const __amdgpu_buffer_rsrc_t xr =
@@ -105,7 +122,19 @@ __global__ __launch_bounds__(256) void gemm_q4k_tiled(const uint8_t *__restrict_
         const int t = tk + 4 * s < MT ? tk + 4 * s : MT - 1;
         xoff[s] = (uint32_t)(t * NB * kQ8KBytes + 4 + 64 * q + 4 * (4 * G + g));
     }
-    auto load = [&](int b) {
+    /* this wavefront's k-th block (clamped: loads past the end re-read the
+     * last block and are never used) */
+    auto block_of = [&](int k) {
+        const int b = phase + S * k;
+        return b < NB ? b : NB - 1;
+    };
+    /* tokens owned: t_j = phase + S * j (clamped; chains of t_j >= MT are
+     * computed and dropped, which keeps the loop free of branches) */
+    int own[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) own[j] = phase + S * j < MT ? phase + S * j : MT - 1;
+    auto load = [&](int k) {
+        const int b = block_of(k);
         Slot sl;
         const int4v h = __builtin_amdgcn_raw_buffer_load_b128(wr, hoff, b * kTileBlockBytes, 0);
         const int4v qv = __builtin_amdgcn_raw_buffer_load_b128(wr, qoff, b * kTileBlockBytes, 0);
@@ -120,53 +149,75 @@ __global__ __launch_bounds__(256) void gemm_q4k_tiled(const uint8_t *__restrict_
     };
     Slot ring[P];
 #pragma unroll
-    for (int i = 0; i < P; ++i) ring[i] = load(i < NB ? i : NB - 1);
+    for (int i = 0; i < P; ++i) ring[i] = load(i);
 
-    /* activation scales and min pair sums: Q8_K dword 0 and bsum dwords 65..72 */
+    /* activation scales and min pair sums: Q8_K dword 0 and bsum dwords
+     * 65..72, loaded in batches of eight per thread (indices past the end are
+     * clamped and their values dropped) so the loads overlap */
     {
-        const uint32_t *src = reinterpret_cast<const uint32_t *>(x);
-        for (int i = threadIdx.x; i < MT * NB * 9; i += 256) {
-            const int blk = i / 9, k = i - blk * 9;
-            const uint32_t v = src[(size_t)blk * 73 + (k == 0 ? 0 : 64 + k)];
-            if (k == 0) xs_s[blk] = __uint_as_float(v);
-            else reinterpret_cast<int *>(pairs_s)[blk * 8 + (k - 1)] = (int)(int16_t)(v & 0xffffu) + ((int)v >> 16);
+        constexpr int kTotal = MT * NB * 9, kThreads = 128 * S * TPW, kDepth = 8;
+        const __amdgpu_buffer_rsrc_t sr =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(x), 0, MT * NB * kQ8KBytes, kBufferFlags);
+        for (int i0 = threadIdx.x; i0 < kTotal; i0 += kDepth * kThreads) {
+            uint32_t v[kDepth];
+#pragma unroll
+            for (int u = 0; u < kDepth; ++u) {
+                const int i = i0 + u * kThreads < kTotal ? i0 + u * kThreads : kTotal - 1;
+                const int blk = i / 9, k = i - blk * 9;
+                v[u] = __builtin_amdgcn_raw_buffer_load_b32(sr, (uint32_t)(blk * kQ8KBytes + (k == 0 ? 0 : 256 + 4 * k)), 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < kDepth; ++u) {
+                const int i = i0 + u * kThreads;
+                if (i >= kTotal) break;
+                const int blk = i / 9, k = i - blk * 9;
+                if (k == 0) xs_s[blk] = __uint_as_float(v[u]);
+                else reinterpret_cast<int *>(pairs_s)[blk * 8 + (k - 1)] =
+                    (int)(int16_t)(v[u] & 0xffffu) + ((int)v[u] >> 16);
+            }
         }
     }
     __syncthreads();
 
-    float acc[MT], accm[MT];
+    /* S == 1: chains of every token; S > 1: of the owned tokens */
+    constexpr int NC = S == 1 ? MT : NT;
+    float acc[NC], accm[NC];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = accm[t] = 0.0f;
+    for (int t = 0; t < NC; ++t) acc[t] = accm[t] = 0.0f;
 
     /* loop-invariant per-lane values (the masks live in registers: VOP3
      * forms cannot take two literals) */
-    uint32_t kMask = 0x000f000fu, kMagic = 0x64006400u;
-    asm volatile("" : "+v"(kMask), "+v"(kMagic));
+    uint32_t kMask = 0x000f000fu, kMaskHi = 0x00f000f0u, kMagic = 0x64006400u;
+    asm volatile("" : "+v"(kMask), "+v"(kMaskHi), "+v"(kMagic));
     const int sh = (q & 1) * 16;
     const bool hi_chunk = q >= 2, q_odd = (q & 1) != 0;
     const uint32_t kLow = hi_chunk ? 0x0f0f0f0fu : 0x3f3f3f3fu, kHigh = hi_chunk ? 0x30303030u : 0u;
 
-    auto step = [&](const Slot &c, int b) {
+    /* integer sums of one block: W[b][4G + q] per token into wv[], and in
+     * wavefront 0 the min sums M[b][q] into mv[] */
+    auto block_sums = [&](const Slot &c, int b, float (&wv)[MT], int (&mv)[MT]) {
         const uint32_t Y = c.h.y, Z = c.h.z, Wd = c.h.w;
         /* 6-bit scales of sub-blocks 2q, 2q+1 (src/qwen38/qwen38_quant.c:131-143) */
         const uint32_t scw = ((hi_chunk ? Wd : Y) & kLow) | ((Y >> 2) & kHigh);
+        /* low nibbles sit in bits 0..3 of each half: fp16 1024 + n, times sc,
+         * minus 1024 sc.  High nibbles are taken in place from bits 4..7:
+         * fp16 1024 + 16 n, times sc / 16, minus 64 sc.  Both products and
+         * sums are exact (sc / 16 and 64 sc are exact in fp16). */
         const half2v SL = pair_of((scw >> sh) & 0xffu), SH = pair_of((scw >> (sh + 8)) & 0xffu);
         const half2v k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-        const half2v NL = SL * k1024, NH = SH * k1024;
-        const float d = f16_to_f32(c.h.x), dmin = f16_to_f32(c.h.x >> 16);
-        float dw[MT];
-#pragma unroll
-        for (int t = 0; t < MT; ++t) dw[t] = fmul_rn(d, xs_s[t * NB + b]);
+        const half2v k16th = {(_Float16)0.0625f, (_Float16)0.0625f};
+        const half2v k64 = {(_Float16)-64.0f, (_Float16)-64.0f};
+        const half2v NL = SL * k1024, SH16 = SH * k16th, NH = SH * k64;
         half8 bv[4];
         const uint32_t qw[4] = {c.qd.x, c.qd.y, c.qd.z, c.qd.w};
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             /* element order per half: u = 0, 2, 1, 3 (the activations use the same) */
-            const uint32_t wd = qw[p];
+            const uint32_t wd = qw[p], w8 = wd >> 8;
             const half2v b0 = __builtin_elementwise_fma(as_h2((wd & kMask) | kMagic), SL, NL);
-            const half2v b1 = __builtin_elementwise_fma(as_h2(((wd >> 8) & kMask) | kMagic), SL, NL);
-            const half2v b2 = __builtin_elementwise_fma(as_h2(((wd >> 4) & kMask) | kMagic), SH, NH);
-            const half2v b3 = __builtin_elementwise_fma(as_h2(((wd >> 12) & kMask) | kMagic), SH, NH);
+            const half2v b1 = __builtin_elementwise_fma(as_h2((w8 & kMask) | kMagic), SL, NL);
+            const half2v b2 = __builtin_elementwise_fma(as_h2((wd & kMaskHi) | kMagic), SH16, NH);
+            const half2v b3 = __builtin_elementwise_fma(as_h2((w8 & kMaskHi) | kMagic), SH16, NH);
             bv[p][0] = b0[0]; bv[p][1] = b0[1]; bv[p][2] = b1[0]; bv[p][3] = b1[1];
             bv[p][4] = b2[0]; bv[p][5] = b2[1]; bv[p][6] = b3[0]; bv[p][7] = b3[1];
         }
@@ -192,56 +243,94 @@ __global__ __launch_bounds__(256) void gemm_q4k_tiled(const uint8_t *__restrict_
                 if (t >= MT) break;
                 /* the diagonal: lane (r, q) takes D_q */
                 const float w01 = q_odd ? D[1][j] : D[0][j], w23 = q_odd ? D[3][j] : D[2][j];
-                acc[t] = __builtin_fmaf(dw[t], hi_chunk ? w23 : w01, acc[t]);
+                wv[t] = hi_chunk ? w23 : w01;
             }
         }
-        if (G == 0) {
-            /* 6-bit mins of sub-blocks 2q, 2q+1 */
-            const uint32_t mw = ((hi_chunk ? (Wd >> 4) : Z) & kLow) | ((Z >> 2) & kHigh);
-            const int m0 = (int)((mw >> sh) & 0xffu), m1 = (int)((mw >> (sh + 8)) & 0xffu);
+        /* 6-bit mins of sub-blocks 2q, 2q+1 (both wavefronts compute them,
+         * which keeps the loop free of branches; only wavefront 0's min
+         * chains are used) */
+        const uint32_t mw = ((hi_chunk ? (Wd >> 4) : Z) & kLow) | ((Z >> 2) & kHigh);
+        const int m0 = (int)((mw >> sh) & 0xffu), m1 = (int)((mw >> (sh + 8)) & 0xffu);
 #pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const int2 pr = pairs_s[(t * NB + b) * 4 + q];
-                const int M = mad24(m0, pr.x, mul24(m1, pr.y));
-                accm[t] = __builtin_fmaf(-fmul_rn(dmin, xs_s[t * NB + b]), (float)M, accm[t]);
-            }
+        for (int t = 0; t < MT; ++t) {
+            const int2 pr = pairs_s[(t * NB + b) * 4 + q];
+            mv[t] = mad24(m0, pr.x, mul24(m1, pr.y));
+        }
+    };
+    /* chain slot j (token t) for block b with d, dmin of the block */
+    auto chain = [&](int j, int t, int b, float d, float dmin, float wq, int mq) {
+        const float xs = xs_s[t * NB + b];
+        acc[j] = __builtin_fmaf(fmul_rn(d, xs), wq, acc[j]);
+        accm[j] = __builtin_fmaf(-fmul_rn(dmin, xs), (float)mq, accm[j]);
+    };
+
+    auto round = [&](const Slot &c, int k) {
+        const int b = phase + S * k;
+        float wv[MT];
+        int mv[MT];
+        block_sums(c, b, wv, mv);
+        if (S == 1) {
+            const float d = f16_to_f32(c.h.x), dmin = f16_to_f32(c.h.x >> 16);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) chain(t, t, b, d, dmin, wv[t], mv[t]);
+            return;
+        }
+        const int par = k & 1;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            ring_w[tl][par][phase][G][t][lane] = wv[t];
+            ring_m[tl][par][phase][G][t][lane] = mv[t];
+        }
+        ring_d[tl][par][phase][G][lane] = c.h.x;
+        __syncthreads();
+#pragma unroll
+        for (int f = 0; f < S; ++f) {
+            const int b2 = f + S * k;
+            const uint32_t dpair = ring_d[tl][par][f][G][lane];
+            const float d = f16_to_f32(dpair), dmin = f16_to_f32(dpair >> 16);
+#pragma unroll
+            for (int j = 0; j < NC; ++j)
+                chain(j, own[j], b2, d, dmin, ring_w[tl][par][f][G][own[j]][lane], ring_m[tl][par][f][0][own[j]][lane]);
         }
     };
 
-    constexpr int kFull = NB / P, kRem = NB % P;
+    constexpr int kFull = KB / P, kRem = KB % P;   /* rounds in ring-sized groups, then the rest */
 #pragma unroll 1
     for (int it = 0; it < kFull; ++it) {
 #pragma unroll
         for (int i = 0; i < P; ++i) {
-            const int b = it * P + i;
-            step(ring[i], b);
-            /* refill the slot after its last use (loads past the end re-read
-             * the last block and are never used) */
-            ring[i] = load(b + P < NB ? b + P : NB - 1);
+            const int k = it * P + i;
+            round(ring[i], k);
+            /* refill the slot after its last use */
+            ring[i] = load(k + P);
         }
     }
 #pragma unroll
-    for (int i = 0; i < kRem; ++i) step(ring[i], NB - kRem + i);
+    for (int i = 0; i < kRem; ++i) round(ring[i], KB - kRem + i);
 
-    /* wavefront 1 hands AVX2 lanes 4..7 to wavefront 0, which applies the
-     * reference's trees: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)), then
-     * ((m0+m2)+(m1+m3)) (qwen38_quant.c:303-310, 1626-1630) */
+    /* the G = 1 owner of token t hands AVX2 lanes 4..7 to the G = 0 owner,
+     * which applies the reference's trees: ((a0+a4)+(a2+a6)) +
+     * ((a1+a5)+(a3+a7)), then ((m0+m2)+(m1+m3)) (qwen38_quant.c:303-310,
+     * 1626-1630) */
     if (G == 1) {
 #pragma unroll
-        for (int t = 0; t < MT; ++t) xch[tl][t][lane] = acc[t];
+        for (int j = 0; j < NC; ++j)
+            if (S == 1 || phase + S * j < MT) xch[tl][S == 1 ? j : own[j]][lane] = acc[j];
     }
     __syncthreads();
     if (G == 0) {
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            float v = fadd_rn(acc[t], xch[tl][t][lane]);
+        for (int j = 0; j < NC; ++j) {
+            const int t = S == 1 ? j : own[j];
+            if (S > 1 && phase + S * j >= MT) continue;
+            float v = fadd_rn(acc[j], xch[tl][t][lane]);
             v = fadd_rn(v, __shfl_xor(v, 32, 64));
             v = fadd_rn(v, __shfl_xor(v, 16, 64));
-            float m = accm[t];
+            float m = accm[j];
             m = fadd_rn(m, __shfl_xor(m, 32, 64));
             m = fadd_rn(m, __shfl_xor(m, 16, 64));
-            const uint32_t row = tile * kTileRows + (uint32_t)r;
-            if (q == 0 && tile < ntiles && row < rows) y[(size_t)t * ldy + row] = fadd_rn(v, m);
+            const uint32_t row = tile_raw * kTileRows + (uint32_t)r;
+            if (q == 0 && tile_raw < ntiles && row < rows) y[(size_t)t * ldy + row] = fadd_rn(v, m);
         }
     }
 }
@@ -282,11 +371,34 @@ bool launch_repack_q4k_tiles(uint8_t *dst, const uint8_t *src, uint32_t rows, ui
 
 namespace {
 
+/* Launch shape (measured on MI355X): with 5..8 tokens, two tiles of 2
+ * wavefronts per workgroup; with 2..4 tokens, each tile's blocks split over
+ * 2 wavefront pairs for tall matrices and 4 for short ones. */
+int tiled_shape(uint32_t tiles, int mt)
+{
+#ifdef Q38_TILED_SPLIT_ENV
+    if (const char *v = getenv("Q38_TILED_S")) return atoi(v);
+#endif
+    if (mt >= 5) return 12;
+    return tiles >= 768 ? 2 : 4;
+}
+
 template <int MT, int NB>
 void launch_tiled_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, hipStream_t stream)
 {
     const uint32_t tiles = (rows + kTileRows - 1) / kTileRows;
-    hipLaunchKernelGGL((gemm_q4k_tiled<MT, NB, 4>), dim3((tiles + 1) / 2), dim3(256), 0, stream, w, x, y, ldy, rows);
+    switch (tiled_shape(tiles, MT)) {
+    case 12:
+        hipLaunchKernelGGL((gemm_q4k_tiled<MT, NB, 1, 4, 2>), dim3((tiles + 1) / 2), dim3(256), 0, stream, w, x, y,
+                           ldy, rows);
+        break;
+    case 2:
+        hipLaunchKernelGGL((gemm_q4k_tiled<MT, NB, 2, 4, 1>), dim3(tiles), dim3(256), 0, stream, w, x, y, ldy, rows);
+        break;
+    default:
+        hipLaunchKernelGGL((gemm_q4k_tiled<MT, NB, 4, 4, 1>), dim3(tiles), dim3(512), 0, stream, w, x, y, ldy, rows);
+        break;
+    }
 }
 
 template <int NB>
