@@ -7,16 +7,19 @@ block; random-init weights from the seeded synthetic GGUF writer) with MTP
 draft length 3 through the engine ABI (q38_model_speculative_greedy): a
 512-token random prompt is prefilled, then 256 tokens are decoded.  A "step"
 is one speculative transaction; `value` is decoded tokens per second.
-The `roofline` object is that of the dominant kernel of the step, the
-Q4_K x Q8_K GEMV at 17408 x 5120 (FFN gate/up), timed in the same run.
+The `roofline` object is that of the dominant kernel of the step: the
+matrix-core Q4_K x Q8_K GEMM over the 16-row tiled weights at the verify
+batch's shape, 3 tokens x 34816 x 5120 (the fused FFN gate|up projection,
+64 launches per transaction), timed in the same run on its own with the
+weights rotated over >= 1 GiB of distinct copies.
 
-GEMV workloads (`q4k_gemv` ...): the GEMV alone, quantised activations
-resident in HBM, weights rotated over >= 1 GiB of distinct copies so every
-launch streams from HBM rather than the 256 MB last-level cache; a "step" is
-one launch.
+Kernel workloads (`q4k_gemv`, `q4k_tiled_m3` ...): one GEMV / GEMM alone,
+quantised activations resident in HBM, weights rotated over >= 1 GiB of
+distinct copies so every launch streams from HBM rather than the 256 MB
+last-level cache; a "step" is one launch.
 
 Prints one JSON line (see the fields below).  `roofline.achieved` is the
-algorithmic bytes of one GEMV launch divided by its average duration measured
+algorithmic bytes of one launch divided by its average duration measured
 with HIP events on the stream the kernels run on.  `roofline.traffic` is the
 HBM bytes per launch read from the committed counter summary
 profiles/<kernel>.<workload>.pmc.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated
@@ -27,6 +30,11 @@ more distinct copies than the host caches hold.
 
 `--workload copy` times a plain device-to-device copy of 64 MiB buffers; it
 is the calibration run for the memory counters, not a bench line.
+
+`--trace-summary DIR` prints, from a rocprofv3 `--kernel-trace --output-format
+csv` directory, the calls and average / min / max duration of every kernel
+per launch grid (one kernel name serves several matrix shapes; the grid tells
+them apart), and exits.
 """
 import argparse
 import glob
@@ -44,12 +52,14 @@ sys.path.insert(0, os.path.join(ROOT, "qwen3.8-27b-in-c_amd"))
 PEAK_HBM_GBS = 8000.0
 
 WORKLOADS = {
-    # name: (type, rows, width, label)
-    "q4k_gemv": (12, 17408, 5120, "Q4_K GEMV 17408x5120"),
-    "q4k_gemv_t": (12, 5120, 17408, "Q4_K GEMV 5120x17408"),
-    "iq1m_gemv": (29, 17408, 5120, "IQ1_M GEMV 17408x5120"),
-    "iq1m_gemv_t": (29, 5120, 17408, "IQ1_M GEMV 5120x17408"),
-    "q6k_gemv": (14, 17408, 5120, "Q6_K GEMV 17408x5120"),
+    # name: (type, rows, width, tokens, tiled, label)
+    "q4k_gemv": (12, 17408, 5120, 1, False, "Q4_K GEMV 17408x5120"),
+    "q4k_gemv_t": (12, 5120, 17408, 1, False, "Q4_K GEMV 5120x17408"),
+    "iq1m_gemv": (29, 17408, 5120, 1, False, "IQ1_M GEMV 17408x5120"),
+    "iq1m_gemv_t": (29, 5120, 17408, 1, False, "IQ1_M GEMV 5120x17408"),
+    "q6k_gemv": (14, 17408, 5120, 1, False, "Q6_K GEMV 17408x5120"),
+    "q4k_tiled_m3": (12, 34816, 5120, 3, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 3 tokens"),
+    "q4k_tiled_down_m3": (12, 5120, 17408, 3, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 3 tokens"),
 }
 BLOCK = {12: 144, 14: 210, 29: 56}
 TYPE_NAME = {12: "Q4_K", 14: "Q6_K", 29: "IQ1_M"}
@@ -65,14 +75,16 @@ def parse():
     p.add_argument("--decode-tokens", type=int, default=256)
     p.add_argument("--prompt", type=int, default=512)
     p.add_argument("--draft", type=int, default=3)
+    p.add_argument("--plain-tokens", type=int, default=32, help="plain greedy tokens after the timed region")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
+    p.add_argument("--trace-summary", metavar="DIR", help="summarise a rocprofv3 kernel trace and exit")
     return p.parse_args()
 
 
-def algorithmic_bytes(qtype, rows, width):
-    """weights + Q8_K activation blocks + fp32 outputs of one GEMV launch"""
-    return rows * (width // 256) * BLOCK[qtype] + (width // 256) * 292 + rows * 4
+def algorithmic_bytes(qtype, rows, width, tokens=1):
+    """weights + Q8_K activation blocks + fp32 outputs of one launch"""
+    return rows * (width // 256) * BLOCK[qtype] + tokens * (width // 256) * 292 + tokens * rows * 4
 
 
 def committed_traffic(workload):
@@ -85,10 +97,11 @@ def committed_traffic(workload):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(qtype, rows, width, budget_s):
-    """The reference's AVX2 GEMV (oracle/_ref) on the host cores, bounded sample.
+def cpu_baseline(qtype, rows, width, tokens, budget_s):
+    """The reference's AVX2 GEMV / GEMM (oracle/_ref) on the host cores,
+    bounded sample.
 
-    The weights rotate over enough distinct copies (>= 512 MB) that each GEMV
+    The weights rotate over enough distinct copies (>= 512 MB) that each call
     streams its matrix from DRAM as the GPU launches stream theirs from HBM."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Reference
@@ -99,24 +112,32 @@ def cpu_baseline(qtype, rows, width, budget_s):
     base = synth.matrix(qtype, rows, width, seed=1)
     copies = max(2, -(-(512 << 20) // base.nbytes))
     weights = [base] + [base.copy() for _ in range(copies - 1)]
-    x = synth.activations(width, seed=2)
+    x = synth.activations(width, seed=2, count=tokens)
     q = ref.quantize(x.reshape(-1))
-    ref.gemv(qtype, weights[0], rows, q)  # warm-up (thread pool start)
+
+    def call(w):
+        if tokens == 1:
+            ref.gemv(qtype, w, rows, q)
+        else:
+            ref.gemm(qtype, w, rows, q, tokens)
+
+    call(weights[0])  # warm-up (thread pool start)
     count = 0
     start = time.perf_counter()
     while True:
-        ref.gemv(qtype, weights[count % copies], rows, q)
+        call(weights[count % copies])
         count += 1
         elapsed = time.perf_counter() - start
         if elapsed >= budget_s:
             break
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(algorithmic_bytes(qtype, rows, width) * count / elapsed / 1e9, 3),
+    entry = "q38_tensor_gemv_q8_k" if tokens == 1 else "q38_tensor_gemm_q8_k"
+    return {"value": round(algorithmic_bytes(qtype, rows, width, tokens) * count / elapsed / 1e9, 3),
             "unit": "GB/s", "cores": threads, "kind": "reference",
-            "sample": "%d single-token %s x Q8_K GEMVs %dx%d (q38_tensor_gemv_q8_k, AVX2 build), "
+            "sample": "%d %d-token %s x Q8_K products %dx%d (%s, AVX2 build), "
                       "weights rotated over %d copies (%d MB), %.1f s, OpenMP threads=%d" % (
-                          count, TYPE_NAME[qtype], rows, width, copies, copies * base.nbytes >> 20,
-                          elapsed, threads)}
+                          count, tokens, TYPE_NAME[qtype], rows, width, entry, copies,
+                          copies * base.nbytes >> 20, elapsed, threads)}
 
 
 def timed(torch, stream, steps, launch):
@@ -150,25 +171,34 @@ def run_copy(torch, args):
                       "steps": steps, "ms_per_step": round(wall * 1e3 / steps, 5)}))
 
 
-def gemv_roofline(torch, workload, steps, warmup):
-    """Time `steps` back-to-back launches of one GEMV workload on the current
-    stream (HIP events); returns (per-launch ms, wall s, roofline dict)."""
+def kernel_roofline(torch, workload, steps, warmup):
+    """Time `steps` back-to-back launches of one GEMV / GEMM workload on the
+    current stream (HIP events); returns (per-launch ms, wall s, roofline
+    dict, weight copies)."""
     import q38hip
     from q38hip import synth
-    qtype, rows, width, _ = WORKLOADS[workload]
+    qtype, rows, width, tokens, tiled, label = WORKLOADS[workload]
     dev = torch.device("cuda:0")
-    nbytes = algorithmic_bytes(qtype, rows, width)
-    wbytes = rows * (width // 256) * BLOCK[qtype]
-    copies = max(2, -(-(1 << 30) // wbytes) + 1)
+    nbytes = algorithmic_bytes(qtype, rows, width, tokens)
     base = torch.from_numpy(synth.matrix(qtype, rows, width, seed=1)).to(dev)
-    weights = [base] + [base.clone() for _ in range(copies - 1)]
-    x = torch.from_numpy(synth.activations(width, seed=2)).to(dev)
-    xq = q38hip.quantize_q8_k(x)
-    out = torch.empty((1, rows), dtype=torch.float32, device=dev)
+    if tiled:
+        base = q38hip.repack_q4k_tiles(base, width, rows)
+    copies = max(2, -(-(1 << 30) // base.numel()) + 1)
+    # one allocation holds every copy, as the engine holds all weights in one
+    pool = torch.empty(copies * base.numel(), dtype=torch.uint8, device=dev)
+    weights = [pool[i * base.numel():(i + 1) * base.numel()] for i in range(copies)]
+    for w in weights:
+        w.copy_(base)
+    x = torch.from_numpy(synth.activations(width, seed=2, count=tokens)).to(dev)
+    xq = q38hip.quantize_q8_k(x.reshape(tokens, width))
+    out = torch.empty((tokens, rows), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream()
 
     def launch(i):
-        q38hip.gemm_q8_k(weights[i % copies], qtype, width, rows, xq, 1, out=out)
+        if tiled:
+            q38hip.gemm_q8_k_tiled(weights[i % copies], width, rows, xq, tokens, out=out)
+        else:
+            q38hip.gemm_q8_k(weights[i % copies], qtype, width, rows, xq, tokens, out=out)
 
     for i in range(warmup):
         launch(i)
@@ -177,10 +207,38 @@ def gemv_roofline(torch, workload, steps, warmup):
     traffic = committed_traffic(workload)
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None if traffic is None else int(traffic),
-                "kernel": "gemm_q8k (%s GEMV %dx%d, M=1)" % (TYPE_NAME[qtype], rows, width),
+                "kernel": "%s (%s)" % ("gemm_q4k_tiled" if tiled else "gemm_q8k", label),
                 "bytes_per_launch": nbytes, "launch_us": round(per_launch_ms * 1e3, 3)}
-    del weights, base
+    del weights, pool, base
     return per_launch_ms, wall, roofline, copies
+
+
+def trace_summary(directory):
+    """calls / avg / min / max ns per (kernel, grid) of a rocprofv3 kernel trace"""
+    import csv
+    paths = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)
+    if not paths:
+        raise SystemExit("no *kernel_trace.csv under %s" % directory)
+    stats = {}
+    for path in paths:
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                name = row["Kernel_Name"]
+                name = re.sub(r"\(.*$", "", name.replace("void ", "").replace("q38::", ""))
+                threads = int(row["Workgroup_Size_X"])
+                key = (name, int(row["Grid_Size_X"]) // max(threads, 1), threads)
+                d = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+                s = stats.setdefault(key, [0, 0, d, d])
+                s[0] += 1
+                s[1] += d
+                s[2] = min(s[2], d)
+                s[3] = max(s[3], d)
+    total = sum(v[1] for v in stats.values())
+    print("%-44s %7s %7s %7s %10s %8s %8s %6s" % ("kernel", "groups", "threads", "calls", "avg_ns", "min_ns",
+                                                  "max_ns", "share"))
+    for (name, groups, threads), (calls, dsum, dmin, dmax) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
+        print("%-44s %7d %7d %7d %10.1f %8d %8d %5.1f%%" % (name[:44], groups, threads, calls, dsum / calls, dmin,
+                                                           dmax, 100.0 * dsum / total))
 
 
 def prompt_ids(count, seed=11):
@@ -253,14 +311,14 @@ def run_decode(torch, args):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     # plain greedy decode on the same model (no MTP) for reference
-    plain_n = 32
+    plain_n = args.plain_tokens
     t1 = time.perf_counter()
     for _ in range(plain_n):
         token = int(np.argmax(model.forward_token(token)))
     plain_wall = time.perf_counter() - t1
     model.close()
 
-    _, _, roofline, copies = gemv_roofline(torch, "q4k_gemv", 200, 20)
+    _, _, roofline, copies = kernel_roofline(torch, "q4k_tiled_m3", 200, 20)
     result = {
         "metric": "decode tokens/s (27B Q4_K_M + MTP k=%d, greedy)" % args.draft,
         "value": round(produced / wall, 3),
@@ -280,7 +338,7 @@ def run_decode(torch, args):
                    "accepted_per_transaction": round(produced / steps, 4),
                    "prefill_s": round(t_prefill, 3), "open_upload_s": round(t_open, 3),
                    "synth_s": round(t_synth, 3),
-                   "plain_greedy_tokens_per_s": round(plain_n / plain_wall, 3)},
+                   "plain_greedy_tokens_per_s": round(plain_n / plain_wall, 3) if plain_n else None},
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(path, args.draft, args.cpu_seconds),
     }
@@ -289,6 +347,9 @@ def run_decode(torch, args):
 
 def main():
     args = parse()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",
               file=sys.stderr)
@@ -300,12 +361,13 @@ def main():
     if args.workload == "decode":
         run_decode(torch, args)
         return
-    qtype, rows, width, label = WORKLOADS[args.workload]
+    qtype, rows, width, tokens, tiled, label = WORKLOADS[args.workload]
     steps = args.steps if args.steps is not None else 200
     warmup = args.warmup if args.warmup is not None else 20
-    per_launch_ms, wall, roofline, copies = gemv_roofline(torch, args.workload, steps, warmup)
+    per_launch_ms, wall, roofline, copies = kernel_roofline(torch, args.workload, steps, warmup)
     result = {
-        "metric": "quant-GEMV HBM GB/s (%s x Q8_K decode GEMV)" % TYPE_NAME[qtype],
+        "metric": "quant-%s HBM GB/s (%s x Q8_K, %d token%s)" % ("GEMV" if tokens == 1 else "GEMM",
+                                                               TYPE_NAME[qtype], tokens, "s" if tokens > 1 else ""),
         "value": roofline["achieved"],
         "unit": "GB/s",
         "n_gpus": 1,
@@ -319,9 +381,9 @@ def main():
         "data": "synthetic (seeded GGUF blocks, N(0,1) activations)",
         "config": {"workload": label, "weight_copies_rotated": copies,
                    "rotated_bytes": copies * rows * (width // 256) * BLOCK[qtype],
-                   "bytes_per_launch": algorithmic_bytes(qtype, rows, width)},
+                   "bytes_per_launch": algorithmic_bytes(qtype, rows, width, tokens)},
         "roofline": roofline,
-        "cpu_baseline": None if args.no_cpu else cpu_baseline(qtype, rows, width, args.cpu_seconds),
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(qtype, rows, width, tokens, args.cpu_seconds),
     }
     print(json.dumps(result))
 

@@ -88,7 +88,9 @@ int q38hip_gemm_q8_k(float *output, const Q38Q8KBlock *input,
                      const Q38GGUFTensor *tensor, void *stream);
 
 /* Row-wise first-maximum index (q38_argmax, src/qwen38/qwen38_model.c:
- * 1228-1239) of `rows` rows of `count` floats; index_out[rows]. */
+ * 1228-1239) of `rows` rows of `count` floats; index_out[rows].  Partial
+ * maxima go to a per-device scratch buffer that the library grows on demand
+ * (after synchronising the device): calls that overlap on one device race. */
 int q38hip_argmax(uint32_t *index_out, const float *values, uint32_t count,
                   uint32_t rows, void *stream);
 

@@ -212,6 +212,10 @@ int q38hip_argmax(uint32_t *index_out, const float *values, uint32_t count, uint
     {
         std::lock_guard<std::mutex> lock(g_mutex);
         if (state->argmax_capacity < need) {
+            /* launches enqueued earlier (on any stream) may still read the
+             * old scratch: let them finish before it is released */
+            if (state->argmax_values && hipDeviceSynchronize() != hipSuccess)
+                return fail("device synchronisation failed");
             if (state->argmax_values) (void)hipFree(state->argmax_values);
             if (state->argmax_index) (void)hipFree(state->argmax_index);
             state->argmax_values = nullptr;
