@@ -34,7 +34,8 @@ is the calibration run for the memory counters, not a bench line.
 `--trace-summary DIR` prints, from a rocprofv3 `--kernel-trace --output-format
 csv` directory, the calls and average / min / max duration of every kernel
 per launch grid (one kernel name serves several matrix shapes; the grid tells
-them apart), and exits.
+them apart), and exits; `--trace-transactions N` restricts a decode run's
+trace to its N transactions and reports each kernel's time per transaction.
 """
 import argparse
 import glob
@@ -79,6 +80,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     p.add_argument("--trace-summary", metavar="DIR", help="summarise a rocprofv3 kernel trace and exit")
+    p.add_argument("--trace-transactions", type=int, default=0,
+                   help="with --trace-summary of a decode run: its transaction count (warmup + steps)")
     return p.parse_args()
 
 
@@ -213,32 +216,54 @@ def kernel_roofline(torch, workload, steps, warmup):
     return per_launch_ms, wall, roofline, copies
 
 
-def trace_summary(directory):
-    """calls / avg / min / max ns per (kernel, grid) of a rocprofv3 kernel trace"""
+def _trace_rows(directory):
     import csv
     paths = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)
     if not paths:
         raise SystemExit("no *kernel_trace.csv under %s" % directory)
-    stats = {}
+    rows = []
     for path in paths:
         with open(path) as f:
-            for row in csv.DictReader(f):
-                name = row["Kernel_Name"]
-                name = re.sub(r"\(.*$", "", name.replace("void ", "").replace("q38::", ""))
-                threads = int(row["Workgroup_Size_X"])
-                key = (name, int(row["Grid_Size_X"]) // max(threads, 1), threads)
-                d = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
-                s = stats.setdefault(key, [0, 0, d, d])
-                s[0] += 1
-                s[1] += d
-                s[2] = min(s[2], d)
-                s[3] = max(s[3], d)
+            rows.extend(csv.DictReader(f))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    for r in rows:
+        r["short"] = re.sub(r"\(.*$", "", r["Kernel_Name"].replace("void ", "").replace("q38::", ""))
+        r["groups"] = int(r["Grid_Size_X"]) // max(int(r["Workgroup_Size_X"]), 1)
+        r["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    return rows
+
+
+def trace_summary(directory, transactions=0):
+    """calls / avg / min / max ns per (kernel, grid) of a rocprofv3 kernel
+    trace.  With `transactions` > 0 the trace is that of the decode workload
+    and only its transactions are summarised: the dispatches after the
+    prefill's last 8-token GEMM and before the roofline's weight repack,
+    reported per transaction."""
+    rows = _trace_rows(directory)
+    if transactions:
+        names = [r["short"] for r in rows]
+        first = max(i for i, n in enumerate(names) if n.startswith("gemm_q4k_tiled<8")) + 1
+        last = max(i for i, n in enumerate(names) if n.startswith("repack_q4k_tiles"))
+        rows = rows[first:last]
+        wall = int(rows[-1]["End_Timestamp"]) - int(rows[0]["Start_Timestamp"])
+        busy = sum(r["ns"] for r in rows)
+        print("%d dispatches over %d transactions: %.3f ms wall and %.3f ms kernel time per transaction"
+              % (len(rows), transactions, wall / 1e6 / transactions, busy / 1e6 / transactions))
+    stats = {}
+    for r in rows:
+        s = stats.setdefault((r["short"], r["groups"], int(r["Workgroup_Size_X"])), [0, 0, r["ns"], r["ns"]])
+        s[0] += 1
+        s[1] += r["ns"]
+        s[2] = min(s[2], r["ns"])
+        s[3] = max(s[3], r["ns"])
     total = sum(v[1] for v in stats.values())
-    print("%-44s %7s %7s %7s %10s %8s %8s %6s" % ("kernel", "groups", "threads", "calls", "avg_ns", "min_ns",
-                                                  "max_ns", "share"))
+    per = " per_txn us/txn" if transactions else ""
+    print("%-40s %7s %7s %7s %10s %8s %8s %6s%s" % ("kernel", "groups", "threads", "calls", "avg_ns", "min_ns",
+                                                    "max_ns", "share", per))
     for (name, groups, threads), (calls, dsum, dmin, dmax) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
-        print("%-44s %7d %7d %7d %10.1f %8d %8d %5.1f%%" % (name[:44], groups, threads, calls, dsum / calls, dmin,
-                                                           dmax, 100.0 * dsum / total))
+        extra = " %7.2f %6.1f" % (calls / transactions, dsum / transactions / 1e3) if transactions else ""
+        print("%-40s %7d %7d %7d %10.1f %8d %8d %5.1f%%%s" % (name[:40], groups, threads, calls, dsum / calls, dmin,
+                                                             dmax, 100.0 * dsum / total, extra))
 
 
 def prompt_ids(count, seed=11):
@@ -348,7 +373,7 @@ def run_decode(torch, args):
 def main():
     args = parse()
     if args.trace_summary:
-        trace_summary(args.trace_summary)
+        trace_summary(args.trace_summary, args.trace_transactions)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",
