@@ -23,6 +23,9 @@ size_t tiled_q4k_bytes(uint32_t rows, uint32_t nb);
 bool launch_repack_q4k_tiles(uint8_t *dst, const uint8_t *src, uint32_t rows, uint32_t nb, hipStream_t stream);
 bool launch_gemm_q4k_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                            uint32_t nb, hipStream_t stream);
+/* same product, 32 weight rows per wavefront (v_mfma_f32_32x32x16_f16) */
+bool launch_gemm_q4k_t32(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                         uint32_t nb, hipStream_t stream);
 /* same with the token rows of y `ldy` floats apart (ldy >= rows) */
 bool launch_gemm_ld(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                     uint32_t nblk, const void *grid, hipStream_t stream);

@@ -1,0 +1,389 @@
+/* Q4_K x Q8_K for 2..8 tokens on the gfx950 matrix cores, 32 weight rows per
+ * wavefront (v_mfma_f32_32x32x16_f16), over the 16-row tiled copy built by
+ * repack_q4k_tiles ([tile = row / 16][block][row % 16][144 bytes]).
+ *
+ * Arithmetic (as in q38_tiled.hip).  Per row, token and super-block b the
+ * reference's AVX2 kernel (src/qwen38/qwen38_quant.c:1546-1634) forms eight
+ * exact integers W[b][l] (l = AVX2 accumulator lane; lane l of chunk c is
+ * quant dword l of the chunk: low nibbles = elements 64c + 4l + u, high
+ * nibbles = elements 64c + 32 + 4l + u, scales sc[2c] and sc[2c + 1]) and
+ * four min sums M[b][i], then runs fp32 chains acc[l] = fmaf(d_b, W, acc[l]),
+ * accm[i] = fmaf(-dmin_b, M, accm[i]) over b in order.  Every product sc * q
+ * (<= 945) and activation (int8) is exact in fp16 and every partial sum is
+ * an integer below 2^22, so the matrix core returns W exactly.
+ *
+ * Mapping.  Lane i of a wavefront: r = i % 32 (tile row; the wavefront's 32
+ * rows are two consecutive 16-row tiles), q = i / 32.  For chunk pair c2 and
+ * AVX2 lane p (one MFMA):
+ *   B (16 x 32): K-slots 8q..8q+7 of column r = the 8 quants of lane p in
+ *     chunk c = 2 c2 + q of row r, as fp16 sc * q;
+ *   A (32 x 16): row m = (g, t) = (m / 4, m % 4), K-slots 8q..8q+7 = token
+ *     t's activations of lane g in chunk c (lane i supplies row m = r);
+ *   D_p[(g, t)][r] accumulated over c2 = sum over all chunks of
+ *     act(g) . w(p), which for g == p is W[b][p] of token t.
+ * Lane (r, q) holds D rows 8 (j / 4) + 4 q + j % 4 in register j, i.e. the
+ * diagonal of D_p for p = 2k + q at registers 4k .. 4k + 3: it owns AVX2
+ * lanes q, q + 2, q + 4, q + 6 and min lanes (= chunks) q, q + 2 of row r.
+ *
+ * Work split.  S wavefronts share a 32-row tile; wavefront s computes the
+ * integer sums of blocks b = s (mod S).  With S > 1 each round of S blocks
+ * goes through a double-buffered LDS ring (per lane: W of every token and the
+ * block header), and after a barrier wavefront s advances the chains of
+ * tokens t = s (mod S) over the round's blocks in block order, so the fp32
+ * order is the reference's.  The owner of a token applies the reference's
+ * final tree: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) + ((m0+m2)+(m1+m3))
+ * (qwen38_quant.c:303-310, 1626-1630).
+ *
+ * Memory.  Buffer loads with the block offset in a scalar, P blocks ahead;
+ * a ring slot is refilled right after its last use.
+ */
+#include "q38_device.h"
+#include "q38_kernels.h"
+
+namespace q38 {
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+constexpr int kRows16 = 16;
+constexpr int kBlockBytes = 144;
+constexpr int kTileBlock = kRows16 * kBlockBytes;   /* 2304 bytes: one block of a 16-row tile */
+constexpr uint32_t kRawBuffer = 0x00020000u;        /* raw 32-bit buffer resource (gfx9) */
+
+__device__ __forceinline__ half2v h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
+
+/* fp16 pair (n, n) for an integer n < 1024: (1024 + n) - 1024 */
+__device__ __forceinline__ half2v pair_n(uint32_t n)
+{
+    const half2v v = h2(__builtin_amdgcn_perm(0x64646464u, n, 0x07000700u));
+    return v - (half2v){(_Float16)1024.0f, (_Float16)1024.0f};
+}
+
+/* loads of one block for one lane */
+template <int TS>
+struct Blk {
+    uint4 h;                 /* header of row r: d|dmin, 12 scale/min bytes */
+    uint4 w0[2], w1[2];      /* quant dwords 0..7 of chunk q (w0) and q + 2 (w1) */
+    uint32_t lo[TS][2], hi[TS][2];   /* activations: token set, chunk pair */
+};
+
+struct Scale {
+    half2v sl, nl, sh16, nh;
+};
+
+/* the 8 quants of one dword as fp16 sc * q, element order per half
+ * u = 0, 2, 1, 3 (the activations use the same order) */
+__device__ __forceinline__ half8 dequant(uint32_t wd, const Scale &s, uint32_t kMask, uint32_t kMaskHi,
+                                         uint32_t kMagic)
+{
+    const uint32_t w8 = wd >> 8;
+    const half2v b0 = __builtin_elementwise_fma(h2((wd & kMask) | kMagic), s.sl, s.nl);
+    const half2v b1 = __builtin_elementwise_fma(h2((w8 & kMask) | kMagic), s.sl, s.nl);
+    const half2v b2 = __builtin_elementwise_fma(h2((wd & kMaskHi) | kMagic), s.sh16, s.nh);
+    const half2v b3 = __builtin_elementwise_fma(h2((w8 & kMaskHi) | kMagic), s.sh16, s.nh);
+    half8 v;
+    v[0] = b0[0]; v[1] = b0[1]; v[2] = b1[0]; v[3] = b1[1];
+    v[4] = b2[0]; v[5] = b2[1]; v[6] = b3[0]; v[7] = b3[1];
+    return v;
+}
+
+/* 8 int8 activations (4 low-nibble elements, 4 high) as fp16 */
+__device__ __forceinline__ half8 act8(uint32_t lo, uint32_t hi)
+{
+    const half2v k1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t ua = lo ^ 0x80808080u, ub = hi ^ 0x80808080u;
+    const half2v a02 = h2(__builtin_amdgcn_perm(0x64646464u, ua, 0x04020400u)) + k1152;
+    const half2v a13 = h2(__builtin_amdgcn_perm(0x64646464u, ua, 0x04030401u)) + k1152;
+    const half2v b02 = h2(__builtin_amdgcn_perm(0x64646464u, ub, 0x04020400u)) + k1152;
+    const half2v b13 = h2(__builtin_amdgcn_perm(0x64646464u, ub, 0x04030401u)) + k1152;
+    half8 v;
+    v[0] = a02[0]; v[1] = a02[1]; v[2] = a13[0]; v[3] = a13[1];
+    v[4] = b02[0]; v[5] = b02[1]; v[6] = b13[0]; v[7] = b13[1];
+    return v;
+}
+
+}  // namespace
+
+template <int MT, int NB, int S, int P>
+__global__ __launch_bounds__(64 * S) void gemm_q4k_t32(const uint8_t *__restrict__ w, const uint8_t *__restrict__ x,
+                                                       float *__restrict__ y, uint32_t ldy, uint32_t rows)
+{
+    constexpr int TS = (MT + 3) / 4;           /* MFMA token sets of four */
+    constexpr int KB = (NB + S - 1) / S;       /* rounds */
+    constexpr int NO = (MT + S - 1) / S;       /* chains' tokens per wavefront */
+    constexpr int RP = S > 1 ? 2 : 1;
+    constexpr int RING = S > 1 ? RP * S * (MT + 1) * 64 : 1;
+    __shared__ int2 pairs_s[MT * NB * 4];
+    __shared__ float xs_s[MT * NB];
+    __shared__ uint4 ring[RING];   /* [parity][wavefront][token | header][lane] */
+
+    const int lane = threadIdx.x & 63;
+    const int sw = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int r = lane & 31, q = lane >> 5, g = r >> 2, tk = r & 3;
+    const uint32_t ntiles = (rows + kRows16 - 1) / kRows16;
+    const uint32_t t0 = 2 * blockIdx.x;
+    const bool pair = t0 + 1 < ntiles;   /* second 16-row tile present */
+
+    const uint8_t *tb = w + (size_t)t0 * NB * kTileBlock;
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(tb), 0, (pair ? 2 : 1) * NB * kTileBlock, kRawBuffer);
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(x), 0, MT * NB * kQ8KBytes, kRawBuffer);
+    /* rows of a missing second tile re-read the first tile (never stored) */
+    const uint32_t hoff = (uint32_t)((pair ? (r >> 4) : 0) * NB * kTileBlock + (r & 15) * kBlockBytes);
+    const uint32_t q0off = hoff + 16 + 32 * q, q1off = q0off + 64;
+    uint32_t xoff[TS];   /* token tk + 4s (clamped), lane g, chunk q, low half */
+#pragma unroll
+    for (int s = 0; s < TS; ++s) {
+        const int t = tk + 4 * s < MT ? tk + 4 * s : MT - 1;
+        xoff[s] = (uint32_t)(t * NB * kQ8KBytes + 4 + 64 * q + 4 * g);
+    }
+    auto block_of = [&](int k) {
+        const int b = sw + S * k;
+        return b < NB ? b : NB - 1;   /* past the end: re-read the last block, results unused */
+    };
+    auto load = [&](int k) {
+        const int b = block_of(k);
+        const int wo = b * kTileBlock, xo = b * kQ8KBytes;
+        Blk<TS> c;
+        int4v v = __builtin_amdgcn_raw_buffer_load_b128(wr, hoff, wo, 0);
+        c.h = make_uint4(v[0], v[1], v[2], v[3]);
+        v = __builtin_amdgcn_raw_buffer_load_b128(wr, q0off, wo, 0);
+        c.w0[0] = make_uint4(v[0], v[1], v[2], v[3]);
+        v = __builtin_amdgcn_raw_buffer_load_b128(wr, q0off + 16, wo, 0);
+        c.w0[1] = make_uint4(v[0], v[1], v[2], v[3]);
+        v = __builtin_amdgcn_raw_buffer_load_b128(wr, q1off, wo, 0);
+        c.w1[0] = make_uint4(v[0], v[1], v[2], v[3]);
+        v = __builtin_amdgcn_raw_buffer_load_b128(wr, q1off + 16, wo, 0);
+        c.w1[1] = make_uint4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+        for (int s = 0; s < TS; ++s)
+#pragma unroll
+            for (int c2 = 0; c2 < 2; ++c2) {
+                c.lo[s][c2] = __builtin_amdgcn_raw_buffer_load_b32(xr, xoff[s] + 128 * c2, xo, 0);
+                c.hi[s][c2] = __builtin_amdgcn_raw_buffer_load_b32(xr, xoff[s] + 128 * c2 + 32, xo, 0);
+            }
+        return c;
+    };
+    Blk<TS> slot[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) slot[i] = load(i);
+
+    /* activation scales and min pair sums (Q8_K dword 0 and sum dwords
+     * 65..72), eight loads in flight per thread */
+    {
+        constexpr int kTotal = MT * NB * 9, kThreads = 64 * S, kDepth = 8;
+        for (int i0 = threadIdx.x; i0 < kTotal; i0 += kDepth * kThreads) {
+            uint32_t v[kDepth];
+#pragma unroll
+            for (int u = 0; u < kDepth; ++u) {
+                const int i = i0 + u * kThreads < kTotal ? i0 + u * kThreads : kTotal - 1;
+                const int blk = i / 9, k = i - blk * 9;
+                v[u] = __builtin_amdgcn_raw_buffer_load_b32(xr, (uint32_t)(blk * kQ8KBytes + (k == 0 ? 0 : 256 + 4 * k)), 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < kDepth; ++u) {
+                const int i = i0 + u * kThreads;
+                if (i >= kTotal) break;
+                const int blk = i / 9, k = i - blk * 9;
+                if (k == 0) xs_s[blk] = __uint_as_float(v[u]);
+                else reinterpret_cast<int *>(pairs_s)[blk * 8 + (k - 1)] =
+                    (int)(int16_t)(v[u] & 0xffffu) + ((int)v[u] >> 16);
+            }
+        }
+    }
+    __syncthreads();
+
+    constexpr int NC = S == 1 ? MT : NO;   /* chain token slots of this wavefront */
+    float acc[NC][4], accm[NC][2];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[j][k] = 0.0f;
+        accm[j][0] = accm[j][1] = 0.0f;
+    }
+    int own[NC];   /* token of chain slot j (clamped; slots past MT are dropped) */
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int t = S == 1 ? j : sw + S * j;
+        own[j] = t < MT ? t : MT - 1;
+    }
+
+    uint32_t kMask = 0x000f000fu, kMaskHi = 0x00f000f0u, kMagic = 0x64006400u;
+    asm volatile("" : "+v"(kMask), "+v"(kMaskHi), "+v"(kMagic));
+    const int sh = 16 * q;
+
+    /* integer sums of one block: wv[t][k] = W[b][2k + q] of token t */
+    auto block_sums = [&](const Blk<TS> &c, float (&wv)[MT][4]) {
+        const uint32_t Y = c.h.y, Wd = c.h.w;
+        /* 6-bit scales (qwen38_quant.c:131-143): sub-blocks 2q, 2q+1 from
+         * bytes 0..3, sub-blocks 4+2q, 5+2q from bytes 8..11 low nibbles and
+         * the top bits of bytes 0..3 */
+        const uint32_t scw[2] = {Y & 0x3f3f3f3fu, (Wd & 0x0f0f0f0fu) | ((Y >> 2) & 0x30303030u)};
+        Scale sc[2];
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+            const half2v SL = pair_n((scw[c2] >> sh) & 0xffu), SH = pair_n((scw[c2] >> (sh + 8)) & 0xffu);
+            sc[c2].sl = SL;
+            sc[c2].nl = SL * (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f};
+            sc[c2].sh16 = SH * (half2v){(_Float16)0.0625f, (_Float16)0.0625f};
+            sc[c2].nh = SH * (half2v){(_Float16)-64.0f, (_Float16)-64.0f};
+        }
+        half8 av[TS][2];
+#pragma unroll
+        for (int s = 0; s < TS; ++s)
+#pragma unroll
+            for (int c2 = 0; c2 < 2; ++c2) av[s][c2] = act8(c.lo[s][c2], c.hi[s][c2]);
+        const uint32_t q0[8] = {c.w0[0].x, c.w0[0].y, c.w0[0].z, c.w0[0].w, c.w0[1].x, c.w0[1].y, c.w0[1].z, c.w0[1].w};
+        const uint32_t q1[8] = {c.w1[0].x, c.w1[0].y, c.w1[0].z, c.w1[0].w, c.w1[1].x, c.w1[1].y, c.w1[1].z, c.w1[1].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const half8 b00 = dequant(q0[2 * k], sc[0], kMask, kMaskHi, kMagic);
+            const half8 b10 = dequant(q1[2 * k], sc[1], kMask, kMaskHi, kMagic);
+            const half8 b01 = dequant(q0[2 * k + 1], sc[0], kMask, kMaskHi, kMagic);
+            const half8 b11 = dequant(q1[2 * k + 1], sc[1], kMask, kMaskHi, kMagic);
+#pragma unroll
+            for (int s = 0; s < TS; ++s) {
+                const float16v z = {};
+                float16v d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[s][0], b00, z, 0, 0, 0);
+                float16v d1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[s][0], b01, z, 0, 0, 0);
+                d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[s][1], b10, d0, 0, 0, 0);
+                d1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[s][1], b11, d1, 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int t = 4 * s + j;
+                    if (t < MT) wv[t][k] = q ? d1[4 * k + j] : d0[4 * k + j];
+                }
+            }
+        }
+    };
+
+    /* advance chain slot j (token t) over block b with W values wq and the
+     * block header h */
+    auto chain = [&](int j, int t, int b, const uint4 &h, const float (&wq)[4]) {
+        const float xs = xs_s[t * NB + b];
+        const float d = f16_to_f32(h.x), dmin = f16_to_f32(h.x >> 16);
+        const float dx = fmul_rn(d, xs), mx = -fmul_rn(dmin, xs);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[j][k] = __builtin_fmaf(dx, wq[k], acc[j][k]);
+        /* 6-bit mins of chunks q and q + 2 */
+        const uint32_t mw[2] = {h.z & 0x3f3f3f3fu, ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u)};
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+            const int m0 = (int)((mw[c2] >> sh) & 0xffu), m1 = (int)((mw[c2] >> (sh + 8)) & 0xffu);
+            const int2 pr = pairs_s[(t * NB + b) * 4 + 2 * c2 + q];
+            accm[j][c2] = __builtin_fmaf(mx, (float)mad24(m0, pr.x, mul24(m1, pr.y)), accm[j][c2]);
+        }
+    };
+
+    auto round = [&](const Blk<TS> &c, int k) {
+        float wv[MT][4];
+        const uint4 hd = c.h;
+        block_sums(c, wv);
+        if (S == 1) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t) chain(t, t, k, hd, wv[t]);
+            return;
+        }
+        const int base = ((k & 1) * S + sw) * (MT + 1) * 64;
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+            ring[base + t * 64 + lane] =
+                make_uint4(__float_as_uint(wv[t][0]), __float_as_uint(wv[t][1]), __float_as_uint(wv[t][2]),
+                           __float_as_uint(wv[t][3]));
+        ring[base + MT * 64 + lane] = hd;
+        __syncthreads();
+#pragma unroll
+        for (int f = 0; f < S; ++f) {
+            const int b2 = f + S * k;
+            if (b2 >= NB) break;
+            const int fb = ((k & 1) * S + f) * (MT + 1) * 64;
+            const uint4 h = ring[fb + MT * 64 + lane];
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const uint4 v = ring[fb + own[j] * 64 + lane];
+                const float wq[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
+                                     __uint_as_float(v.w)};
+                chain(j, own[j], b2, h, wq);
+            }
+        }
+    };
+
+    constexpr int kFull = KB / P, kRem = KB % P;
+#pragma unroll 1
+    for (int it = 0; it < kFull; ++it) {
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int k = it * P + i;
+            round(slot[i], k);
+            /* refill the slot after its last use */
+            slot[i] = load(k + P);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kRem; ++i) round(slot[i], KB - kRem + i);
+
+    /* final trees; lane q = 0 of each row stores */
+    const uint32_t row = 32 * blockIdx.x + (uint32_t)r;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int t = S == 1 ? j : sw + S * j;
+        if (t >= MT) break;
+        float a = fadd_rn(fadd_rn(acc[j][0], acc[j][2]), fadd_rn(acc[j][1], acc[j][3]));
+        a = fadd_rn(a, __shfl_xor(a, 32, 64));
+        float m = fadd_rn(accm[j][0], accm[j][1]);
+        m = fadd_rn(m, __shfl_xor(m, 32, 64));
+        if (q == 0 && row < rows) y[(size_t)t * ldy + row] = fadd_rn(a, m);
+    }
+}
+
+namespace {
+
+/* Launch shape (measured on MI355X for 2..4 tokens and 5120..34816 rows):
+ * four wavefronts per 32-row tile, two blocks in flight per wavefront. */
+constexpr int kT32Waves = 4, kT32Prefetch = 2;
+
+template <int MT, int NB>
+bool launch_t32_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, hipStream_t stream)
+{
+    const uint32_t tiles32 = (rows + 31) / 32;
+    hipLaunchKernelGGL((gemm_q4k_t32<MT, NB, kT32Waves, kT32Prefetch>), dim3(tiles32), dim3(64 * kT32Waves), 0,
+                       stream, w, x, y, ldy, rows);
+    return hipGetLastError() == hipSuccess;
+}
+
+template <int NB>
+bool launch_t32_nb(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                   hipStream_t stream)
+{
+    switch (m) {
+    case 2: return launch_t32_typed<2, NB>(w, x, y, ldy, rows, stream);
+    case 3: return launch_t32_typed<3, NB>(w, x, y, ldy, rows, stream);
+    case 4: return launch_t32_typed<4, NB>(w, x, y, ldy, rows, stream);
+    default: return false;
+    }
+}
+
+}  // namespace
+
+/* y[t * ldy + row] = W_row . x_t (t < m) from the 16-row tiled copy, 32 rows
+ * per wavefront; 2..4 tokens (more tokens need a second MFMA token set and
+ * twice the registers); false for unsupported shapes. */
+bool launch_gemm_q4k_t32(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                         uint32_t nb, hipStream_t stream)
+{
+    if (!rows || ldy < rows) return false;
+    switch (nb) {
+    case 20: return launch_t32_nb<20>(m, w_tiled, x, y, ldy, rows, stream);
+    case 24: return launch_t32_nb<24>(m, w_tiled, x, y, ldy, rows, stream);
+    case 40: return launch_t32_nb<40>(m, w_tiled, x, y, ldy, rows, stream);
+    case 68: return launch_t32_nb<68>(m, w_tiled, x, y, ldy, rows, stream);
+    default: return false;
+    }
+}
+
+}  // namespace q38

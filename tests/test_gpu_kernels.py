@@ -162,10 +162,13 @@ def tiled_numpy(w, rows, width):
     return np.ascontiguousarray(padded.reshape(tiles, 16, nb, 144).transpose(0, 2, 1, 3)).reshape(-1)
 
 
-@pytest.mark.parametrize("rows,width", [(1000, 5120), (48, 5120), (2064, 6144), (520, 10240), (1040, 17408)])
+@pytest.mark.parametrize("rows,width", [(1000, 5120), (48, 5120), (2064, 6144), (520, 10240), (1040, 17408),
+                                        (4112, 5120), (4100, 6144), (5136, 17408)])
 def test_tiled_repack_and_gemm_bit_exact(hip, oracle, device, rows, width):
     """Tiled Q4_K copy (2..8 tokens, matrix cores) equals the oracle bit for bit;
-    the repack equals the host restatement of the layout (zero-padded tail)."""
+    the repack equals the host restatement of the layout (zero-padded tail).
+    From 4096 rows on, 2..4 tokens run the 32-row kernel: 4112 and 5136 rows
+    end on an unpaired 16-row tile, 4100 also on a padded one."""
     w = synth.matrix(Q4_K, rows, width, seed=rows + width)
     wd = to_dev(w, device)
     tiled = hip.repack_q4k_tiles(wd, width, rows)
