@@ -13,6 +13,11 @@ batch's shape, 3 tokens x 34816 x 5120 (the fused FFN gate|up projection,
 64 launches per transaction), timed in the same run on its own with the
 weights rotated over >= 1 GiB of distinct copies.
 
+`--layout iq1m` runs the same on the IQ1_M layout of the model (IQ1_M layer
+matrices, Q4_K embedding, Q6_K LM head): a 4096-token prompt is prefilled
+(`prefill_tokens_per_s`), then 1024 tokens are decoded (context 5124+); its
+roofline is the IQ1_M GEMM of the fused FFN gate|up at 3 tokens.
+
 Kernel workloads (`q4k_gemv`, `q4k_tiled_m3` ...): one GEMV / GEMM alone,
 quantised activations resident in HBM, weights rotated over >= 1 GiB of
 distinct copies so every launch streams from HBM rather than the 256 MB
@@ -61,6 +66,7 @@ WORKLOADS = {
     "q6k_gemv": (14, 17408, 5120, 1, False, "Q6_K GEMV 17408x5120"),
     "q4k_tiled_m3": (12, 34816, 5120, 3, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 3 tokens"),
     "q4k_tiled_down_m3": (12, 5120, 17408, 3, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 3 tokens"),
+    "iq1m_gemm_m3": (29, 34816, 5120, 3, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 3 tokens"),
 }
 BLOCK = {12: 144, 14: 210, 29: 56}
 TYPE_NAME = {12: "Q4_K", 14: "Q6_K", 29: "IQ1_M"}
@@ -74,7 +80,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=None)
     p.add_argument("--workload", default="decode", choices=["decode"] + sorted(WORKLOADS) + ["copy"])
     p.add_argument("--decode-tokens", type=int, default=256)
-    p.add_argument("--prompt", type=int, default=512)
+    p.add_argument("--layout", default="q4km", choices=["q4km", "iq1m"],
+                   help="decode workload: Q4_K_M layout (default) or IQ1_M layer matrices")
+    p.add_argument("--prompt", type=int, default=None, help="prompt tokens (512 for q4km, 4096 for iq1m)")
     p.add_argument("--draft", type=int, default=3)
     p.add_argument("--plain-tokens", type=int, default=32, help="plain greedy tokens after the timed region")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -299,16 +307,26 @@ def cpu_decode_baseline(path, draft, budget_s):
                       % (draft, transactions, produced, elapsed, threads)}
 
 
+LAYOUTS = {
+    # layout: (matrix types, dominant kernel workload, default prompt, default transactions)
+    "q4km": ("Q4_K_M", "q4k_tiled_m3", 512, 248),
+    "iq1m": ("IQ1_M", "iq1m_gemm_m3", 4096, 1016),
+}
+
+
 def run_decode(torch, args):
     from q38hip import synth
     from q38hip.model import Model
-    steps = args.steps if args.steps is not None else 248
+    label, roof_workload, default_prompt, default_steps = LAYOUTS[args.layout]
+    if args.prompt is None:
+        args.prompt = default_prompt
+    steps = args.steps if args.steps is not None else default_steps
     warmup = args.warmup if args.warmup is not None else 8
-    path = synth.model_path(1, "q4km")
+    path = synth.model_path(1, args.layout)
     if path is None:
-        raise SystemExit("no directory with room for the 15.7 GB synthetic model (set Q38_MODEL_DIR)")
+        raise SystemExit("no directory with room for the synthetic model (set Q38_MODEL_DIR)")
     t0 = time.perf_counter()
-    synth.write_model_gguf(path, 1, "q4km")
+    synth.write_model_gguf(path, 1, args.layout)
     t_synth = time.perf_counter() - t0
     context = args.prompt + args.draft * (warmup + steps) + 16
     t0 = time.perf_counter()
@@ -343,9 +361,9 @@ def run_decode(torch, args):
     plain_wall = time.perf_counter() - t1
     model.close()
 
-    _, _, roofline, copies = kernel_roofline(torch, "q4k_tiled_m3", 200, 20)
+    _, _, roofline, copies = kernel_roofline(torch, roof_workload, 200, 20)
     result = {
-        "metric": "decode tokens/s (27B Q4_K_M + MTP k=%d, greedy)" % args.draft,
+        "metric": "decode tokens/s (27B %s + MTP k=%d, greedy)" % (label, args.draft),
         "value": round(produced / wall, 3),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -355,13 +373,14 @@ def run_decode(torch, args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "i8xQ4_K/Q6_K->i32, f32",
-        "data": "synthetic (seeded random-init 27B Q4_K_M GGUF, random prompt ids)",
-        "config": {"workload": "decode 27B Q4_K_M + MTP k=%d" % args.draft, "layers": 64, "hidden": 5120,
+        "dtype": "i8x%s/Q6_K->i32, f32" % ("Q4_K" if args.layout == "q4km" else "IQ1_M"),
+        "data": "synthetic (seeded random-init 27B %s GGUF, random prompt ids)" % label,
+        "config": {"workload": "decode 27B %s + MTP k=%d" % (label, args.draft), "layers": 64, "hidden": 5120,
                    "ffn": 17408, "vocab": 248320, "prompt_tokens": args.prompt, "context": context,
                    "decoded_tokens": produced, "transactions": steps,
                    "accepted_per_transaction": round(produced / steps, 4),
-                   "prefill_s": round(t_prefill, 3), "open_upload_s": round(t_open, 3),
+                   "prefill_s": round(t_prefill, 3),
+                   "prefill_tokens_per_s": round(args.prompt / t_prefill, 1), "open_upload_s": round(t_open, 3),
                    "synth_s": round(t_synth, 3),
                    "plain_greedy_tokens_per_s": round(plain_n / plain_wall, 3) if plain_n else None},
         "roofline": roofline,

@@ -51,4 +51,70 @@ __device__ __forceinline__ void wave_quantize_q8k(const float v[4], uint8_t *__r
     if (lane == 0) *reinterpret_cast<float *>(blk) = div_rn(1.0f, inv);
 }
 
+/* wave_quantize_q8k for K blocks at once (block k at blk + k * stride),
+ * with the K reductions interleaved so their cross-lane latencies overlap.
+ * Same results as K separate calls. */
+template <int K>
+__device__ __forceinline__ void wave_quantize_q8k_multi(const float (&v)[K][4], uint8_t *__restrict__ blk,
+                                                        size_t stride, int lane)
+{
+    float amax[K];
+    int idx[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        amax[k] = 0.0f;
+        idx[k] = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = fabsf(v[k][i]);
+            if (a > amax[k]) { amax[k] = a; idx[k] = 4 * lane + i; }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        float oa[K];
+        int oi[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            oa[k] = __shfl_xor(amax[k], off, 64);
+            oi[k] = __shfl_xor(idx[k], off, 64);
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            if (oa[k] > amax[k] || (oa[k] == amax[k] && oi[k] < idx[k])) { amax[k] = oa[k]; idx[k] = oi[k]; }
+    }
+    float maximum[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int e = idx[k] & 3;
+        const float mine = e == 0 ? v[k][0] : e == 1 ? v[k][1] : e == 2 ? v[k][2] : v[k][3];
+        maximum[k] = __shfl(mine, (idx[k] >> 2) & 63, 64);
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        uint8_t *b = blk + k * stride;
+        if (amax[k] == 0.0f) {   /* uniform over the wave */
+            reinterpret_cast<uint32_t *>(b + 4)[lane] = 0u;
+            if (lane < 16) reinterpret_cast<int16_t *>(b + 260)[lane] = 0;
+            if (lane == 0) *reinterpret_cast<float *>(b) = 0.0f;
+            continue;
+        }
+        const float inv = div_rn(-127.0f, maximum[k]);
+        uint32_t packed = 0;
+        int sum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float shifted = __fadd_rn(__fmul_rn(inv, v[k][i]), 12582912.0f);
+            int qv = (int)(__float_as_uint(shifted) & 0x007fffffu) - 0x00400000;
+            if (qv > 127) qv = 127;
+            sum += qv;
+            packed |= (static_cast<uint32_t>(qv) & 0xffu) << (8 * i);
+        }
+        reinterpret_cast<uint32_t *>(b + 4)[lane] = packed;
+        sum = quad_sum(sum);
+        if ((lane & 3) == 0) reinterpret_cast<int16_t *>(b + 260)[lane >> 2] = static_cast<int16_t>(sum);
+        if (lane == 0) *reinterpret_cast<float *>(b) = div_rn(1.0f, inv);
+    }
+}
+
 }  // namespace q38

@@ -85,7 +85,7 @@ def activations(width, seed, count=1):
 
 
 SYNTH_GGUF = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "synth", "q38_synth_gguf")
-MODEL_GGUF_BYTES = {"q4km": 15704910464}
+MODEL_GGUF_BYTES = {"q4km": 15704910464, "iq1m": 7188425344}
 
 
 def write_model_gguf(path, seed, variant="q4km"):

@@ -38,13 +38,14 @@ def device():
 MODEL_SEED = 1
 
 
-@pytest.fixture(scope="session")
-def model_gguf():
-    """Path of the synthetic 27B-shaped Q4_K_M GGUF (seed 1), written by
-    qwen3.8-27b-in-c_amd/synth/q38_synth_gguf when missing (about 15.7 GB)."""
+def synthetic_model(variant):
+    """Path of the synthetic 27B-shaped GGUF of `variant` (seed 1; q4km about
+    15.7 GB, iq1m about 7.2 GB), written by
+    qwen3.8-27b-in-c_amd/synth/q38_synth_gguf when missing."""
     from q38hip import synth
-    path = synth.model_path(MODEL_SEED, "q4km")
+    path = synth.model_path(MODEL_SEED, variant)
     if path is None:
-        pytest.skip("no directory with 17 GB free for the synthetic model")
+        pytest.skip("no directory with room for the synthetic %s model" % variant)
     print("synthetic model:", path, flush=True)
-    return synth.write_model_gguf(path, MODEL_SEED, "q4km")
+    return synth.write_model_gguf(path, MODEL_SEED, variant)
+

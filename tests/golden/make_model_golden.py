@@ -1,7 +1,9 @@
 #!/usr/bin/env python3
 """Golden token sequences and logits digests of the COMPILED REFERENCE engine
 (oracle/_ref/libq38ref.so, the reference's own C sources) on the synthetic
-27B-shaped Q4_K_M model written by qwen3.8-27b-in-c_amd/synth/q38_synth_gguf.
+27B-shaped models written by qwen3.8-27b-in-c_amd/synth/q38_synth_gguf: the
+Q4_K_M layout (variant q4km) and the IQ1_M layout (variant iq1m: IQ1_M layer
+matrices, Q4_K embedding, Q6_K LM head).
 
 The GGUF is a pure function of its seed (about 15.7 GB, not committed); this
 script writes it when missing, runs the reference's model API
@@ -17,7 +19,7 @@ Scenarios (context 256, MTP enabled, prompt of 12 seeded ids):
   spec     prefill(prompt) then speculative_greedy(k=3) until 12 tokens
 
 Run from the repository root:
-  python tests/golden/make_model_golden.py [GGUF_PATH]
+  python tests/golden/make_model_golden.py [q4km|iq1m [GGUF_PATH]]
 """
 import hashlib
 import os
@@ -117,15 +119,18 @@ def run(model, log):
 def main():
     from oracle import reference_model
     from q38hip import synth
-    path = sys.argv[1] if len(sys.argv) > 1 else os.path.join(ROOT, "_work", "big", "q4km_s%d.gguf" % SEED)
-    synth.write_model_gguf(path, SEED, "q4km")
+    variant = sys.argv[1] if len(sys.argv) > 1 else "q4km"
+    if variant not in ("q4km", "iq1m"):
+        raise SystemExit("variant must be q4km or iq1m")
+    path = sys.argv[2] if len(sys.argv) > 2 else synth.model_path(SEED, variant)
+    synth.write_model_gguf(path, SEED, variant)
     t0 = time.time()
     log = lambda msg: print("[%6.1f s] %s" % (time.time() - t0, msg), flush=True)  # noqa: E731
     model = reference_model().open(path, CONTEXT)
     model.enable_mtp()
     out = run(model, log)
     model.close()
-    dest = os.path.join(os.path.dirname(os.path.abspath(__file__)), "model_q4km_s%d.npz" % SEED)
+    dest = os.path.join(os.path.dirname(os.path.abspath(__file__)), "model_%s_s%d.npz" % (variant, SEED))
     np.savez_compressed(dest, seed=np.array([SEED, CONTEXT, DRAFT]), **out)
     log("wrote " + dest)
 

@@ -1,6 +1,7 @@
 """Full-model parity on the GPU: the engine ABI of libq38hip (include/q38model.h)
 against the compiled reference engine's outputs on the same synthetic
-27B-shaped Q4_K_M checkpoint (tests/golden/model_q4km_s1.npz, written by
+27B-shaped checkpoints, Q4_K_M layout and IQ1_M layout
+(tests/golden/model_<variant>_s1.npz, written by
 tests/golden/make_model_golden.py from oracle/_ref).
 
 Bar: bit-identical.  Hidden states after 1 and 4 blocks compare as uint32;
@@ -16,7 +17,8 @@ import pytest
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
 
-GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "model_q4km_s1.npz")
+GOLDEN_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+VARIANTS = [v for v in ("q4km", "iq1m") if os.path.exists(os.path.join(GOLDEN_DIR, "model_%s_s1.npz" % v))]
 NO_STOP = 0xFFFFFFFF
 
 
@@ -24,17 +26,24 @@ def digest(logits):
     return hashlib.sha256(np.ascontiguousarray(logits, dtype=np.float32).tobytes()).hexdigest()
 
 
-@pytest.fixture(scope="module")
-def golden():
-    return dict(np.load(GOLDEN))
+@pytest.fixture(scope="module", params=VARIANTS)
+def variant(request):
+    return request.param
 
 
 @pytest.fixture(scope="module")
-def model(device, model_gguf, golden):
+def golden(variant):
+    return dict(np.load(os.path.join(GOLDEN_DIR, "model_%s_s1.npz" % variant)))
+
+
+@pytest.fixture(scope="module")
+def model(device, variant, golden):
+    from conftest import synthetic_model
     from q38hip.model import Model
+    path = synthetic_model(variant)
     t0 = time.time()
     context = int(golden["seed"][1])
-    m = Model.open(model_gguf, context)
+    m = Model.open(path, context)
     print("model open + upload %.1f s" % (time.time() - t0), flush=True)
     m.enable_mtp()
     yield m

@@ -1,15 +1,24 @@
-"""Consistency of the full-model fixture written by the compiled reference
-(tests/golden/model_q4km_s1.npz; CPU only).  The fixture itself is the pin of
-the model path: the reference engine ran on the synthetic checkpoint."""
+"""Consistency of the full-model fixtures written by the compiled reference
+(tests/golden/model_<variant>_s1.npz; CPU only).  The fixtures themselves are
+the pin of the model path: the reference engine ran on the synthetic
+checkpoints."""
+import glob
 import os
 
 import numpy as np
+import pytest
 
-GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "model_q4km_s1.npz")
+GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "model_*_s1.npz")))
 
 
-def test_fixture_is_self_consistent():
-    g = np.load(GOLDEN)
+def test_both_layouts_have_fixtures():
+    names = {os.path.basename(p) for p in GOLDEN}
+    assert {"model_q4km_s1.npz", "model_iq1m_s1.npz"} <= names
+
+
+@pytest.mark.parametrize("path", GOLDEN, ids=os.path.basename)
+def test_fixture_is_self_consistent(path):
+    g = np.load(path)
     greedy, spec = list(g["greedy_tokens"]), list(g["spec_tokens"])
     # the reference's speculative path reproduces its greedy sequence
     assert spec == greedy
