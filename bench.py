@@ -278,7 +278,7 @@ def prompt_ids(count, seed=11):
     return np.random.Generator(np.random.PCG64(seed)).integers(0, 248320, count).astype(np.uint32)
 
 
-def cpu_decode_baseline(path, draft, budget_s):
+def cpu_decode_baseline(path, draft, budget_s, label="Q4_K_M"):
     """The reference engine (oracle/_ref, its own C sources, AVX2 build) on the
     host cores: a 4-token prompt, then speculative_greedy(draft) transactions
     for about `budget_s` seconds; decoded tokens per second."""
@@ -302,9 +302,9 @@ def cpu_decode_baseline(path, draft, budget_s):
     model.close()
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {"value": round(produced / elapsed, 4), "unit": "tokens/s", "cores": threads, "kind": "reference",
-            "sample": "reference engine q38_model_speculative_greedy(k=%d) on the same synthetic 27B Q4_K_M "
+            "sample": "reference engine q38_model_speculative_greedy(k=%d) on the same synthetic 27B %s "
                       "GGUF: 4-token prompt, %d transactions, %d tokens in %.1f s, OpenMP threads=%d"
-                      % (draft, transactions, produced, elapsed, threads)}
+                      % (draft, label, transactions, produced, elapsed, threads)}
 
 
 LAYOUTS = {
@@ -384,7 +384,7 @@ def run_decode(torch, args):
                    "synth_s": round(t_synth, 3),
                    "plain_greedy_tokens_per_s": round(plain_n / plain_wall, 3) if plain_n else None},
         "roofline": roofline,
-        "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(path, args.draft, args.cpu_seconds),
+        "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(path, args.draft, args.cpu_seconds, label),
     }
     print(json.dumps(result))
 

@@ -841,6 +841,8 @@ bool launch_gemm_ld(int type, int m, const uint8_t *w, const uint8_t *x, float *
                     uint32_t nblk, const void *grid, hipStream_t stream)
 {
     if (m < 1 || m > 8 || ldy < rows) return false;
+    /* IQ1_M at the Qwen3.8 row widths: the matrix-core kernel (q38_iq1m.hip) */
+    if (type == kIQ1M && launch_gemm_iq1m_mfma(m, w, x, y, ldy, rows, nblk, grid, stream)) return true;
     if (launch_gemv_lanes(type, m, w, x, y, ldy, rows, nblk, stream)) return true;
     const uint2 *g = static_cast<const uint2 *>(grid);
     switch (type) {

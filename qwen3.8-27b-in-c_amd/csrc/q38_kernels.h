@@ -21,6 +21,9 @@ bool launch_gemv_lanes(int type, int m, const uint8_t *w, const uint8_t *x, floa
  * tokens (false when the width or token count is not supported) */
 size_t tiled_q4k_bytes(uint32_t rows, uint32_t nb);
 bool launch_repack_q4k_tiles(uint8_t *dst, const uint8_t *src, uint32_t rows, uint32_t nb, hipStream_t stream);
+/* IQ1_M x Q8_K for 1..8 tokens on the matrix cores (row-major blocks) */
+bool launch_gemm_iq1m_mfma(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                           uint32_t nb, const void *grid, hipStream_t stream);
 bool launch_gemm_q4k_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                            uint32_t nb, hipStream_t stream);
 /* same product, 32 weight rows per wavefront (v_mfma_f32_32x32x16_f16) */

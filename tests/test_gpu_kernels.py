@@ -65,14 +65,15 @@ def test_gemv_full_shape_bit_exact(hip, oracle, device, qtype, rows, width):
 @pytest.mark.parametrize("qtype", [Q4_K, IQ1_M, Q6_K])
 @pytest.mark.parametrize("rows,width", [(1024, 5120), (96, 17408), (48, 5120), (77, 6144)])
 def test_gemm_rows_bit_exact(hip, oracle, device, qtype, rows, width):
-    """Verify-batch GEMM, M = 1..5 rows, against the per-token oracle GEMV."""
+    """Verify-batch and prefill GEMM, M = 1..8 rows, against the per-token
+    oracle GEMV."""
     w = synth.matrix(qtype, rows, width, seed=11 * qtype + rows)
-    x = synth.activations(width, seed=width + rows, count=5)
+    x = synth.activations(width, seed=width + rows, count=8)
     q = oracle.quantize(x.reshape(-1))
     wd = to_dev(w, device)
     xq = hip.quantize_q8_k(to_dev(x, device))
     nb = width // 256
-    for m in range(1, 6):
+    for m in range(1, 9):
         want = oracle.gemm(qtype, w, rows, q[:m * nb], m)
         got = hip.gemm_q8_k(wd, qtype, width, rows, xq[:m * nb * 292], m).cpu().numpy()
         assert np.array_equal(bits(got), bits(want)), "M=%d" % m
