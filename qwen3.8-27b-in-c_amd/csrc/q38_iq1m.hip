@@ -12,11 +12,11 @@
  * integer E = 8 weighted + correction, so the chain here is
  * total += d * (float(E) * 0.125f), bit for bit the reference's.
  *
- * E comes from three int8 matrix products per 64-element chunk with the
+ * E comes from two int8 matrix products per 64-element chunk with the
  * activations as the A operand (16 token rows) and, as B operand per weight
- * row: s * (grid + 1) (bytes 0..30), s * sign (bytes +-15) and s (broadcast):
- *   E = 8 * (A.[s(g+1)] - A.[s]) + A.[s sign].
- * The products are exact int32.
+ * row, s * grid and s * sign (bytes in -15..15):
+ *   E = 8 * A.[s grid] + A.[s sign],
+ * exact in int32.
  *
  * Mapping (lane i of a wavefront, 16 weight rows per tile): r = i % 16 is the
  * weight row (B column) and the token (A row), q = i / 16 picks bytes
@@ -25,6 +25,8 @@
  * 4q + j of row r.  S wavefronts split the blocks of a tile (block b to
  * wavefront b mod S); every block's E and scale land in LDS, and after one
  * barrier one lane per (row, token) runs the fp32 chain in block order.
+ * Workgroups stride over the tiles (the codebook is staged in LDS once per
+ * workgroup) and load ahead across tile boundaries.
  */
 #include "q38_device.h"
 #include "q38_kernels.h"
@@ -55,16 +57,16 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
     constexpr int TS = (MT + 15) / 16;   /* token sets of 16 (MT <= 8: one) */
     constexpr int KB = (NB + S - 1) / S;
     __shared__ uint2 grid_s[2048];        /* codebook entries as bytes grid + 1 */
-    __shared__ float e_s[NB * MT * 16];   /* [block][token][row] */
-    __shared__ float d_s[NB * 16];        /* [block][row] super-scale */
+    __shared__ float e_s[2 * NB * MT * 16];   /* [tile parity][block][token][row] */
+    __shared__ float d_s[2 * NB * 16];        /* [tile parity][block][row] super-scale */
     __shared__ float xs_s[MT * NB];
 
     const int lane = threadIdx.x & 63;
     const int sw = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int r = lane & 15, q = lane >> 4;
-    const uint32_t row0 = blockIdx.x * 16;
-    const uint32_t row = row0 + (uint32_t)r < rows ? row0 + (uint32_t)r : rows - 1;
+    const uint32_t ntiles = (rows + 15) / 16;
 
+    /* once per workgroup: the codebook and the activation scales */
     for (int i = threadIdx.x; i < 2048; i += 64 * S) {
         /* bytes {-1, 0, 1} -> {0, 1, 2}: add 1 to the low 7 bits of every
          * byte (no carry out of a byte), then flip bit 7 back */
@@ -80,21 +82,39 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w), 0, rows * NB * kIQ1MBytes, kRawBuf);
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(x), 0, MT * NB * kQ8KBytes, kRawBuf);
-    const uint32_t woff = row * NB * kIQ1MBytes;
     uint32_t xoff[TS];   /* token r + 16s (clamped), bytes 16q.. of chunk 0 */
 #pragma unroll
     for (int s = 0; s < TS; ++s) {
         const int t = r + 16 * s < MT ? r + 16 * s : MT - 1;
         xoff[s] = (uint32_t)(t * NB * kQ8KBytes + 4 + 16 * q);
     }
-    auto load = [&](int k) {
-        int b = sw + S * k;
+    const int qhi = q >> 1, qlo = q & 1;
+    const uint32_t soff = (uint32_t)(6 * qhi + 3 * qlo);   /* sub-scale bits inside the group's u16 */
+
+    /* The workgroup's work is a stream of items n = (j-th tile of the
+     * workgroup, k-th round of its blocks): tile blockIdx.x + j * gridDim.x,
+     * block sw + S * k.  Loads run P items ahead, across tile boundaries.
+     * After the last round of a tile a barrier publishes its E and scales
+     * (double-buffered by tile parity) and one lane per (row, token) runs the
+     * tile's fp32 chains. */
+    const uint32_t my_tiles = ntiles > blockIdx.x ? (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    const int items = (int)my_tiles * KB;
+    auto tile_of = [&](int n) {
+        const uint32_t j = (uint32_t)(n / KB);
+        const uint32_t t = blockIdx.x + j * gridDim.x;
+        return t < ntiles ? t : ntiles - 1;   /* past the end: re-read the last tile, unused */
+    };
+    auto load = [&](int n) {
+        const uint32_t tile = tile_of(n);
+        const uint32_t row = tile * 16 + (uint32_t)r < rows ? tile * 16 + (uint32_t)r : rows - 1;
+        int b = sw + S * (n % KB);
         b = b < NB ? b : NB - 1;   /* past the end: re-read the last block, unused */
+        const uint32_t woff = row * NB * kIQ1MBytes;
         IQBlk<TS> c;
 #pragma unroll
         for (int h = 0; h < 7; ++h) {
-            const int2v v = __builtin_bit_cast(int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff + 8 * h,
-                                                                                           b * kIQ1MBytes, 0));
+            const int2v v = __builtin_bit_cast(
+                int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff + 8 * h, b * kIQ1MBytes, 0));
             const uint32_t lo = (uint32_t)v[0], hi = (uint32_t)v[1];
             if (h < 4) { c.qs[2 * h] = lo; c.qs[2 * h + 1] = hi; }
             else if (h < 6) { c.qh[2 * (h - 4)] = lo; c.qh[2 * (h - 4) + 1] = hi; }
@@ -107,18 +127,13 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
                 c.a[s][cc] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[s] + 64 * cc, b * kQ8KBytes, 0);
         return c;
     };
-    IQBlk<TS> slot[P];
-#pragma unroll
-    for (int i = 0; i < P; ++i) slot[i] = load(i);
 
-    const int qhi = q >> 1, qlo = q & 1;
-    const uint32_t soff = (uint32_t)(6 * qhi + 3 * qlo);   /* sub-scale bits inside the group's u16 */
-
-    auto block = [&](const IQBlk<TS> &c, int k) {
-        const int b = sw + S * k;
-        int4v d1[TS], d2[TS], d3[TS];
+    auto block = [&](const IQBlk<TS> &c, int n) {
+        const int b = sw + S * (n % KB);
+        const int par = (n / KB) & 1;
+        int4v d1[TS], d2[TS];
 #pragma unroll
-        for (int s = 0; s < TS; ++s) d1[s] = d2[s] = d3[s] = (int4v){0, 0, 0, 0};
+        for (int t = 0; t < TS; ++t) d1[t] = d2[t] = (int4v){0, 0, 0, 0};
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
             /* group 2cc + q/2, sections 2(q&1) and 2(q&1)+1 of this row */
@@ -129,87 +144,98 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
             const uint32_t i1 = (ib >> 8) | ((hb & 0x70u) << 4);
             const uint32_t s = 2u * ((c.sc[cc >> 1] >> (16 * (cc & 1) + soff)) & 7u) + 1u;
             const uint2 g0 = grid_s[i0], g1 = grid_s[i1];
-            /* s * (g + 1) per byte: the bytes g + 1 in {0, 1, 2} select from
-             * the byte table {0, s, 2s} */
-            const uint32_t lut = s * 0x00020100u;
-            int4v bw, bs, bb;
+            /* s * g per byte: the bytes g + 1 in {0, 1, 2} select from the
+             * byte table {-s, 0, s} */
+            const uint32_t ns = 256u - s;
+            const uint32_t lut = ns | (s << 16);
+            int4v bw, bs;
             bw[0] = (int)__builtin_amdgcn_perm(0u, lut, g0.x);
             bw[1] = (int)__builtin_amdgcn_perm(0u, lut, g0.y);
             bw[2] = (int)__builtin_amdgcn_perm(0u, lut, g1.x);
             bw[3] = (int)__builtin_amdgcn_perm(0u, lut, g1.y);
-            /* s and -s in every byte */
-            const uint32_t sp = __builtin_amdgcn_perm(0u, s, 0u), sn = __builtin_amdgcn_perm(0u, 256u - s, 0u);
-            const uint32_t c0 = (hb & 0x08u) ? sn : sp, c1 = (hb & 0x80u) ? sn : sp;
+            /* s * sign in every byte of each section */
+            const uint32_t c0 = __builtin_amdgcn_perm(0u, (hb & 0x08u) ? ns : s, 0u);
+            const uint32_t c1 = __builtin_amdgcn_perm(0u, (hb & 0x80u) ? ns : s, 0u);
             bs[0] = (int)c0; bs[1] = (int)c0; bs[2] = (int)c1; bs[3] = (int)c1;
-            bb[0] = bb[1] = bb[2] = bb[3] = (int)sp;
 #pragma unroll
             for (int t = 0; t < TS; ++t) {
                 d1[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(c.a[t][cc], bw, d1[t], 0, 0, 0);
                 d2[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(c.a[t][cc], bs, d2[t], 0, 0, 0);
-                d3[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(c.a[t][cc], bb, d3[t], 0, 0, 0);
             }
         }
-        if (b >= NB) return;
+        if (b < NB) {
 #pragma unroll
-        for (int t = 0; t < TS; ++t)
+            for (int t = 0; t < TS; ++t)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int tok = 16 * t + 4 * q + j;
-                if (tok < MT) e_s[(b * MT + tok) * 16 + r] = (float)(8 * (d1[t][j] - d3[t][j]) + d2[t][j]);
+                for (int j = 0; j < 4; ++j) {
+                    const int tok = 16 * t + 4 * q + j;
+                    if (tok < MT) e_s[((par * NB + b) * MT + tok) * 16 + r] = (float)(8 * d1[t][j] + d2[t][j]);
+                }
+            if (q == 0) {
+                const uint32_t u0 = c.sc[0] & 0xffffu, u1 = c.sc[0] >> 16, u2 = c.sc[1] & 0xffffu,
+                               u3 = c.sc[1] >> 16;
+                const uint32_t bits = (u0 >> 12) | ((u1 >> 8) & 0x00f0u) | ((u2 >> 4) & 0x0f00u) | (u3 & 0xf000u);
+                d_s[(par * NB + b) * 16 + r] = f16_to_f32(bits);
             }
-        if (q == 0) {
-            const uint32_t u0 = c.sc[0] & 0xffffu, u1 = c.sc[0] >> 16, u2 = c.sc[1] & 0xffffu, u3 = c.sc[1] >> 16;
-            const uint32_t bits = (u0 >> 12) | ((u1 >> 8) & 0x00f0u) | ((u2 >> 4) & 0x0f00u) | (u3 & 0xf000u);
-            d_s[b * 16 + r] = f16_to_f32(bits);
+        }
+        if (n % KB == KB - 1) {
+            /* the tile's last round: publish, then its fp32 chains in block
+             * order, total += d * (E * 0.125) with d = dscale * xs */
+            __syncthreads();
+            const uint32_t row0 = tile_of(n) * 16;
+            for (int idx = threadIdx.x; idx < 16 * MT; idx += 64 * S) {
+                const int rr = idx & 15, t = idx >> 4;
+                float total = 0.0f;
+                for (int bb = 0; bb < NB; ++bb) {
+                    const float d = fmul_rn(d_s[(par * NB + bb) * 16 + rr], xs_s[t * NB + bb]);
+                    total = fadd_rn(total, fmul_rn(d, fmul_rn(e_s[((par * NB + bb) * MT + t) * 16 + rr], 0.125f)));
+                }
+                if (row0 + (uint32_t)rr < rows) y[(size_t)t * ldy + row0 + rr] = total;
+            }
         }
     };
 
-    constexpr int kFull = KB / P, kRem = KB % P;
+    IQBlk<TS> slot[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) slot[i] = load(i);
+    const int full = items / P, rem = items % P;
 #pragma unroll 1
-    for (int it = 0; it < kFull; ++it) {
+    for (int it = 0; it < full; ++it) {
 #pragma unroll
         for (int i = 0; i < P; ++i) {
-            const int k = it * P + i;
-            block(slot[i], k);
-            slot[i] = load(k + P);
+            const int n = it * P + i;
+            block(slot[i], n);
+            slot[i] = load(n + P);
         }
     }
 #pragma unroll
-    for (int i = 0; i < kRem; ++i) block(slot[i], KB - kRem + i);
-    __syncthreads();
-
-    /* fp32 chains in block order: total += d * (E * 0.125), d = dscale * xs */
-    for (int idx = threadIdx.x; idx < 16 * MT; idx += 64 * S) {
-        const int rr = idx & 15, t = idx >> 4;
-        float total = 0.0f;
-        for (int b = 0; b < NB; ++b) {
-            const float d = fmul_rn(d_s[b * 16 + rr], xs_s[t * NB + b]);
-            total = fadd_rn(total, fmul_rn(d, fmul_rn(e_s[(b * MT + t) * 16 + rr], 0.125f)));
-        }
-        if (row0 + (uint32_t)rr < rows) y[(size_t)t * ldy + row0 + rr] = total;
-    }
+    for (int i = 0; i < P; ++i)
+        if (i < rem) block(slot[i], full * P + i);
 }
 
 namespace {
 
-/* wavefronts per 16-row tile (measured on MI355X): 8 for rows of 20..40
- * blocks, 4 for the 68-block rows of the FFN down projection */
-int iq1m_waves(int nb) { return nb >= 68 ? 4 : 8; }
+/* Launch shape (measured on MI355X): 4 wavefronts per 16-row tile, 512
+ * workgroups striding over the tiles, 2 blocks in flight per wavefront. */
+constexpr int kIQ1MWaves = 4;
+constexpr uint32_t kIQ1MGroups = 512;
+constexpr int kIQ1MPrefetch = 2;
 
 template <int MT, int NB, int S>
 void launch_iq1m_s(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, const uint2 *grid,
                    hipStream_t stream)
 {
-    hipLaunchKernelGGL((gemm_iq1m_mfma<MT, NB, S, 2>), dim3((rows + 15) / 16), dim3(64 * S), 0, stream, w, x, y, ldy,
-                       rows, grid);
+    const uint32_t tiles = (rows + 15) / 16;
+    const uint32_t groups = tiles < kIQ1MGroups ? tiles : kIQ1MGroups;
+    hipLaunchKernelGGL((gemm_iq1m_mfma<MT, NB, S, kIQ1MPrefetch>), dim3(groups), dim3(64 * S), 0, stream, w, x, y,
+                       ldy, rows, grid);
 }
 
 template <int MT, int NB>
 bool launch_iq1m_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, const uint2 *grid,
                        hipStream_t stream)
 {
-    if (iq1m_waves(NB) == 4) launch_iq1m_s<MT, NB, 4>(w, x, y, ldy, rows, grid, stream);
-    else launch_iq1m_s<MT, NB, 8>(w, x, y, ldy, rows, grid, stream);
+    launch_iq1m_s<MT, NB, kIQ1MWaves>(w, x, y, ldy, rows, grid, stream);
     return hipGetLastError() == hipSuccess;
 }
 
