@@ -282,6 +282,12 @@ __global__ __launch_bounds__(256) void deltanet_out_quant_kernel(float *__restri
 
 constexpr int kAttnHeads = 24, kKVHeads = 4, kAttnDim = 256, kKVDim = 1024, kQDim = 6144;
 constexpr int kScoreChunk = 64;
+/* q heads per lane in the score kernel (more heads: fewer wavefronts, more
+ * independent chains per lane) */
+#ifndef Q38_SCORE_HPL
+#define Q38_SCORE_HPL 2
+#endif
+constexpr int kScoreHeadsPerLane = Q38_SCORE_HPL;
 constexpr int kMaxLdsPositions = 32768;   /* softmax weights kept in LDS up to this many positions */
 
 /* q / gate split, per-head RMSNorm of q and k (q_norm / k_norm weights),
@@ -334,26 +340,30 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float *__restrict__ q_ou
     else kc[h * kAttnDim + i] = y;
 }
 
-/* Attention scores of row t (blockIdx.z) for the six q heads sharing KV head
- * blockIdx.x, positions blockIdx.y*64 .. +63 (one per lane):
- * score = fmaf-chain over the 256 dims in order, times 1/16
- * (qwen38_model.c:854-862).  Each lane reads its K row once for six
+/* Attention scores of row t (blockIdx.z) for HPL of the six q heads sharing
+ * a KV head (head group blockIdx.x), positions blockIdx.y*64 .. +63 (one per
+ * lane): score = fmaf-chain over the 256 dims in order, times 1/16
+ * (qwen38_model.c:854-862).  Each lane reads its K row once for HPL
  * independent chains.  scores is [rows][24][context]. */
+template <int HPL>
 __global__ __launch_bounds__(64) void attn_scores_kernel(float *__restrict__ scores, const float *__restrict__ q,
                                                          const float *__restrict__ key_cache, int context,
                                                          const uint32_t *__restrict__ position_ptr)
 {
-    const int kvh = blockIdx.x, chunk = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
+    constexpr int kGroups = 6 / HPL;   /* head groups per KV head */
+    const int hg = blockIdx.x, chunk = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
+    const int kvh = hg / kGroups, h0 = kvh * 6 + (hg % kGroups) * HPL;
     const int n = (int)*position_ptr + t + 1;
     if (chunk * kScoreChunk >= n) return;
-    __shared__ float qs[6][kAttnDim];
-    const float *qsrc = q + (size_t)t * kQDim + kvh * 6 * kAttnDim;
-    for (int e = lane; e < 6 * kAttnDim; e += 64) qs[e >> 8][e & 255] = qsrc[e];
+    __shared__ float qs[HPL][kAttnDim];
+    const float *qsrc = q + (size_t)t * kQDim + h0 * kAttnDim;
+    for (int e = lane; e < HPL * kAttnDim; e += 64) qs[e >> 8][e & 255] = qsrc[e];
     __syncthreads();
     const int p = chunk * kScoreChunk + lane;
     if (p >= n) return;
     const float4 *k4 = reinterpret_cast<const float4 *>(key_cache + (size_t)p * kKVDim + kvh * kAttnDim);
-    float acc[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[HPL];
+    for (int j = 0; j < HPL; ++j) acc[j] = 0.0f;
     for (int c = 0; c < 4; ++c) {
         float4 kk[16];
         for (int m = 0; m < 16; ++m) kk[m] = k4[c * 16 + m];
@@ -361,12 +371,12 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(float *__restrict__ sco
             const float kv[4] = {kk[m].x, kk[m].y, kk[m].z, kk[m].w};
             for (int e = 0; e < 4; ++e) {
                 const int d = c * 64 + 4 * m + e;
-                for (int j = 0; j < 6; ++j) acc[j] = __builtin_fmaf(qs[j][d], kv[e], acc[j]);
+                for (int j = 0; j < HPL; ++j) acc[j] = __builtin_fmaf(qs[j][d], kv[e], acc[j]);
             }
         }
     }
-    for (int j = 0; j < 6; ++j)
-        scores[((size_t)t * kAttnHeads + kvh * 6 + j) * context + p] = __fmul_rn(acc[j], 0.0625f);
+    for (int j = 0; j < HPL; ++j)
+        scores[((size_t)t * kAttnHeads + h0 + j) * context + p] = __fmul_rn(acc[j], 0.0625f);
 }
 
 /* Softmax and weighted sum of V for q head blockIdx.x of row blockIdx.y
@@ -508,8 +518,9 @@ void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_
 {
     attn_prep_kernel<<<dim3(kAttnHeads + kKVHeads + 1, rows), 256, 0, stream>>>(
         q_buf, q_and_gate, key, value, in_stride, q_norm, k_norm, rope, key_cache, value_cache, position, 0);
-    attn_scores_kernel<<<dim3(kKVHeads, (context + kScoreChunk - 1) / kScoreChunk, rows), 64, 0, stream>>>(
-        scores, q_buf, key_cache, context, position);
+    attn_scores_kernel<kScoreHeadsPerLane>
+        <<<dim3(kKVHeads * 6 / kScoreHeadsPerLane, (context + kScoreChunk - 1) / kScoreChunk, rows), 64, 0, stream>>>(
+            scores, q_buf, key_cache, context, position);
     if (context <= kMaxLdsPositions)
         attn_output_kernel<true><<<dim3(kAttnHeads, rows), 256, (size_t)context * 4, stream>>>(
             attn, q_out, scores, q_and_gate, in_stride, value_cache, context, position);

@@ -344,15 +344,26 @@ __global__ __launch_bounds__(64 * S) void gemm_q4k_t32(const uint8_t *__restrict
 namespace {
 
 /* Launch shape (measured on MI355X for 2..4 tokens and 5120..34816 rows):
- * four wavefronts per 32-row tile, two blocks in flight per wavefront. */
+ * four wavefronts per 32-row tile, two blocks in flight per wavefront; a
+ * matrix with fewer tiles than the chip has compute units runs one
+ * workgroup per unit, so its wavefronts keep more blocks in flight. */
 constexpr int kT32Waves = 4, kT32Prefetch = 2;
+#ifndef Q38_T32_PREFETCH_NARROW
+#define Q38_T32_PREFETCH_NARROW 2
+#endif
+constexpr int kT32PrefetchNarrow = Q38_T32_PREFETCH_NARROW;
+constexpr uint32_t kT32NarrowTiles = 256;
 
 template <int MT, int NB>
 bool launch_t32_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, hipStream_t stream)
 {
     const uint32_t tiles32 = (rows + 31) / 32;
-    hipLaunchKernelGGL((gemm_q4k_t32<MT, NB, kT32Waves, kT32Prefetch>), dim3(tiles32), dim3(64 * kT32Waves), 0,
-                       stream, w, x, y, ldy, rows);
+    if (tiles32 < kT32NarrowTiles)
+        hipLaunchKernelGGL((gemm_q4k_t32<MT, NB, kT32Waves, kT32PrefetchNarrow>), dim3(tiles32), dim3(64 * kT32Waves),
+                           0, stream, w, x, y, ldy, rows);
+    else
+        hipLaunchKernelGGL((gemm_q4k_t32<MT, NB, kT32Waves, kT32Prefetch>), dim3(tiles32), dim3(64 * kT32Waves), 0,
+                           stream, w, x, y, ldy, rows);
     return hipGetLastError() == hipSuccess;
 }
 
