@@ -48,6 +48,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef int int4v __attribute__((ext_vector_type(4)));
+typedef short short2v __attribute__((ext_vector_type(2)));
 
 constexpr int kRows16 = 16;
 constexpr int kBlockBytes = 144;
@@ -117,7 +118,9 @@ __global__ __launch_bounds__(64 * S) void gemm_q4k_t32(const uint8_t *__restrict
     constexpr int NO = (MT + S - 1) / S;       /* chains' tokens per wavefront */
     constexpr int RP = S > 1 ? 2 : 1;
     constexpr int RING = S > 1 ? RP * S * (MT + 1) * 64 : 1;
-    __shared__ int2 pairs_s[MT * NB * 4];
+    /* 32-element sub-block sums of the activations, int16 (|sum| <= 4096),
+     * sub-blocks 2c and 2c + 1 of chunk c in one dword */
+    __shared__ __attribute__((aligned(16))) int16_t sub_s[MT * NB * 8];
     __shared__ float xs_s[MT * NB];
     __shared__ uint4 ring[RING];   /* [parity][wavefront][token | header][lane] */
 
@@ -191,8 +194,7 @@ __global__ __launch_bounds__(64 * S) void gemm_q4k_t32(const uint8_t *__restrict
                 if (i >= kTotal) break;
                 const int blk = i / 9, k = i - blk * 9;
                 if (k == 0) xs_s[blk] = __uint_as_float(v[u]);
-                else reinterpret_cast<int *>(pairs_s)[blk * 8 + (k - 1)] =
-                    (int)(int16_t)(v[u] & 0xffffu) + ((int)v[u] >> 16);
+                else sub_s[blk * 8 + (k - 1)] = (int16_t)((int)(int16_t)(v[u] & 0xffffu) + ((int)v[u] >> 16));
             }
         }
     }
@@ -262,27 +264,36 @@ __global__ __launch_bounds__(64 * S) void gemm_q4k_t32(const uint8_t *__restrict
         }
     };
 
+    /* the token-independent part of a block header for this lane's chains:
+     * d and dmin as fp32, and the 6-bit mins (qwen38_quant.c:131-143) of
+     * sub-blocks 2c, 2c + 1 of chunks c = q and q + 2 as u16 pairs */
+    const uint32_t min_sel = q ? 0x0c030c02u : 0x0c010c00u;
+    auto chain_header = [&](const uint4 &h) {
+        const uint32_t mw0 = h.z & 0x3f3f3f3fu, mw1 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+        return make_uint4(__float_as_uint(f16_to_f32(h.x)), __float_as_uint(f16_to_f32(h.x >> 16)),
+                          __builtin_amdgcn_perm(0u, mw0, min_sel), __builtin_amdgcn_perm(0u, mw1, min_sel));
+    };
+
     /* advance chain slot j (token t) over block b with W values wq and the
-     * block header h */
+     * chain header h; the min sums m0 * s(2c) + m1 * s(2c + 1) are exact
+     * int32 dot products */
     auto chain = [&](int j, int t, int b, const uint4 &h, const float (&wq)[4]) {
         const float xs = xs_s[t * NB + b];
-        const float d = f16_to_f32(h.x), dmin = f16_to_f32(h.x >> 16);
-        const float dx = fmul_rn(d, xs), mx = -fmul_rn(dmin, xs);
+        const float dx = fmul_rn(__uint_as_float(h.x), xs), mx = -fmul_rn(__uint_as_float(h.y), xs);
 #pragma unroll
         for (int k = 0; k < 4; ++k) acc[j][k] = __builtin_fmaf(dx, wq[k], acc[j][k]);
-        /* 6-bit mins of chunks q and q + 2 */
-        const uint32_t mw[2] = {h.z & 0x3f3f3f3fu, ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u)};
+        const uint32_t *sub2 = reinterpret_cast<const uint32_t *>(sub_s) + (t * NB + b) * 4 + q;
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
-            const int m0 = (int)((mw[c2] >> sh) & 0xffu), m1 = (int)((mw[c2] >> (sh + 8)) & 0xffu);
-            const int2 pr = pairs_s[(t * NB + b) * 4 + 2 * c2 + q];
-            accm[j][c2] = __builtin_fmaf(mx, (float)mad24(m0, pr.x, mul24(m1, pr.y)), accm[j][c2]);
+            const int msum = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2v, c2 ? h.w : h.z),
+                                                    __builtin_bit_cast(short2v, sub2[2 * c2]), 0, false);
+            accm[j][c2] = __builtin_fmaf(mx, (float)msum, accm[j][c2]);
         }
     };
 
     auto round = [&](const Blk<TS> &c, int k) {
         float wv[MT][4];
-        const uint4 hd = c.h;
+        const uint4 hd = chain_header(c.h);
         block_sums(c, wv);
         if (S == 1) {
 #pragma unroll
