@@ -186,10 +186,9 @@ def test_tiled_repack_and_gemm_bit_exact(hip, oracle, device, rows, width):
 
 @pytest.mark.parametrize("m", [2, 3, 4, 8])
 def test_tiled_gemm_full_shape_matches_row_major(hip, device, m):
-    """34816x5120 (fused gate|up) and 5120x17408 (down): tiled = row-major kernels.
-    34816 and 24584 rows have more 32-row tiles than the chip holds
-    workgroups, so workgroups run several tiles; 24584 rows end on an unpaired
-    16-row tile that is not the first tile of its workgroup."""
+    """34816x5120 (fused gate|up) and 5120x17408 (down): tiled = row-major kernels;
+    24584x5120 ends on an unpaired 16-row tile at a size where the 32-row
+    kernel's workgroups run in more than one wave over the chip."""
     for rows, width in ((34816, 5120), (5120, 17408), (24584, 5120)):
         w = synth.matrix(Q4_K, rows, width, seed=m + rows)
         wd = to_dev(w, device)
