@@ -55,6 +55,49 @@ __device__ __forceinline__ int quad_sum(int v)
     return v + quad_xor2(v);
 }
 
+/* Whole-wavefront reductions with DPP row operations (no LDS traffic);
+ * every lane must be active and the result is uniform.  Within each row of
+ * 16 lanes: quad swaps, row_half_mirror, row_mirror; then row_bcast15 into
+ * rows 1 and 3 and row_bcast31 into rows 2 and 3, so lane 63 holds the
+ * total. */
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int dpp_move(int old, int v)
+{
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWS, 0xF, false);
+}
+
+/* maximum over the wavefront of non-NaN values (fmaxf) */
+__device__ __forceinline__ float wave_max(float v)
+{
+    v = fmaxf(v, __int_as_float(dpp_move<0xB1>(0, __float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_move<0x4E>(0, __float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_move<0x141>(0, __float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_move<0x140>(0, __float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_move<0x142, 0xA>(__float_as_int(v), __float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_move<0x143, 0xC>(__float_as_int(v), __float_as_int(v))));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ double dpp_move_f64(double v)
+{
+    const int lo = dpp_move<CTRL, ROWS>(0, __double2loint(v)), hi = dpp_move<CTRL, ROWS>(0, __double2hiint(v));
+    return __hiloint2double(hi, lo);
+}
+
+/* sum over the wavefront (rows outside a broadcast's row mask add 0.0) */
+__device__ __forceinline__ double wave_sum(double v)
+{
+    v += dpp_move_f64<0xB1>(v);
+    v += dpp_move_f64<0x4E>(v);
+    v += dpp_move_f64<0x141>(v);
+    v += dpp_move_f64<0x140>(v);
+    v += dpp_move_f64<0x142, 0xA>(v);
+    v += dpp_move_f64<0x143, 0xC>(v);
+    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), 63),
+                            __builtin_amdgcn_readlane(__double2loint(v), 63));
+}
+
 /* IEEE correctly rounded fp32 division and square root.  In this toolchain
  * __fdiv_rn is plain '/', and __fsqrt_rn is the approximate native square
  * root unless OCML_BASIC_ROUNDED_OPERATIONS is defined, so neither is used;

@@ -20,16 +20,19 @@ namespace q38 {
 
 /* ---- RMSNorm + Q8_K ------------------------------------------------------ */
 
-/* One block of 256 threads per row (rmsnorm_quant_row). */
+/* One block of kNormThreads threads per 5120-element row
+ * (rmsnorm_quant_row): ten wavefronts of two Q8_K blocks each, so that the
+ * per-block reductions of the quantisation run on ten SIMDs. */
+constexpr int kNormThreads = 640;
 template <int NV, bool ADD>
-__global__ __launch_bounds__(256) void norm_quant_kernel(float *__restrict__ norm_out, long long norm_stride,
+__global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(float *__restrict__ norm_out, long long norm_stride,
                                                          uint8_t *__restrict__ q_out, int q_stride_blocks,
                                                          float *__restrict__ hidden, long long in_stride,
                                                          const float *__restrict__ branch,
                                                          const float *__restrict__ weight)
 {
     const long long row = blockIdx.x;
-    rmsnorm_quant_row<NV, ADD>(norm_out ? norm_out + row * norm_stride : nullptr,
+    rmsnorm_quant_row<kNormThreads, NV, ADD>(norm_out ? norm_out + row * norm_stride : nullptr,
                                q_out ? q_out + (size_t)row * q_stride_blocks * kQ8KBytes : nullptr,
                                hidden + row * in_stride, ADD ? branch + row * in_stride : nullptr, weight);
 }
@@ -457,11 +460,11 @@ void launch_norm_quant(float *norm_out, long long norm_stride, uint8_t *q_out, i
                        long long in_stride, const float *branch, const float *weight, int rows, hipStream_t stream)
 {
     if (branch)
-        norm_quant_kernel<5, true><<<rows, 256, 0, stream>>>(norm_out, norm_stride, q_out, q_stride_blocks, hidden,
-                                                              in_stride, branch, weight);
+        norm_quant_kernel<2, true><<<rows, kNormThreads, 0, stream>>>(norm_out, norm_stride, q_out, q_stride_blocks,
+                                                                       hidden, in_stride, branch, weight);
     else
-        norm_quant_kernel<5, false><<<rows, 256, 0, stream>>>(norm_out, norm_stride, q_out, q_stride_blocks, hidden,
-                                                               in_stride, nullptr, weight);
+        norm_quant_kernel<2, false><<<rows, kNormThreads, 0, stream>>>(norm_out, norm_stride, q_out, q_stride_blocks,
+                                                                        hidden, in_stride, nullptr, weight);
 }
 
 void launch_add(float *hidden, const float *branch, long long n, hipStream_t stream)

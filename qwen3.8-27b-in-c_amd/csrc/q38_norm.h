@@ -27,7 +27,7 @@ __device__ float block_sum_finish(double s, const float *x, int n, Post post)
     static_assert(THREADS % 64 == 0 && THREADS <= 1024, "block size");
     __shared__ double partial[THREADS / 64];
     __shared__ float result;
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = s;
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -71,34 +71,35 @@ struct FloatPost {
 
 /* ---- RMSNorm + Q8_K of one row ---------------------------------------------- */
 
-/* One 256-thread block over one row of N = 1024*NV floats at h.  ADD: the
+/* One block of T threads over one row of N = 4*T*NV floats at h.  ADD: the
  * row first becomes h + branch (the residual add of qwen38_model.c:975/983,
  * written back to h).  Then y = (x * scale) * w with scale =
  * 1/sqrtf(mean + 1e-6) (q38_rmsnorm, :426-435), written to norm_out (when
  * not null) and quantised to Q8_K into q_out (when not null): float4
- * f = tid + 256*j holds elements 4f..4f+3, i.e. lane `tid % 64` of Q8_K
- * block 4*j + tid/64, so each wavefront quantises whole blocks. */
-template <int NV, bool ADD>
+ * f = tid + T*j holds elements 4f..4f+3, i.e. lane `tid % 64` of Q8_K
+ * block (T/64)*j + tid/64, so each wavefront quantises whole blocks. */
+template <int T, int NV, bool ADD>
 __device__ __forceinline__ void rmsnorm_quant_row(float *__restrict__ norm_out, uint8_t *__restrict__ q_out,
                                                   float *__restrict__ h, const float *__restrict__ branch,
                                                   const float *__restrict__ weight)
 {
-    constexpr int N = 1024 * NV;
+    static_assert(T % 64 == 0, "whole wavefronts");
+    constexpr int N = 4 * T * NV;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     /* the weights do not depend on the row: load them with the row */
     const float4 *w4 = reinterpret_cast<const float4 *>(weight);
     float4 w[NV], x[NV];
-    for (int j = 0; j < NV; ++j) w[j] = w4[tid + 256 * j];
-    for (int j = 0; j < NV; ++j) x[j] = reinterpret_cast<const float4 *>(h)[tid + 256 * j];
+    for (int j = 0; j < NV; ++j) w[j] = w4[tid + T * j];
+    for (int j = 0; j < NV; ++j) x[j] = reinterpret_cast<const float4 *>(h)[tid + T * j];
     if (ADD) {
         const float4 *b = reinterpret_cast<const float4 *>(branch);
         for (int j = 0; j < NV; ++j) {
-            const float4 bj = b[tid + 256 * j];
+            const float4 bj = b[tid + T * j];
             x[j].x = __fadd_rn(x[j].x, bj.x);
             x[j].y = __fadd_rn(x[j].y, bj.y);
             x[j].z = __fadd_rn(x[j].z, bj.z);
             x[j].w = __fadd_rn(x[j].w, bj.w);
-            reinterpret_cast<float4 *>(h)[tid + 256 * j] = x[j];
+            reinterpret_cast<float4 *>(h)[tid + T * j] = x[j];
         }
     }
     double s = 0.0;
@@ -108,7 +109,7 @@ __device__ __forceinline__ void rmsnorm_quant_row(float *__restrict__ norm_out, 
         s += (double)__fmul_rn(x[j].z, x[j].z);
         s += (double)__fmul_rn(x[j].w, x[j].w);
     }
-    const float mean = block_sum_finish<256>(s, h, N, MeanPost{(double)N});
+    const float mean = block_sum_finish<T>(s, h, N, MeanPost{(double)N});
     const float scale = rms_scale(mean);
     float v[NV][4];
     for (int j = 0; j < NV; ++j) {
@@ -117,9 +118,9 @@ __device__ __forceinline__ void rmsnorm_quant_row(float *__restrict__ norm_out, 
         v[j][2] = __fmul_rn(__fmul_rn(x[j].z, scale), w[j].z);
         v[j][3] = __fmul_rn(__fmul_rn(x[j].w, scale), w[j].w);
         if (norm_out)
-            reinterpret_cast<float4 *>(norm_out)[tid + 256 * j] = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+            reinterpret_cast<float4 *>(norm_out)[tid + T * j] = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
     }
-    if (q_out) wave_quantize_q8k_multi<NV>(v, q_out + (size_t)wave * kQ8KBytes, 4 * kQ8KBytes, lane);
+    if (q_out) wave_quantize_q8k_multi<NV>(v, q_out + (size_t)wave * kQ8KBytes, (T / 64) * kQ8KBytes, lane);
 }
 
 }  // namespace q38
