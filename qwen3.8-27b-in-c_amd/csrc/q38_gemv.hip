@@ -193,6 +193,9 @@ __device__ __forceinline__ int q6k_w(const Lane<kQ6K> &r, const uint8_t *a, int 
     const int av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
     const int upper = l >= 4 ? 1 : 0;
     int w = 0;
+    /* every r.sc[] index is a compile-time constant (a lane-dependent index
+     * would keep the array in scratch memory): scale 8h + 2j + upper is
+     * byte 2(j & 1) + upper of word 2h + j/2 */
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -201,14 +204,15 @@ __device__ __forceinline__ int q6k_w(const Lane<kQ6K> &r, const uint8_t *a, int 
             const uint32_t lo4 = (j < 2 ? low : (low >> 4)) & 0x0f0f0f0fu;
             const uint32_t hi2 = ((r.qh[h] >> (2 * j)) & 0x03030303u) << 4;
             const int q = (int)(lo4 | hi2);
-            const int si = 8 * h + 2 * j + upper;
-            w = mad24(dot4z(q, av[4 * h + j]), sbyte_of(r.sc[si >> 2], si & 3), w);
+            w = mad24(dot4z(q, av[4 * h + j]), sbyte_of(r.sc[2 * h + (j >> 1)], 2 * (j & 1) + upper), w);
         }
     }
     const uint32_t s = *reinterpret_cast<const uint32_t *>(a + kSumsOff + 4 * l);
     const int s0 = (int)(int16_t)(s & 0xffffu), s1 = (int)s >> 16;
-    const int i0 = 2 * l, i1 = 2 * l + 1;
-    const int offset = 32 * mad24(s0, sbyte_of(r.sc[i0 >> 2], i0 & 3), mul24(s1, sbyte_of(r.sc[i1 >> 2], i1 & 3)));
+    /* scales 2l and 2l + 1: bytes 2(l & 1), 2(l & 1) + 1 of word l / 2 */
+    const uint32_t sw = (l & 4) ? ((l & 2) ? r.sc[3] : r.sc[2]) : ((l & 2) ? r.sc[1] : r.sc[0]);
+    const int b0 = 2 * (l & 1);
+    const int offset = 32 * mad24(s0, sbyte_of(sw, b0), mul24(s1, sbyte_of(sw, b0 + 1)));
     return w - offset;
 }
 
