@@ -57,10 +57,11 @@ constexpr uint32_t kRawBuffer = 0x00020000u;        /* raw 32-bit buffer resourc
 
 __device__ __forceinline__ half2v h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
 
-/* fp16 pair (n, n) for an integer n < 1024: (1024 + n) - 1024 */
-__device__ __forceinline__ half2v pair_n(uint32_t n)
+/* fp16 pair (n, n) for the byte n of w that `sel` picks (sel = 0x07000700
+ * + k * 0x00010001 for byte k): (1024 + n) - 1024 */
+__device__ __forceinline__ half2v pair_byte(uint32_t w, uint32_t sel)
 {
-    const half2v v = h2(__builtin_amdgcn_perm(0x64646464u, n, 0x07000700u));
+    const half2v v = h2(__builtin_amdgcn_perm(0x64646464u, w, sel));
     return v - (half2v){(_Float16)1024.0f, (_Float16)1024.0f};
 }
 
@@ -217,7 +218,8 @@ __global__ __launch_bounds__(64 * S) void gemm_q4k_t32(const uint8_t *__restrict
 
     uint32_t kMask = 0x000f000fu, kMaskHi = 0x00f000f0u, kMagic = 0x64006400u;
     asm volatile("" : "+v"(kMask), "+v"(kMaskHi), "+v"(kMagic));
-    const int sh = 16 * q;
+    /* byte 2q of a scale word: sub-block 2q (low nibbles) of its chunk */
+    const uint32_t sel_lo = 0x07000700u + (uint32_t)(2 * q) * 0x00010001u;
 
     /* integer sums of one block: wv[t][k] = W[b][2k + q] of token t */
     auto block_sums = [&](const Blk<TS> &c, float (&wv)[MT][4]) {
@@ -229,7 +231,7 @@ __global__ __launch_bounds__(64 * S) void gemm_q4k_t32(const uint8_t *__restrict
         Scale sc[2];
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
-            const half2v SL = pair_n((scw[c2] >> sh) & 0xffu), SH = pair_n((scw[c2] >> (sh + 8)) & 0xffu);
+            const half2v SL = pair_byte(scw[c2], sel_lo), SH = pair_byte(scw[c2], sel_lo + 0x00010001u);
             sc[c2].sl = SL;
             sc[c2].nl = SL * (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f};
             sc[c2].sh16 = SH * (half2v){(_Float16)0.0625f, (_Float16)0.0625f};
