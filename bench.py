@@ -340,14 +340,14 @@ def run_decode(torch, args):
     t_prefill = time.perf_counter() - t0
     token = int(np.argmax(logits))
     for _ in range(warmup):
-        accepted, _ = model.speculative_greedy(token, 0xFFFFFFFF, args.draft)
+        accepted, _ = model.speculative_greedy(token, 0xFFFFFFFF, args.draft, logits=False)
         token = int(accepted[-1])
     produced = 0
     counts = []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        accepted, _ = model.speculative_greedy(token, 0xFFFFFFFF, args.draft)
+        accepted, _ = model.speculative_greedy(token, 0xFFFFFFFF, args.draft, logits=False)
         counts.append(len(accepted))
         produced += len(accepted)
         token = int(accepted[-1])

@@ -337,6 +337,10 @@ struct Q38Model {
     uint32_t ck_position = 0, ck_mtp_position = 0;
 
     hipStream_t stream = nullptr;
+    /* second stream (default priority) for the logits download, which then
+     * overlaps the MTP catch-up on `stream` */
+    hipStream_t copy_stream = nullptr;
+    hipEvent_t logits_ready = nullptr;
     const void *grid = nullptr;
     /* state */
     /* recurrent state: kRecurrentStateSlots slots of [48 layers][...]; layer r's
@@ -353,6 +357,7 @@ struct Q38Model {
     uint8_t *q8k = nullptr;
     /* params[0] = position of row 0 of the current step, params[1 + r] = slot of recurrent layer r */
     uint32_t *tokens = nullptr, *params = nullptr, *targets = nullptr, *drafts = nullptr, *accept = nullptr;
+    uint32_t *words = nullptr;   /* one allocation: drafts [0, 16), targets [16, 32), accept [32, 48) */
     float *argmax_pv = nullptr;
     uint32_t *argmax_pi = nullptr;
     /* host side */
@@ -619,7 +624,7 @@ void release(Q38Model *m)
                        &m->branch, &m->wide0, &m->qbuf, &m->attn, &m->scores, &m->logits, &m->target_norm,
                        &m->argmax_pv};
     for (float **p : fbufs) dfree(*p);
-    uint32_t **ubufs[] = {&m->tokens, &m->params, &m->targets, &m->drafts, &m->accept, &m->argmax_pi};
+    uint32_t **ubufs[] = {&m->tokens, &m->params, &m->words, &m->argmax_pi};
     for (uint32_t **p : ubufs) dfree(*p);
     dfree(m->q8k);
     if (m->weights) (void)hipFree(m->weights);
@@ -630,6 +635,9 @@ void release(Q38Model *m)
     if (m->host_words) (void)hipHostFree(m->host_words);
     if (m->host_params) (void)hipHostFree(m->host_params);
     for (auto &g : m->graphs) (void)hipGraphExecDestroy(g.second);
+    if (m->copy_stream) (void)hipStreamSynchronize(m->copy_stream);
+    if (m->logits_ready) (void)hipEventDestroy(m->logits_ready);
+    if (m->copy_stream) (void)hipStreamDestroy(m->copy_stream);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
 }
@@ -648,9 +656,8 @@ bool allocate_state(Q38Model *m)
               dalloc(&m->scores, (size_t)B * kAttnHeads * ctx) &&
               dalloc(&m->logits, (size_t)B * kVocab) && dalloc(&m->target_norm, (size_t)B * kHidden) &&
               dalloc(&m->q8k, (size_t)B * (kFFN / 256) * kQ8KBytes) && dalloc(&m->tokens, B) &&
-              dalloc(&m->params, (size_t)kParamSets * kParamWords) && dalloc(&m->targets, B) &&
-              dalloc(&m->drafts, B + 1) &&
-              dalloc(&m->accept, B + 3) && dalloc(&m->argmax_pv, (size_t)B * q38::argmax_chunks(kVocab)) &&
+              dalloc(&m->params, (size_t)kParamSets * kParamWords) && dalloc(&m->words, 48) &&
+              dalloc(&m->argmax_pv, (size_t)B * q38::argmax_chunks(kVocab)) &&
               dalloc(&m->argmax_pi, (size_t)B * q38::argmax_chunks(kVocab)) &&
               hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_logits), kVocab * sizeof(float)),
                      "pinned logits") &&
@@ -658,6 +665,9 @@ bool allocate_state(Q38Model *m)
               hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_params),
                                    (size_t)kParamSets * kParamWords * sizeof(uint32_t)), "pinned parameters");
     if (!ok) return false;
+    m->drafts = m->words;
+    m->targets = m->words + 16;
+    m->accept = m->words + 32;
     /* RoPE table: theta starts at the position and is multiplied by
      * powf(1e7, -2/64) per pair; cosf/sinf of the host C library, exactly the
      * values q38_rope computes (qwen38_model.c:697-713). */
@@ -948,15 +958,21 @@ bool linear_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count
     }
     float *conv = m->conv_state + (size_t)r * kQKV * 3;
     float *delta = m->delta_state + (size_t)r * kVHeads * kHeadDim * kHeadDim;
-    q38::launch_deltanet_prep(m->wide0, ld, (int)g.first[2], (int)g.first[3], conv, (long long)conv_count(),
-                              s.params + 1 + r, (int)count, L.conv.f32(), L.a.f32(), L.dt.f32(), m->stream);
     if (tr) {
+        /* the layer trace prints the prepared q/k/v: separate kernels */
+        q38::launch_deltanet_prep(m->wide0, ld, (int)g.first[2], (int)g.first[3], conv, (long long)conv_count(),
+                                  s.params + 1 + r, (int)count, L.conv.f32(), L.a.f32(), L.dt.f32(), m->stream);
         trace(m, "dn_qkv-", layer, m->wide0, kQKV);
         trace(m, "dn_beta-", layer, m->wide0 + g.first[2], kVHeads);
         trace(m, "dn_alpha-", layer, m->wide0 + g.first[3], kVHeads);
+        q38::launch_deltanet_state(m->attn, delta, (long long)delta_count(), s.params + 1 + r, (int)count, m->wide0,
+                                   ld, (int)g.first[2], (int)g.first[3], m->query_scale, m->stream);
+    } else if (!q38::launch_deltanet_fused(m->attn, delta, (long long)delta_count(), s.params + 1 + r, (int)count,
+                                           m->wide0, ld, (int)g.first[2], (int)g.first[3], m->query_scale, conv,
+                                           (long long)conv_count(), L.conv.f32(), L.a.f32(), L.dt.f32(),
+                                           m->stream)) {
+        return report("unsupported DeltaNet batch");
     }
-    q38::launch_deltanet_state(m->attn, delta, (long long)delta_count(), s.params + 1 + r, (int)count, m->wide0, ld,
-                               (int)g.first[2], (int)g.first[3], m->query_scale, m->stream);
     if (tr) trace(m, "dn_core-", layer, m->attn, kLinV);
     q38::launch_deltanet_out_quant(m->attn, m->q8k, m->wide0 + g.first[1], ld, L.ssm_norm.f32(), (int)count,
                                    m->stream);
@@ -1158,9 +1174,10 @@ Q38Model *q38_model_open_gguf(const char *path, uint32_t context_length)
     if (!path || context_length == 0) return nullptr;
     Q38Model *m = new Q38Model();
     m->context_length = context_length;
-    bool ok = m->gguf.open(path) && validate_base(m) && hip_ok(hipStreamCreateWithFlags(&m->stream,
-                                                                                          hipStreamNonBlocking),
-                                                                "stream");
+    bool ok = m->gguf.open(path) && validate_base(m) &&
+              hip_ok(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "stream") &&
+              hip_ok(hipStreamCreateWithFlags(&m->copy_stream, hipStreamNonBlocking), "stream") &&
+              hip_ok(hipEventCreateWithFlags(&m->logits_ready, hipEventDisableTiming), "event");
     ok = ok && (m->grid = q38::iq1m_grid_for_current_device()) != nullptr;
     ok = ok && upload(m->gguf, &m->weights);
     const uint8_t *base = static_cast<const uint8_t *>(m->weights);
@@ -1357,13 +1374,11 @@ int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_toke
         q38::launch_accept(m->accept, m->targets, m->drafts + 1, k, m->stream);
         return true;
     });
-    uint32_t *hw = m->host_words;   /* [64..) drafts, [80..) targets, [96..) acceptance */
+    /* drafts, targets and the acceptance in one download: host words
+     * [64..) mirror m->words (drafts at 64, targets at 80, acceptance at 96) */
+    uint32_t *hw = m->host_words;
     ok = ok &&
-         hip_ok(hipMemcpyAsync(hw + 64, m->drafts + 1, k * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream),
-                "drafts") &&
-         hip_ok(hipMemcpyAsync(hw + 80, m->targets, k * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream),
-                "targets") &&
-         hip_ok(hipMemcpyAsync(hw + 96, m->accept, (k + 3) * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream),
+         hip_ok(hipMemcpyAsync(hw + 64, m->words, 48 * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream),
                 "acceptance") &&
          hip_ok(hipStreamSynchronize(m->stream), "acceptance");
     if (!ok) {
@@ -1372,7 +1387,7 @@ int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_toke
         (void)hipStreamSynchronize(m->stream);
         return 0;
     }
-    const uint32_t *drafts = hw + 64, *targets = hw + 80;
+    const uint32_t *drafts = hw + 65, *targets = hw + 80;
     uint32_t n = k;
     for (uint32_t i = 0; i < k; ++i)
         if (drafts[i] == stop_token) { n = i + 1; break; }
@@ -1404,14 +1419,20 @@ int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_toke
     (void)restore_mtp(m);
     write_params(m, kParamCatchup, m->ck_mtp_position);
     const Step sc = step_of(m, kParamCatchup, m->drafts);
-    ok = hip_ok(hipMemcpyAsync(m->host_logits, m->logits + (size_t)(consumed - 1) * kVocab, kVocab * sizeof(float),
-                               hipMemcpyDeviceToHost, m->stream), "logits download") &&
+    /* the verify logits are final (the stream is synchronised) and the
+     * catch-up does not write them: download on the copy stream meanwhile */
+    ok = hip_ok(hipEventRecord(m->logits_ready, m->stream), "event") &&
+         hip_ok(hipStreamWaitEvent(m->copy_stream, m->logits_ready, 0), "event") &&
+         hip_ok(hipMemcpyAsync(m->host_logits, m->logits + (size_t)(consumed - 1) * kVocab, kVocab * sizeof(float),
+                               hipMemcpyDeviceToHost, m->copy_stream), "logits download") &&
          flush_params(m) && run_step(m, graph_key(kGraphCatchup, consumed), [&] { return mtp_catchup(m, sc, consumed); }) &&
-         hip_ok(hipStreamSynchronize(m->stream), "catch-up");
+         hip_ok(hipStreamSynchronize(m->stream), "catch-up") &&
+         hip_ok(hipStreamSynchronize(m->copy_stream), "logits download");
     if (!ok) {
         restore_target(m);
         (void)restore_mtp(m);
         (void)hipStreamSynchronize(m->stream);
+        (void)hipStreamSynchronize(m->copy_stream);
         return 0;
     }
     m->mtp_position = m->ck_mtp_position + consumed;

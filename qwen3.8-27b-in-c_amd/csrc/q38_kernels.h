@@ -62,6 +62,12 @@ void launch_deltanet_prep(float *qkv, long long ld, int beta_off, int alpha_off,
 void launch_deltanet_state(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,
                            const float *qkv, long long ld, int beta_off, int alpha_off, float query_scale,
                            hipStream_t stream);
+/* launch_deltanet_prep + launch_deltanet_state in one kernel (1..8 rows;
+ * false otherwise); q/k/v, beta and alpha in qkv stay untransformed */
+bool launch_deltanet_fused(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,
+                           const float *qkv, long long ld, int beta_off, int alpha_off, float query_scale,
+                           float *conv_state, long long conv_stride, const float *conv_w, const float *ssm_a,
+                           const float *ssm_dt, hipStream_t stream);
 void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, long long z_stride, const float *ssm_norm,
                                int rows, hipStream_t stream);
 /* full attention over `rows` rows at positions *position + t: prep (norms,

@@ -236,6 +236,133 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
     }
 }
 
+/* deltanet_prep_kernel and deltanet_state_kernel in one launch, for up to
+ * kFusedRows rows.  Block (h, cg) = (blockIdx.x / 16, blockIdx.x % 16) owns
+ * the state columns 8cg..8cg+7 of value head h as in deltanet_state_kernel,
+ * and first redoes, into LDS, the prep arithmetic of what those columns
+ * read: the conv + SiLU + L2 norm of q and k head kh = h % 16 (thread i:
+ * q channel i, k channel i - 128), conv + SiLU of its eight v channels, and
+ * beta / alpha of head h.  Each conv channel's next state slots are written
+ * by one block: q/k channels by block (kh, 0), v channels by their owner. */
+constexpr int kFusedRows = 8;
+
+__device__ __forceinline__ void conv_silu_rows(float *y_out, int y_stride, const float *qkv, long long ld, int ch,
+                                               const float *conv_state, float *conv_out, long long conv_stride,
+                                               uint32_t slot0, int rows, const float *conv_w)
+{
+    const float *st = conv_state + (size_t)(slot0 % kStateSlots) * conv_stride + (size_t)ch * 3;
+    const float4 k = reinterpret_cast<const float4 *>(conv_w)[ch];
+    float s0 = st[0], s1 = st[1], s2 = st[2];
+    float xs[kFusedRows];   /* every row's input in flight at once */
+#pragma unroll
+    for (int t = 0; t < kFusedRows; ++t) xs[t] = t < rows ? qkv[(long long)t * ld + ch] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < kFusedRows; ++t) {
+        if (t >= rows) break;
+        const float x = xs[t];
+        float value = 0.0f;
+        value = __fadd_rn(value, __fmul_rn(s0, k.x));
+        value = __fadd_rn(value, __fmul_rn(s1, k.y));
+        value = __fadd_rn(value, __fmul_rn(s2, k.z));
+        value = __fadd_rn(value, __fmul_rn(x, k.w));
+        s0 = s1;
+        s1 = s2;
+        s2 = x;
+        if (conv_out) {
+            float *o = conv_out + (size_t)((slot0 + t + 1) % kStateSlots) * conv_stride + (size_t)ch * 3;
+            o[0] = s0;
+            o[1] = s1;
+            o[2] = s2;
+        }
+        y_out[t * y_stride] = siluf_exact(value);
+    }
+}
+
+__global__ __launch_bounds__(256) void deltanet_fused_kernel(float *__restrict__ out, float *__restrict__ state,
+                                                             long long slot_stride,
+                                                             const uint32_t *__restrict__ slot_ptr, int rows,
+                                                             const float *__restrict__ qkv, long long ld,
+                                                             int beta_off, int alpha_off, float query_scale,
+                                                             float *__restrict__ conv_state, long long conv_stride,
+                                                             const float *__restrict__ conv_w,
+                                                             const float *__restrict__ ssm_a,
+                                                             const float *__restrict__ ssm_dt)
+{
+    __shared__ float qk_s[kFusedRows][256];   /* SiLU outputs: q of head kh (0..127), k (128..255) */
+    __shared__ float v_s[kFusedRows][8];
+    __shared__ float beta_s[kFusedRows], alpha_s[kFusedRows];
+    __shared__ double part_s[kFusedRows][4];
+    __shared__ float scale_s[kFusedRows][2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.x >> 4, cg = blockIdx.x & 15, kh = h % 16;
+    const int c = cg * 8 + (tid >> 5), l = tid & 31;
+    const uint32_t slot0 = *slot_ptr;
+    const size_t col_off = ((size_t)h * kHeadDim + c) * kHeadDim;
+    const float *s = state + (size_t)(slot0 % kStateSlots) * slot_stride + col_off;
+    float sv[4];
+    for (int a = 0; a < 4; ++a) sv[a] = s[32 * a + l];
+
+    /* prep (deltanet_prep_kernel, qwen38_model.c:720-757) */
+    const int ch = tid < 128 ? kh * kHeadDim + tid : kQKDim + kh * kHeadDim + (tid - 128);
+    conv_silu_rows(&qk_s[0][tid], 256, qkv, ld, ch, conv_state, h < 16 && cg == 0 ? conv_state : nullptr,
+                   conv_stride, slot0, rows, conv_w);
+    if (tid < 8)
+        conv_silu_rows(&v_s[0][tid], 8, qkv, ld, 2 * kQKDim + h * kHeadDim + cg * 8 + tid, conv_state, conv_state,
+                       conv_stride, slot0, rows, conv_w);
+    if (tid >= 64 && tid < 64 + rows) {
+        const float *row = qkv + (long long)(tid - 64) * ld;
+        beta_s[tid - 64] = sigmoidf_exact(row[beta_off + h]);
+        alpha_s[tid - 64] = __fmul_rn(ssm_a[h], softplusf_exact(__fadd_rn(row[alpha_off + h], ssm_dt[h])));
+    }
+    /* L2 norms of q and k per row: the double sum of squares of each
+     * 128-vector as block_sum_finish (two wavefronts each) */
+    for (int t = 0; t < rows; ++t) {
+        const float y = qk_s[t][tid];
+        const double sq = wave_sum((double)__fmul_rn(y, y));
+        if (lane == 0) part_s[t][wave] = sq;
+    }
+    __syncthreads();
+    if (tid < 2 * rows) {
+        const int t = tid >> 1, g = tid & 1;
+        const double total = part_s[t][2 * g] + part_s[t][2 * g + 1];
+        const FloatPost post;
+        const float lo = post(total * (1.0 - 0x1p-36)), hi = post(total * (1.0 + 0x1p-36));
+        float sum = lo;
+        if (lo != hi) {
+            double seq = 0.0;
+            for (int i = 0; i < kHeadDim; ++i) seq += (double)__fmul_rn(qk_s[t][128 * g + i], qk_s[t][128 * g + i]);
+            sum = post(seq);
+        }
+        scale_s[t][g] = div_rn(1.0f, fmaxf(sqrt_rn(sum), 1e-6f));
+    }
+    __syncthreads();
+
+    /* state update (deltanet_state_kernel) */
+    for (int t = 0; t < rows; ++t) {
+        const float decay = q38_expf(alpha_s[t]);
+        const float qs = scale_s[t][0], ks = scale_s[t][1];
+        float kv[4], qv[4];
+        for (int a = 0; a < 4; ++a) {
+            sv[a] = __fmul_rn(sv[a], decay);
+            kv[a] = __fmul_rn(qk_s[t][128 + 32 * a + l], ks);
+            qv[a] = __fmul_rn(qk_s[t][32 * a + l], qs);
+        }
+        float p = 0.0f;
+        for (int a = 0; a < 4; ++a) p = __builtin_fmaf(sv[a], kv[a], p);
+        const float pred = avx2_tree32(p);
+        const float delta = __fmul_rn(__fsub_rn(v_s[t][tid >> 5], pred), beta_s[t]);
+        float *s_out = state + (size_t)((slot0 + t + 1) % kStateSlots) * slot_stride + col_off;
+        float r = 0.0f;
+        for (int a = 0; a < 4; ++a) {
+            sv[a] = __builtin_fmaf(kv[a], delta, sv[a]);
+            s_out[32 * a + l] = sv[a];
+            r = __builtin_fmaf(sv[a], qv[a], r);
+        }
+        const float result = avx2_tree32(r);
+        if (l == 0) out[(size_t)t * kLinV + h * kHeadDim + c] = __fmul_rn(result, query_scale);
+    }
+}
+
 /* Per value head: RMSNorm over 128 (ssm_norm weight), then out *= silu(z)
  * (qwen38_model.c:785-791), then Q8_K of the 6144-wide result for the
  * ssm_out projection.  One block of 256 threads per pair of heads (one Q8_K
@@ -499,6 +626,18 @@ void launch_deltanet_state(float *attn, float *delta_state, long long slot_strid
 {
     deltanet_state_kernel<<<kVHeads * kHeadDim / 8, 256, 0, stream>>>(attn, delta_state, slot_stride, slot, rows,
                                                                      qkv, ld, beta_off, alpha_off, query_scale);
+}
+
+bool launch_deltanet_fused(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,
+                           const float *qkv, long long ld, int beta_off, int alpha_off, float query_scale,
+                           float *conv_state, long long conv_stride, const float *conv_w, const float *ssm_a,
+                           const float *ssm_dt, hipStream_t stream)
+{
+    if (rows < 1 || rows > kFusedRows) return false;
+    deltanet_fused_kernel<<<kVHeads * kHeadDim / 8, 256, 0, stream>>>(attn, delta_state, slot_stride, slot, rows, qkv,
+                                                                     ld, beta_off, alpha_off, query_scale, conv_state,
+                                                                     conv_stride, conv_w, ssm_a, ssm_dt);
+    return true;
 }
 
 void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, long long z_stride, const float *ssm_norm,

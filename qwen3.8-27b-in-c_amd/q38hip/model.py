@@ -96,14 +96,18 @@ class Model:
             raise RuntimeError("q38_model_mtp_forward failed")
         return self._copy(p)
 
-    def speculative_greedy(self, token, stop_token, draft_count):
+    def speculative_greedy(self, token, stop_token, draft_count, logits=True):
+        """(accepted token ids, logits after the last one); with logits=False
+        the second item is None and the library's logits buffer is not copied
+        (a caller that only follows the accepted tokens, as the reference's
+        CLI loop does)."""
         accepted = np.zeros(max(int(draft_count), 1), dtype=np.uint32)
         count = ctypes.c_uint32(0)
         p = _f32p()
         if not self.lib.q38_model_speculative_greedy(self.handle, int(token), int(stop_token), int(draft_count),
                                                      accepted.ctypes.data, ctypes.byref(count), ctypes.byref(p)):
             raise RuntimeError("q38_model_speculative_greedy failed")
-        return accepted[:count.value].copy(), self._copy(p)
+        return accepted[:count.value].copy(), (self._copy(p) if logits else None)
 
     def forward_token_layers(self, token, layers):
         hidden = np.zeros(HIDDEN, dtype=np.float32)
