@@ -414,10 +414,7 @@ constexpr int kAttnHeads = 24, kKVHeads = 4, kAttnDim = 256, kKVDim = 1024, kQDi
 constexpr int kScoreChunk = 64;
 /* q heads per lane in the score kernel (more heads: fewer wavefronts, more
  * independent chains per lane) */
-#ifndef Q38_SCORE_HPL
-#define Q38_SCORE_HPL 2
-#endif
-constexpr int kScoreHeadsPerLane = Q38_SCORE_HPL;
+constexpr int kScoreHeadsPerLane = 2;
 constexpr int kMaxLdsPositions = 32768;   /* softmax weights kept in LDS up to this many positions */
 
 /* q / gate split, per-head RMSNorm of q and k (q_norm / k_norm weights),

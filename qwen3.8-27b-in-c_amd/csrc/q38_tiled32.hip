@@ -357,14 +357,14 @@ __global__ __launch_bounds__(64 * S) void gemm_q4k_t32(const uint8_t *__restrict
 namespace {
 
 /* Launch shape (measured on MI355X for 2..4 tokens and 5120..34816 rows):
- * four wavefronts per 32-row tile, two blocks in flight per wavefront; a
+ * four wavefronts per 32-row tile.  Wide matrices keep one block in flight
+ * per wavefront: 103 VGPRs allow four wavefronts per SIMD (the LDS ring's
+ * limit too), which hides more latency than a deeper prefetch at three.  A
  * matrix with fewer tiles than the chip has compute units runs one
- * workgroup per unit, so its wavefronts keep more blocks in flight. */
-constexpr int kT32Waves = 4, kT32Prefetch = 2;
-#ifndef Q38_T32_PREFETCH_NARROW
-#define Q38_T32_PREFETCH_NARROW 2
-#endif
-constexpr int kT32PrefetchNarrow = Q38_T32_PREFETCH_NARROW;
+ * workgroup per unit (one wavefront per SIMD) and keeps two blocks in
+ * flight. */
+constexpr int kT32Waves = 4, kT32Prefetch = 1;
+constexpr int kT32PrefetchNarrow = 2;
 constexpr uint32_t kT32NarrowTiles = 256;
 
 template <int MT, int NB>
