@@ -702,14 +702,12 @@ bool clear_state(Q38Model *m)
 
 /* ---- layer trace (QWEN38_TRACE_LAYERS, as src/qwen38/qwen38_model.c:556-591) */
 
+/* read on every call (a step's launches are recorded once per graph, so a
+ * change reaches graph-replayed steps only when they are recorded) */
 bool trace_enabled()
 {
-    static int enabled = -1;
-    if (enabled < 0) {
-        const char *v = getenv("QWEN38_TRACE_LAYERS");
-        enabled = v && v[0] && strcmp(v, "0") != 0;
-    }
-    return enabled == 1;
+    const char *v = getenv("QWEN38_TRACE_LAYERS");
+    return v && v[0] && strcmp(v, "0") != 0;
 }
 
 /* same line format as the reference's q38_trace_vector; synchronises the

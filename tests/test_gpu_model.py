@@ -65,6 +65,23 @@ def test_hidden_after_first_blocks(model, golden):
     assert same_bits(h4, golden["hidden_l4"]), "max abs diff %g" % np.abs(h4 - golden["hidden_l4"]).max()
 
 
+def test_layer_trace_path(model, golden, capfd):
+    """QWEN38_TRACE_LAYERS=1 runs the DeltaNet prep and state update as two
+    kernels (the trace prints the prepared q/k/v between them) instead of the
+    fused kernel; blocks 0-2 are DeltaNet blocks, and the hidden state after 4
+    blocks is the same bit for bit."""
+    prompt = golden["prompt"]
+    os.environ["QWEN38_TRACE_LAYERS"] = "1"
+    try:
+        model.reset()
+        h4 = model.forward_token_layers(int(prompt[0]), 4)
+    finally:
+        del os.environ["QWEN38_TRACE_LAYERS"]
+    err = capfd.readouterr().err
+    assert "trace dn_qkv-0 " in err and "trace l_out-3 " in err
+    assert same_bits(h4, golden["hidden_l4"]), "max abs diff %g" % np.abs(h4 - golden["hidden_l4"]).max()
+
+
 def test_prefill_and_greedy_decode(model, golden):
     model.reset()
     logits = model.prefill(golden["prompt"])
