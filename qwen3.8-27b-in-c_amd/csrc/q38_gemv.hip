@@ -9,13 +9,8 @@
  * accumulator lanes of a row: each computes its own W[b][l] with
  * v_dot4_i32_i8 from 16 bytes of packed quants and runs the fmaf chain in a
  * register right away, so the integer and fp32 phases need no exchange.
- *
- * Rows with many blocks split the blocks over G groups of eight lanes
- * (block b goes to group b mod G); group 0 keeps the accumulators and takes
- * the other groups' (d_b, W) pairs over cross-lane reads in block order, so
- * the fp32 chain still runs over b = 0, 1, 2, ... exactly as in the
- * reference.  A wavefront holds 8/G rows; the loads of the next P blocks of
- * its rows are in flight while the current block is computed.
+ * A wavefront holds 8 rows; the loads of the next P blocks of its rows are
+ * in flight while the current block is computed.
  *
  * Activations (all M tokens, all blocks) are staged once per workgroup in
  * LDS, with the quants of each block permuted so that the 32 bytes a lane
@@ -218,26 +213,23 @@ __device__ __forceinline__ int q6k_w(const Lane<kQ6K> &r, const uint8_t *a, int 
 
 }  // namespace
 
-template <int TYPE, int MT, int G, int P>
+template <int TYPE, int MT, int P>
 __global__ __launch_bounds__(256) void gemv_lanes(const uint8_t *__restrict__ w, const uint8_t *__restrict__ x,
                                                   float *__restrict__ y, uint32_t ldy, uint32_t rows, uint32_t nb)
 {
-    constexpr int RW = 8 / G;   /* rows per wavefront */
     constexpr int BB = TYPE == kQ4K ? 144 : 210;
     extern __shared__ __align__(16) uint8_t act[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int l = lane & 7, grp = lane >> 3;
-    const int g = grp % G, rw = grp / G;
-    const uint32_t row = (blockIdx.x * 4u + (uint32_t)wave) * RW + (uint32_t)rw;
+    const int l = lane & 7, rw = lane >> 3;
+    const uint32_t row = (blockIdx.x * 4u + (uint32_t)wave) * 8u + (uint32_t)rw;
     const bool row_ok = row < rows;
     const uint8_t *rowp = w + (size_t)(row_ok ? row : 0) * nb * BB;
-    const int steps = ((int)nb + G - 1) / G;
+    const int steps = (int)nb;
 
     Lane<TYPE> ring[P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-        const int b = i * G + g;
-        if (row_ok && i < steps && b < (int)nb) ring[i].load(rowp + (size_t)b * BB, l);
+        if (row_ok && i < steps) ring[i].load(rowp + (size_t)i * BB, l);
         else ring[i].zero();
     }
     stage<TYPE>(act, x, MT * (int)nb);
@@ -246,20 +238,16 @@ __global__ __launch_bounds__(256) void gemv_lanes(const uint8_t *__restrict__ w,
     float acc[MT], accm[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = accm[t] = 0.0f;
-    const int chain_base = (rw * G) * 8 + l;   /* lane of group 0 with the same l */
 
     for (int k0 = 0; k0 < steps; k0 += P) {
 #pragma unroll
         for (int i = 0; i < P; ++i) {
             const int k = k0 + i;
             if (k >= steps) break;
-            const int b = k * G + g;
-            const bool valid = b < (int)nb;
             const Lane<TYPE> cur = ring[i];
-            /* refill this slot with step k + P */
-            const int bn = (k + P) * G + g;
-            if (row_ok && k + P < steps && bn < (int)nb) ring[i].load(rowp + (size_t)bn * BB, l);
-            const int bs = valid ? b : 0;
+            /* refill this slot with block k + P */
+            if (row_ok && k + P < steps) ring[i].load(rowp + (size_t)(k + P) * BB, l);
+            const int bs = k;
             float dw[MT], dm[MT];
             int iw[MT], im[MT];
             if constexpr (TYPE == kQ4K) {
@@ -285,32 +273,10 @@ __global__ __launch_bounds__(256) void gemv_lanes(const uint8_t *__restrict__ w,
                     dm[t] = 0.0f;
                 }
             }
-            if constexpr (G == 1) {
-                if (valid) {
 #pragma unroll
-                    for (int t = 0; t < MT; ++t) {
-                        acc[t] = __builtin_fmaf(dw[t], (float)iw[t], acc[t]);
-                        if (TYPE == kQ4K) accm[t] = __builtin_fmaf(dm[t], (float)im[t], accm[t]);
-                    }
-                }
-            } else {
-                /* group 0 takes blocks kG, kG+1, ... in order */
-#pragma unroll
-                for (int gg = 0; gg < G; ++gg) {
-                    const int src = chain_base + gg * 8;
-                    const bool ok = k * G + gg < (int)nb;
-#pragma unroll
-                    for (int t = 0; t < MT; ++t) {
-                        const float dv = read_lane(dw[t], src);
-                        const int wv = read_lane(iw[t], src);
-                        if (ok) acc[t] = __builtin_fmaf(dv, (float)wv, acc[t]);
-                        if (TYPE == kQ4K) {
-                            const float mv = read_lane(dm[t], src);
-                            const int iv = read_lane(im[t], src);
-                            if (ok) accm[t] = __builtin_fmaf(mv, (float)iv, accm[t]);
-                        }
-                    }
-                }
+            for (int t = 0; t < MT; ++t) {
+                acc[t] = __builtin_fmaf(dw[t], (float)iw[t], acc[t]);
+                if (TYPE == kQ4K) accm[t] = __builtin_fmaf(dm[t], (float)im[t], accm[t]);
             }
         }
     }
@@ -330,7 +296,7 @@ __global__ __launch_bounds__(256) void gemv_lanes(const uint8_t *__restrict__ w,
             m = fadd_rn(m, __shfl_down(m, 1, 8));
             v = fadd_rn(v, m);
         }
-        if (row_ok && g == 0 && l == 0) y[(size_t)t * ldy + row] = v;
+        if (row_ok && l == 0) y[(size_t)t * ldy + row] = v;
     }
 }
 
@@ -346,7 +312,7 @@ static bool launch_lanes_typed(const uint8_t *w, const uint8_t *x, float *y, uin
     if (MT < 2 || lds > 64 * 1024) return false;
     /* one row per 8 lanes, 32 rows per workgroup; P = 4 blocks in flight per row */
     const dim3 grid((rows + 31) / 32);
-    hipLaunchKernelGGL((gemv_lanes<TYPE, MT, 1, 4>), grid, dim3(256), lds, stream, w, x, y, ldy, rows, nb);
+    hipLaunchKernelGGL((gemv_lanes<TYPE, MT, 4>), grid, dim3(256), lds, stream, w, x, y, ldy, rows, nb);
     return true;
 }
 
