@@ -245,15 +245,22 @@ def trace_summary(directory, transactions=0):
     """calls / avg / min / max ns per (kernel, grid) of a rocprofv3 kernel
     trace.  With `transactions` > 0 the trace is that of the decode workload
     and only its transactions are summarised: the dispatches after the
-    prefill's last 8-token GEMM and before the roofline's weight repack,
-    reported per transaction."""
+    prefill's last 8-token GEMM (Q4_K tiled or IQ1_M) and before the first
+    kernel of the roofline run that follows (its weight repack or its
+    activation quantisation, which the model never launches), reported per
+    transaction."""
     rows = _trace_rows(directory)
     if transactions:
         names = [r["short"] for r in rows]
-        first = max(i for i, n in enumerate(names) if n.startswith("gemm_q4k_tiled<8")) + 1
-        last = max(i for i, n in enumerate(names) if n.startswith("repack_q4k_tiles"))
+        first = max(i for i, n in enumerate(names)
+                    if n.startswith("gemm_q4k_tiled<8") or n.startswith("gemm_iq1m_mfma<8")) + 1
+        last = min(i for i, n in enumerate(names)
+                   if i >= first and (n.startswith("repack_q4k_tiles") or n.startswith("quantize_q8k_kernel")))
         rows = rows[first:last]
-        wall = int(rows[-1]["End_Timestamp"]) - int(rows[0]["Start_Timestamp"])
+        # the wall clock stops at the last transaction's acceptance kernel:
+        # host work (the CPU baseline) may separate it from the roofline run
+        rows = rows[:max(i for i, r in enumerate(rows) if r["short"].startswith("accept_kernel")) + 1]
+        wall =int(rows[-1]["End_Timestamp"]) - int(rows[0]["Start_Timestamp"])
         busy = sum(r["ns"] for r in rows)
         print("%d dispatches over %d transactions: %.3f ms wall and %.3f ms kernel time per transaction"
               % (len(rows), transactions, wall / 1e6 / transactions, busy / 1e6 / transactions))
