@@ -19,10 +19,15 @@
  * exact in int32.
  *
  * Mapping (lane i of a wavefront, 16 weight rows per tile): r = i % 16 is the
- * weight row (B column) and the token (A row), q = i / 16 picks bytes
- * 16q..16q+15 of each 64-element chunk c: group g = 2c + q/2, sections
- * 2(q&1) and 2(q&1)+1, one sub-scale.  D register j of lane (r, q) is token
- * 4q + j of row r.  S wavefronts split the blocks of a tile (block b to
+ * weight row (B column) and the token (A row).  E is a sum over the whole
+ * block, so the 16-element sub-block a lane feeds to the K slots it owns may
+ * be chosen freely, as long as A and B agree: in chunk c lane q = i / 16 takes
+ * sub-block k = 4q + c (elements 16k..16k+15: index bytes qs[2k], qs[2k+1],
+ * high nibbles qh[k], sub-scale bits 3(k % 4) of scale word k / 4).  Over its
+ * four chunks a lane thus reads the row's qs[8q..8q+7], qh[4q..4q+3] and
+ * scale word q, 14 of the block's 56 bytes, and the four lanes of a row
+ * together read the block once.  D register j of lane (r, q) is token 4q + j
+ * of row r.  S wavefronts split the blocks of a tile (block b to
  * wavefront b mod S); every block's E and scale land in LDS, and after one
  * barrier one lane per (row, token) runs the fp32 chain in block order.
  * Workgroups stride over the tiles (the codebook is staged in LDS once per
@@ -43,7 +48,7 @@ constexpr uint32_t kRawBuf = 0x00020000u;   /* raw 32-bit buffer resource (gfx9)
 
 template <int TS>
 struct IQBlk {
-    uint32_t qs[8], qh[4], sc[2];   /* the row's block: indices, high bits, scales */
+    uint32_t qs[2], qh, sc[2];      /* the lane's index bytes and high nibbles, the scale words */
     int4v a[TS][4];                 /* activations per token set and chunk */
 };
 
@@ -82,14 +87,12 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w), 0, rows * NB * kIQ1MBytes, kRawBuf);
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(x), 0, MT * NB * kQ8KBytes, kRawBuf);
-    uint32_t xoff[TS];   /* token r + 16s (clamped), bytes 16q.. of chunk 0 */
+    uint32_t xoff[TS];   /* token r + 16s (clamped), quants of sub-block 4q */
 #pragma unroll
     for (int s = 0; s < TS; ++s) {
         const int t = r + 16 * s < MT ? r + 16 * s : MT - 1;
-        xoff[s] = (uint32_t)(t * NB * kQ8KBytes + 4 + 16 * q);
+        xoff[s] = (uint32_t)(t * NB * kQ8KBytes + 4 + 64 * q);
     }
-    const int qhi = q >> 1, qlo = q & 1;
-    const uint32_t soff = (uint32_t)(6 * qhi + 3 * qlo);   /* sub-scale bits inside the group's u16 */
 
     /* The workgroup's work is a stream of items n = (j-th tile of the
      * workgroup, k-th round of its blocks): tile blockIdx.x + j * gridDim.x,
@@ -111,20 +114,20 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
         b = b < NB ? b : NB - 1;   /* past the end: re-read the last block, unused */
         const uint32_t woff = row * NB * kIQ1MBytes;
         IQBlk<TS> c;
-#pragma unroll
-        for (int h = 0; h < 7; ++h) {
-            const int2v v = __builtin_bit_cast(
-                int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff + 8 * h, b * kIQ1MBytes, 0));
-            const uint32_t lo = (uint32_t)v[0], hi = (uint32_t)v[1];
-            if (h < 4) { c.qs[2 * h] = lo; c.qs[2 * h + 1] = hi; }
-            else if (h < 6) { c.qh[2 * (h - 4)] = lo; c.qh[2 * (h - 4) + 1] = hi; }
-            else { c.sc[0] = lo; c.sc[1] = hi; }
-        }
+        const int2v qs = __builtin_bit_cast(
+            int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff + 8 * q, b * kIQ1MBytes, 0));
+        c.qs[0] = (uint32_t)qs[0];
+        c.qs[1] = (uint32_t)qs[1];
+        c.qh = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, woff + 32 + 4 * q, b * kIQ1MBytes, 0);
+        const int2v sc = __builtin_bit_cast(
+            int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff + 48, b * kIQ1MBytes, 0));
+        c.sc[0] = (uint32_t)sc[0];
+        c.sc[1] = (uint32_t)sc[1];
 #pragma unroll
         for (int s = 0; s < TS; ++s)
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc)
-                c.a[s][cc] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[s] + 64 * cc, b * kQ8KBytes, 0);
+                c.a[s][cc] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[s] + 16 * cc, b * kQ8KBytes, 0);
         return c;
     };
 
@@ -134,15 +137,15 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
         int4v d1[TS], d2[TS];
 #pragma unroll
         for (int t = 0; t < TS; ++t) d1[t] = d2[t] = (int4v){0, 0, 0, 0};
+        const uint32_t scw = (q & 2 ? c.sc[1] : c.sc[0]) >> (16 * (q & 1));   /* scale word q */
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
-            /* group 2cc + q/2, sections 2(q&1) and 2(q&1)+1 of this row */
-            const uint32_t qsd = qhi ? c.qs[2 * cc + 1] : c.qs[2 * cc];
-            const uint32_t ib = (qsd >> (16 * qlo)) & 0xffffu;        /* two index bytes */
-            const uint32_t hb = (c.qh[cc] >> (8 * q)) & 0xffu;         /* two high nibbles */
+            /* sub-block 4q + cc of this row: two 8-element sections */
+            const uint32_t ib = (c.qs[cc >> 1] >> (16 * (cc & 1))) & 0xffffu;   /* two index bytes */
+            const uint32_t hb = (c.qh >> (8 * cc)) & 0xffu;                     /* two high nibbles */
             const uint32_t i0 = (ib & 0xffu) | ((hb & 7u) << 8);
             const uint32_t i1 = (ib >> 8) | ((hb & 0x70u) << 4);
-            const uint32_t s = 2u * ((c.sc[cc >> 1] >> (16 * (cc & 1) + soff)) & 7u) + 1u;
+            const uint32_t s = 2u * ((scw >> (3 * cc)) & 7u) + 1u;
             const uint2 g0 = grid_s[i0], g1 = grid_s[i1];
             /* s * g per byte: the bytes g + 1 in {0, 1, 2} select from the
              * byte table {-s, 0, s} */
