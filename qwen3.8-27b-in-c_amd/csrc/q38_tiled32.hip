@@ -27,8 +27,8 @@
  *
  * Work split.  S wavefronts share a 32-row tile; wavefront s computes the
  * integer sums of blocks b = s (mod S).  With S > 1 each round of S blocks
- * goes through a double-buffered LDS ring (per lane: W of every token and the
- * block header), and after a barrier wavefront s advances the chains of
+ * goes through a double-buffered LDS ring (per lane: W of every token, and
+ * in a ring of its own the three header dwords the chains use), and after a barrier wavefront s advances the chains of
  * tokens t = s (mod S) over the round's blocks in block order, so the fp32
  * order is the reference's.  The owner of a token applies the reference's
  * final tree: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) + ((m0+m2)+(m1+m3))
@@ -110,20 +110,38 @@ __device__ __forceinline__ half8 act8(uint32_t lo, uint32_t hi)
 
 }  // namespace
 
+/* LDS bytes of one workgroup of gemm_q4k_t32 */
+template <int MT, int NB, int S>
+constexpr int t32_lds_bytes()
+{
+    return MT * NB * 8 * 2 + MT * NB * 4 + (S > 1 ? 2 * S * 64 * (MT * 16 + 3 * 4) : 0);
+}
+
+/* Wavefronts per SIMD the registers are held to: one block in flight with a
+ * workgroup small enough for five per compute unit (64 KB of LDS per five,
+ * less a 512-byte allocation granule each) runs five; otherwise no bound. */
 template <int MT, int NB, int S, int P>
-__global__ __launch_bounds__(64 * S) void gemm_q4k_t32(const uint8_t *__restrict__ w, const uint8_t *__restrict__ x,
+constexpr int t32_min_waves()
+{
+    return P == 1 && S == 4 && t32_lds_bytes<MT, NB, S>() <= 163840 / 5 - 512 ? 5 : 1;
+}
+
+template <int MT, int NB, int S, int P>
+__global__ __launch_bounds__(64 * S, (t32_min_waves<MT, NB, S, P>())) void gemm_q4k_t32(const uint8_t *__restrict__ w, const uint8_t *__restrict__ x,
                                                        float *__restrict__ y, uint32_t ldy, uint32_t rows)
 {
     constexpr int TS = (MT + 3) / 4;           /* MFMA token sets of four */
     constexpr int KB = (NB + S - 1) / S;       /* rounds */
     constexpr int NO = (MT + S - 1) / S;       /* chains' tokens per wavefront */
     constexpr int RP = S > 1 ? 2 : 1;
-    constexpr int RING = S > 1 ? RP * S * (MT + 1) * 64 : 1;
+    constexpr int RING = S > 1 ? RP * S * MT * 64 : 1;
+    constexpr int HRING = S > 1 ? RP * S * 3 * 64 : 1;
     /* 32-element sub-block sums of the activations, int16 (|sum| <= 4096),
      * sub-blocks 2c and 2c + 1 of chunk c in one dword */
     __shared__ __attribute__((aligned(16))) int16_t sub_s[MT * NB * 8];
     __shared__ float xs_s[MT * NB];
-    __shared__ uint4 ring[RING];   /* [parity][wavefront][token | header][lane] */
+    __shared__ uint4 ring[RING];        /* [parity][wavefront][token][lane] */
+    __shared__ uint32_t hring[HRING];   /* [parity][wavefront][header dword][lane] */
 
     const int lane = threadIdx.x & 63;
     const int sw = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -267,27 +285,27 @@ __global__ __launch_bounds__(64 * S) void gemm_q4k_t32(const uint8_t *__restrict
     };
 
     /* the token-independent part of a block header for this lane's chains:
-     * d and dmin as fp32, and the 6-bit mins (qwen38_quant.c:131-143) of
-     * sub-blocks 2c, 2c + 1 of chunks c = q and q + 2 as u16 pairs */
+     * d and dmin (the block's fp16 pair), and the 6-bit mins
+     * (qwen38_quant.c:131-143) of sub-blocks 2c, 2c + 1 of chunks c = q and
+     * q + 2 as u16 pairs */
     const uint32_t min_sel = q ? 0x0c030c02u : 0x0c010c00u;
     auto chain_header = [&](const uint4 &h) {
         const uint32_t mw0 = h.z & 0x3f3f3f3fu, mw1 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
-        return make_uint4(__float_as_uint(f16_to_f32(h.x)), __float_as_uint(f16_to_f32(h.x >> 16)),
-                          __builtin_amdgcn_perm(0u, mw0, min_sel), __builtin_amdgcn_perm(0u, mw1, min_sel));
+        return make_uint3(h.x, __builtin_amdgcn_perm(0u, mw0, min_sel), __builtin_amdgcn_perm(0u, mw1, min_sel));
     };
 
     /* advance chain slot j (token t) over block b with W values wq and the
      * chain header h; the min sums m0 * s(2c) + m1 * s(2c + 1) are exact
      * int32 dot products */
-    auto chain = [&](int j, int t, int b, const uint4 &h, const float (&wq)[4]) {
+    auto chain = [&](int j, int t, int b, const uint3 &h, const float (&wq)[4]) {
         const float xs = xs_s[t * NB + b];
-        const float dx = fmul_rn(__uint_as_float(h.x), xs), mx = -fmul_rn(__uint_as_float(h.y), xs);
+        const float dx = fmul_rn(f16_to_f32(h.x), xs), mx = -fmul_rn(f16_to_f32(h.x >> 16), xs);
 #pragma unroll
         for (int k = 0; k < 4; ++k) acc[j][k] = __builtin_fmaf(dx, wq[k], acc[j][k]);
         const uint32_t *sub2 = reinterpret_cast<const uint32_t *>(sub_s) + (t * NB + b) * 4 + q;
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
-            const int msum = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2v, c2 ? h.w : h.z),
+            const int msum = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2v, c2 ? h.z : h.y),
                                                     __builtin_bit_cast(short2v, sub2[2 * c2]), 0, false);
             accm[j][c2] = __builtin_fmaf(mx, (float)msum, accm[j][c2]);
         }
@@ -295,27 +313,29 @@ __global__ __launch_bounds__(64 * S) void gemm_q4k_t32(const uint8_t *__restrict
 
     auto round = [&](const Blk<TS> &c, int k) {
         float wv[MT][4];
-        const uint4 hd = chain_header(c.h);
+        const uint3 hd = chain_header(c.h);
         block_sums(c, wv);
         if (S == 1) {
 #pragma unroll
             for (int t = 0; t < MT; ++t) chain(t, t, k, hd, wv[t]);
             return;
         }
-        const int base = ((k & 1) * S + sw) * (MT + 1) * 64;
+        const int base = ((k & 1) * S + sw) * MT * 64, hbase = ((k & 1) * S + sw) * 3 * 64;
 #pragma unroll
         for (int t = 0; t < MT; ++t)
             ring[base + t * 64 + lane] =
                 make_uint4(__float_as_uint(wv[t][0]), __float_as_uint(wv[t][1]), __float_as_uint(wv[t][2]),
                            __float_as_uint(wv[t][3]));
-        ring[base + MT * 64 + lane] = hd;
+        hring[hbase + lane] = hd.x;
+        hring[hbase + 64 + lane] = hd.y;
+        hring[hbase + 128 + lane] = hd.z;
         __syncthreads();
 #pragma unroll
         for (int f = 0; f < S; ++f) {
             const int b2 = f + S * k;
             if (b2 >= NB) break;
-            const int fb = ((k & 1) * S + f) * (MT + 1) * 64;
-            const uint4 h = ring[fb + MT * 64 + lane];
+            const int fb = ((k & 1) * S + f) * MT * 64, fhb = ((k & 1) * S + f) * 3 * 64;
+            const uint3 h = make_uint3(hring[fhb + lane], hring[fhb + 64 + lane], hring[fhb + 128 + lane]);
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
                 const uint4 v = ring[fb + own[j] * 64 + lane];
@@ -358,8 +378,8 @@ namespace {
 
 /* Launch shape (measured on MI355X for 2..4 tokens and 5120..34816 rows):
  * four wavefronts per 32-row tile.  Wide matrices keep one block in flight
- * per wavefront: 103 VGPRs allow four wavefronts per SIMD (the LDS ring's
- * limit too), which hides more latency than a deeper prefetch at three.  A
+ * per wavefront (up to five wavefronts per SIMD where the LDS allows, see
+ * t32_min_waves), which hides more latency than a deeper prefetch at three.  A
  * matrix with fewer tiles than the chip has compute units runs one
  * workgroup per unit (one wavefront per SIMD) and keeps two blocks in
  * flight. */
