@@ -31,7 +31,9 @@
  * wavefront b mod S); every block's E and scale land in LDS, and after one
  * barrier one lane per (row, token) runs the fp32 chain in block order.
  * Workgroups stride over the tiles (the codebook is staged in LDS once per
- * workgroup) and load ahead across tile boundaries.
+ * workgroup) and load ahead across tile boundaries.  For one token the
+ * activation quants (at most 17 KB) are staged in LDS too, once per
+ * workgroup, since every tile reads the same ones.
  */
 #include "q38_device.h"
 #include "q38_kernels.h"
@@ -61,7 +63,9 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
 {
     constexpr int TS = (MT + 15) / 16;   /* token sets of 16 (MT <= 8: one) */
     constexpr int KB = (NB + S - 1) / S;
+    constexpr bool STAGE = MT == 1;       /* activation quants in LDS */
     __shared__ uint2 grid_s[2048];        /* codebook entries as bytes grid + 1 */
+    __shared__ int4v act_s[STAGE ? MT * NB * 16 : 1];   /* [token][block][16 bytes] */
     __shared__ float e_s[2 * NB * MT * 16];   /* [tile parity][block][token][row] */
     __shared__ float d_s[2 * NB * 16];        /* [tile parity][block][row] super-scale */
     __shared__ float xs_s[MT * NB];
@@ -81,17 +85,23 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
     }
     for (int i = threadIdx.x; i < MT * NB; i += 64 * S)
         xs_s[i] = *reinterpret_cast<const float *>(x + (size_t)i * kQ8KBytes);
-    __syncthreads();   /* every wavefront reads the whole codebook */
-
     const __amdgpu_buffer_rsrc_t wr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w), 0, rows * NB * kIQ1MBytes, kRawBuf);
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(x), 0, MT * NB * kQ8KBytes, kRawBuf);
+    if (STAGE)
+        for (int i = threadIdx.x; i < MT * NB * 16; i += 64 * S)
+            act_s[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)((i >> 4) * kQ8KBytes + 4 + 16 * (i & 15)),
+                                                             0, 0);
+    __syncthreads();   /* every wavefront reads the whole codebook */
+
     uint32_t xoff[TS];   /* token r + 16s (clamped), quants of sub-block 4q */
+    int aidx[TS];        /* the same in act_s */
 #pragma unroll
     for (int s = 0; s < TS; ++s) {
         const int t = r + 16 * s < MT ? r + 16 * s : MT - 1;
         xoff[s] = (uint32_t)(t * NB * kQ8KBytes + 4 + 64 * q);
+        aidx[s] = t * NB * 16 + 4 * q;
     }
 
     /* The workgroup's work is a stream of items n = (j-th tile of the
@@ -127,7 +137,8 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
         for (int s = 0; s < TS; ++s)
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc)
-                c.a[s][cc] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[s] + 16 * cc, b * kQ8KBytes, 0);
+                c.a[s][cc] = STAGE ? act_s[aidx[s] + 16 * b + cc]
+                                   : __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[s] + 16 * cc, b * kQ8KBytes, 0);
         return c;
     };
 
