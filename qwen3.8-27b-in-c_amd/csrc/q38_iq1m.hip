@@ -229,9 +229,10 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
 
 namespace {
 
-/* Launch shape (measured on MI355X): 4 wavefronts per 16-row tile, 512
- * workgroups striding over the tiles, 2 blocks in flight per wavefront. */
-constexpr int kIQ1MWaves = 4;
+/* Launch shape (measured on MI355X): 4 wavefronts per 16-row tile (8 for
+ * one token, whose activations come from LDS), 512 workgroups striding over
+ * the tiles, 2 blocks in flight per wavefront. */
+constexpr int kIQ1MWaves = 4, kIQ1MWavesOneToken = 8;
 constexpr uint32_t kIQ1MGroups = 512;
 constexpr int kIQ1MPrefetch = 2;
 
@@ -249,7 +250,7 @@ template <int MT, int NB>
 bool launch_iq1m_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, const uint2 *grid,
                        hipStream_t stream)
 {
-    launch_iq1m_s<MT, NB, kIQ1MWaves>(w, x, y, ldy, rows, grid, stream);
+    launch_iq1m_s<MT, NB, MT == 1 ? kIQ1MWavesOneToken : kIQ1MWaves>(w, x, y, ldy, rows, grid, stream);
     return hipGetLastError() == hipSuccess;
 }
 
