@@ -67,7 +67,11 @@ WORKLOADS = {
     "q4k_tiled_m3": (12, 34816, 5120, 3, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 3 tokens"),
     "q4k_tiled_down_m3": (12, 5120, 17408, 3, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 3 tokens"),
     "iq1m_gemm_m3": (29, 34816, 5120, 3, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 3 tokens"),
+    "q4k_tiled_m8": (12, 34816, 5120, 8, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
+    "iq1m_gemm_m8": (29, 34816, 5120, 8, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
 }
+# dense matrix-core peaks of MI355X, TOP/s: the Q4_K GEMM runs fp16 MFMA, IQ1_M int8
+MFMA_PEAK_TOPS = {12: ("f16", 2500.0), 29: ("i8", 5000.0)}
 BLOCK = {12: 144, 14: 210, 29: 56}
 TYPE_NAME = {12: "Q4_K", 14: "Q6_K", 29: "IQ1_M"}
 COPY_BYTES = 64 << 20
@@ -220,6 +224,13 @@ def kernel_roofline(torch, workload, steps, warmup):
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None if traffic is None else int(traffic),
                 "kernel": "%s (%s)" % ("gemm_q4k_tiled" if tiled else "gemm_q8k", label),
                 "bytes_per_launch": nbytes, "launch_us": round(per_launch_ms * 1e3, 3)}
+    if (tiled and tokens > 1) or qtype == 29:
+        # matrix-core kernels: algorithmic multiply-adds (2 ops each) per second
+        kind, peak = MFMA_PEAK_TOPS[qtype]
+        ops = 2 * rows * width * tokens
+        tops = ops / (per_launch_ms * 1e-3) / 1e12
+        roofline["matrix"] = {"mfma": kind, "ops_per_launch": ops, "achieved": round(tops, 3), "peak": peak,
+                              "unit": "TOP/s", "frac": round(tops / peak, 5)}
     del weights, pool, base
     return per_launch_ms, wall, roofline, copies
 
