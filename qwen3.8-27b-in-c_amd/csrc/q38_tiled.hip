@@ -422,9 +422,9 @@ bool launch_gemm_q4k_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, floa
                            uint32_t nb, hipStream_t stream)
 {
     if (!rows || ldy < rows) return false;
-    /* 2..4 tokens over 4096 rows or more: 32 rows per wavefront (measured
-     * faster there; the 16-row kernel keeps small matrices and 5..8 tokens) */
-    if (m <= 4 && rows >= 4096) return launch_gemm_q4k_t32(m, w_tiled, x, y, ldy, rows, nb, stream);
+    /* 4096 rows or more: 32 rows per wavefront (measured faster there; the
+     * 16-row kernel keeps the small matrices) */
+    if (rows >= 4096) return launch_gemm_q4k_t32(m, w_tiled, x, y, ldy, rows, nb, stream);
     switch (nb) {
     case 20: return launch_tiled_nb<20>(m, w_tiled, x, y, ldy, rows, stream);
     case 24: return launch_tiled_nb<24>(m, w_tiled, x, y, ldy, rows, stream);

@@ -408,6 +408,10 @@ bool launch_t32_nb(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t
     case 2: return launch_t32_typed<2, NB>(w, x, y, ldy, rows, stream);
     case 3: return launch_t32_typed<3, NB>(w, x, y, ldy, rows, stream);
     case 4: return launch_t32_typed<4, NB>(w, x, y, ldy, rows, stream);
+    case 5: return launch_t32_typed<5, NB>(w, x, y, ldy, rows, stream);
+    case 6: return launch_t32_typed<6, NB>(w, x, y, ldy, rows, stream);
+    case 7: return launch_t32_typed<7, NB>(w, x, y, ldy, rows, stream);
+    case 8: return launch_t32_typed<8, NB>(w, x, y, ldy, rows, stream);
     default: return false;
     }
 }
@@ -415,7 +419,7 @@ bool launch_t32_nb(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t
 }  // namespace
 
 /* y[t * ldy + row] = W_row . x_t (t < m) from the 16-row tiled copy, 32 rows
- * per wavefront; 2..4 tokens (more tokens need a second MFMA token set and
+ * per wavefront; 2..8 tokens (5..8 take a second MFMA token set and about
  * twice the registers); false for unsupported shapes. */
 bool launch_gemm_q4k_t32(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                          uint32_t nb, hipStream_t stream)

@@ -168,8 +168,9 @@ def tiled_numpy(w, rows, width):
 def test_tiled_repack_and_gemm_bit_exact(hip, oracle, device, rows, width):
     """Tiled Q4_K copy (2..8 tokens, matrix cores) equals the oracle bit for bit;
     the repack equals the host restatement of the layout (zero-padded tail).
-    From 4096 rows on, 2..4 tokens run the 32-row kernel: 4112 and 5136 rows
-    end on an unpaired 16-row tile, 4100 also on a padded one."""
+    From 4096 rows on, 2..8 tokens run the 32-row kernel (5..8 with a second
+    token set): 4112 and 5136 rows end on an unpaired 16-row tile, 4100 also
+    on a padded one."""
     w = synth.matrix(Q4_K, rows, width, seed=rows + width)
     wd = to_dev(w, device)
     tiled = hip.repack_q4k_tiles(wd, width, rows)
