@@ -416,6 +416,7 @@ constexpr int kScoreChunk = 64;
  * independent chains per lane) */
 constexpr int kScoreHeadsPerLane = 2;
 constexpr int kMaxLdsPositions = 32768;   /* softmax weights kept in LDS up to this many positions */
+constexpr int kAttnLoadBatch = 32;        /* value-cache loads in flight per thread */
 
 /* q / gate split, per-head RMSNorm of q and k (q_norm / k_norm weights),
  * RoPE on dims 0..63 (pairs i, i+32) and the K/V cache write
@@ -558,13 +559,18 @@ __global__ __launch_bounds__(256) void attn_output_kernel(float *__restrict__ ou
     const float denominator = den_s;
     for (int p = tid; p < n; p += 256) e[p] = div_rn(e[p], denominator);
     __syncthreads();
+    /* the chain runs in position order; the V loads of kAttnLoadBatch
+     * positions are issued together, so a round trip to memory covers that
+     * many links */
     const float *vcol = value_cache + kvh * kAttnDim + tid;
     float o = 0.0f;
     int p = 0;
-    for (; p + 8 <= n; p += 8) {
-        float vv[8];
-        for (int k = 0; k < 8; ++k) vv[k] = vcol[(size_t)(p + k) * kKVDim];
-        for (int k = 0; k < 8; ++k) o = __builtin_fmaf(e[p + k], vv[k], o);
+    for (; p + kAttnLoadBatch <= n; p += kAttnLoadBatch) {
+        float vv[kAttnLoadBatch];
+#pragma unroll
+        for (int k = 0; k < kAttnLoadBatch; ++k) vv[k] = vcol[(size_t)(p + k) * kKVDim];
+#pragma unroll
+        for (int k = 0; k < kAttnLoadBatch; ++k) o = __builtin_fmaf(e[p + k], vv[k], o);
     }
     for (; p < n; ++p) o = __builtin_fmaf(e[p], vcol[(size_t)p * kKVDim], o);
     const float g = q_and_gate[(size_t)t * qg_stride + h * 2 * kAttnDim + kAttnDim + tid];
