@@ -417,6 +417,7 @@ constexpr int kScoreChunk = 64;
 constexpr int kScoreHeadsPerLane = 2;
 constexpr int kMaxLdsPositions = 32768;   /* softmax weights kept in LDS up to this many positions */
 constexpr int kAttnLoadBatch = 32;        /* value-cache loads in flight per thread */
+constexpr int kScoreLoads = 32;           /* float4 key loads in flight per lane */
 
 /* q / gate split, per-head RMSNorm of q and k (q_norm / k_norm weights),
  * RoPE on dims 0..63 (pairs i, i+32) and the K/V cache write
@@ -492,13 +493,17 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(float *__restrict__ sco
     const float4 *k4 = reinterpret_cast<const float4 *>(key_cache + (size_t)p * kKVDim + kvh * kAttnDim);
     float acc[HPL];
     for (int j = 0; j < HPL; ++j) acc[j] = 0.0f;
-    for (int c = 0; c < 4; ++c) {
-        float4 kk[16];
-        for (int m = 0; m < 16; ++m) kk[m] = k4[c * 16 + m];
-        for (int m = 0; m < 16; ++m) {
+    /* the chain runs over d in order; kScoreLoads float4 of the key row are
+     * loaded together */
+    for (int c = 0; c < 64 / kScoreLoads; ++c) {
+        float4 kk[kScoreLoads];
+#pragma unroll
+        for (int m = 0; m < kScoreLoads; ++m) kk[m] = k4[c * kScoreLoads + m];
+#pragma unroll
+        for (int m = 0; m < kScoreLoads; ++m) {
             const float kv[4] = {kk[m].x, kk[m].y, kk[m].z, kk[m].w};
             for (int e = 0; e < 4; ++e) {
-                const int d = c * 64 + 4 * m + e;
+                const int d = (c * kScoreLoads + m) * 4 + e;
                 for (int j = 0; j < HPL; ++j) acc[j] = __builtin_fmaf(qs[j][d], kv[e], acc[j]);
             }
         }
