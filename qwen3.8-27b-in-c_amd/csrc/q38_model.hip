@@ -552,10 +552,14 @@ __global__ __launch_bounds__(256) void attn_output_kernel(float *__restrict__ ou
     if (tid == 0) {
         float d = 0.0f;
         int p = 0;
-        for (; p + 8 <= n; p += 8) {
-            float a[8];
-            for (int k = 0; k < 8; ++k) a[k] = e[p + k];
-            for (int k = 0; k < 8; ++k) d = __fadd_rn(d, a[k]);
+        /* position order; the weights of kAttnLoadBatch positions are read
+         * ahead of their adds */
+        for (; p + kAttnLoadBatch <= n; p += kAttnLoadBatch) {
+            float a[kAttnLoadBatch];
+#pragma unroll
+            for (int k = 0; k < kAttnLoadBatch; ++k) a[k] = e[p + k];
+#pragma unroll
+            for (int k = 0; k < kAttnLoadBatch; ++k) d = __fadd_rn(d, a[k]);
         }
         for (; p < n; ++p) d = __fadd_rn(d, e[p]);
         den_s = d;
