@@ -69,7 +69,7 @@ int q38_tensor_gemv_q8_k(float *output, const Q38Q8KBlock *input,
                          const Q38GGUFTensor *tensor);
 
 /* replaces q38_tensor_gemm_q8_k, include/qwen38/qwen38_quant.h:48-50;
- * output is batch-major, output[token * rows + row] */
+ * output is batch-major, output[token * rows + row]; any batch_size >= 1 */
 int q38_tensor_gemm_q8_k(float *output, const Q38Q8KBlock *input,
                          uint32_t batch_size, uint64_t input_length,
                          const Q38GGUFTensor *tensor);
@@ -82,7 +82,10 @@ int q38hip_quantize_q8_k(Q38Q8KBlock *output, const float *input,
                          uint64_t length, uint32_t rows, void *stream);
 
 /* Device form of q38_tensor_gemm_q8_k (src/qwen38/qwen38_quant.c:2950-3169);
- * batch_size = 1 is q38_tensor_gemv_q8_k (:2833-2922).  batch_size <= 8. */
+ * batch_size = 1 is q38_tensor_gemv_q8_k (:2833-2922).  Any batch_size >= 1:
+ * the kernels take up to 8 tokens per launch, and larger batches run as
+ * consecutive launches over token chunks (every token's outputs are
+ * independent of the rest of the batch, so the bits are those of one call). */
 int q38hip_gemm_q8_k(float *output, const Q38Q8KBlock *input,
                      uint32_t batch_size, uint64_t input_length,
                      const Q38GGUFTensor *tensor, void *stream);
@@ -113,11 +116,35 @@ int q38hip_repack_q4k_tiles(void *tiled, const void *q4k_rows, uint32_t rows,
                             uint64_t input_length, void *stream);
 
 /* q38hip_gemm_q8_k over a tiled Q4_K copy: output[t * rows + r] for
- * t < batch_size (2..8), input_length 5120, 6144, 10240 or 17408.  The
- * results are those of q38hip_gemm_q8_k bit for bit. */
+ * t < batch_size (at least 2; launches of 2..8 tokens), input_length 5120,
+ * 6144, 10240 or 17408.  The results are those of q38hip_gemm_q8_k bit for
+ * bit. */
 int q38hip_gemm_q8_k_tiled(float *output, const Q38Q8KBlock *input,
                            uint32_t batch_size, uint64_t input_length,
                            const void *tiled, uint32_t rows, void *stream);
+
+/* Library extension: the full-attention decode core of one layer on the
+ * device, for kernel-level use and tests.  It is the reference's static
+ * q38_full_core (src/qwen38/qwen38_model.c:816-885) for `rows` consecutive
+ * positions position .. position + rows - 1, row t seeing positions
+ * 0 .. position + t (q38_batch_full_attention, :1089-1119): per-head RMS
+ * norms of q and k (q_norm, k_norm: 256 floats), RoPE, the K/V cache write
+ * of each row, scores, softmax and the sigmoid-gated output.
+ *   q_and_gate: row t at t * in_stride floats, 24 heads x (256 q | 256 gate);
+ *   key, value: row t at t * in_stride floats, 1024 each;
+ *   key_cache, value_cache: [context_length][1024] fp32 (one layer), rows
+ *     before `position` already filled; rows position .. position + rows - 1
+ *     are written;
+ *   attention: [rows][6144] gated output; attention_q8k (optional, may be
+ *     NULL): its Q8_K blocks [rows][24], the input of the output projection.
+ * All pointers are device pointers.  position + rows <= context_length.
+ * Allocates and frees its working buffers (the RoPE table of the context,
+ * the scores) and synchronises `stream` before returning. */
+int q38hip_attention_rows(float *attention, Q38Q8KBlock *attention_q8k, const float *q_and_gate,
+                          const float *key, const float *value, uint64_t in_stride,
+                          const float *q_norm, const float *k_norm, float *key_cache,
+                          float *value_cache, uint32_t context_length, uint32_t position,
+                          uint32_t rows, void *stream);
 
 /* Last argument error of the calling thread ("" when none). */
 const char *q38hip_last_error(void);

@@ -160,6 +160,8 @@ class Reference:
         lib.q38_tensor_gemm_q8_k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
                                              ctypes.c_uint64, ctypes.POINTER(GGUFTensor)]
         lib.q38_tensor_row_f32.argtypes = [ctypes.c_void_p, ctypes.POINTER(GGUFTensor), ctypes.c_uint64]
+        lib.q38ref_full_core.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_uint32, ctypes.c_void_p,
+                                                                  ctypes.c_void_p, ctypes.c_uint32]
         self.lib = lib
 
     @staticmethod
@@ -197,6 +199,22 @@ class Reference:
         out = np.zeros(width, dtype=np.float32)
         if not self.lib.q38_tensor_row_f32(_ptr(out), ctypes.byref(tensor), row):
             raise ValueError("row decode failed")
+        return out
+
+
+    def full_core(self, q_and_gate, key, value, key_cache, value_cache, q_norm, k_norm, position):
+        """The reference's static q38_full_core (qwen38_model.c:816-885)
+        through oracle/ref_attention_shim.c: the gated attention output
+        [6144] of one row; key_cache / value_cache ([context, 1024] fp32)
+        are updated in place."""
+        out = np.zeros(6144, dtype=np.float32)
+        args = [np.ascontiguousarray(a, dtype=np.float32).copy() for a in (q_and_gate, key, value, q_norm, k_norm)]
+        assert key_cache.dtype == np.float32 and value_cache.dtype == np.float32
+        assert key_cache.flags.c_contiguous and value_cache.flags.c_contiguous
+        if not self.lib.q38ref_full_core(_ptr(out), _ptr(args[0]), _ptr(args[1]), _ptr(args[2]), _ptr(key_cache),
+                                         _ptr(value_cache), key_cache.shape[0], _ptr(args[3]), _ptr(args[4]),
+                                         position):
+            raise ValueError("q38ref_full_core refused its arguments")
         return out
 
 

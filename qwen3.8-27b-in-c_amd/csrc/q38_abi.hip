@@ -79,10 +79,18 @@ int check_gemm(const void *output, const void *input, uint32_t batch, uint64_t i
     if (input_length % Q38_Q8_K_BLOCK_SIZE) return fail("input length is not a multiple of 256");
     if (!supported_type(tensor->type)) return fail("tensor type is not Q4_K, Q6_K or IQ1_M");
     if (!tensor->data) return fail("tensor has no data");
-    if (batch > 8) return fail("batch_size above 8");
     if (tensor->shape[1] == 0 || tensor->shape[1] > 0xffffffffull) return fail("bad row count");
     if (input_length / 256 > 0xffffffffull) return fail("input too long");
     return 1;
+}
+
+/* tokens of the next launch when `left` tokens remain: at most 8, and never
+ * leaving fewer than `min_tokens` for the launch after it */
+uint32_t token_chunk(uint32_t left, uint32_t min_tokens)
+{
+    uint32_t n = left < 8 ? left : 8;
+    if (left > n && left - n < min_tokens) n = left - min_tokens;
+    return n;
 }
 
 struct DeviceBuffer {
@@ -102,6 +110,9 @@ struct DeviceBuffer {
 }  // namespace
 
 namespace q38 {
+/* record an argument error for q38hip_last_error(); returns 0 */
+int abi_fail(const char *message) { return fail(message); }
+
 /* device IQ1_M codebook of the current device (uploaded on first use) */
 const void *iq1m_grid_for_current_device()
 {
@@ -164,11 +175,20 @@ int q38hip_gemm_q8_k(float *output, const Q38Q8KBlock *input, uint32_t batch_siz
     if (!check_gemm(output, input, batch_size, input_length, tensor)) return 0;
     DeviceState *state = device_state();
     if (!state) return fail("device initialisation failed");
-    const bool ok = q38::launch_gemm((int)tensor->type, (int)batch_size, tensor->data,
-                                     reinterpret_cast<const uint8_t *>(input), output,
-                                     (uint32_t)tensor->shape[1], (uint32_t)(input_length / 256),
-                                     state->grid, static_cast<hipStream_t>(stream));
-    return ok ? 1 : fail("unsupported GEMM configuration");
+    /* Any batch size, as the reference (qwen38_quant.c:2950-2956): the
+     * kernels take up to 8 tokens per launch and every token's row results
+     * are independent of the others in the batch, so consecutive launches
+     * over token chunks give the same bits as one. */
+    const uint32_t rows = (uint32_t)tensor->shape[1], nb = (uint32_t)(input_length / 256);
+    for (uint32_t t0 = 0; t0 < batch_size;) {
+        const uint32_t n = token_chunk(batch_size - t0, 1);
+        if (!q38::launch_gemm((int)tensor->type, (int)n, tensor->data,
+                              reinterpret_cast<const uint8_t *>(input) + (size_t)t0 * nb * sizeof(Q38Q8KBlock),
+                              output + (size_t)t0 * rows, rows, nb, state->grid, static_cast<hipStream_t>(stream)))
+            return fail("unsupported GEMM configuration");
+        t0 += n;
+    }
+    return 1;
 }
 
 uint64_t q38hip_tiled_q4k_bytes(uint32_t rows, uint64_t input_length)
@@ -193,13 +213,19 @@ int q38hip_gemm_q8_k_tiled(float *output, const Q38Q8KBlock *input, uint32_t bat
                            const void *tiled, uint32_t rows, void *stream)
 {
     if (!output || !input || !tiled || !rows) return fail("null argument");
-    if (batch_size < 2 || batch_size > 8) return fail("batch_size must be 2..8");
+    if (batch_size < 2) return fail("batch_size must be at least 2");
     if (!device_state()) return fail("device initialisation failed");
-    if (input_length % Q38_Q8_K_BLOCK_SIZE ||
-        !q38::launch_gemm_q4k_tiled((int)batch_size, static_cast<const uint8_t *>(tiled),
-                                    reinterpret_cast<const uint8_t *>(input), output, rows, rows,
-                                    (uint32_t)(input_length / 256), static_cast<hipStream_t>(stream)))
-        return fail("unsupported tiled GEMM shape (input_length 5120, 6144, 10240 or 17408)");
+    if (input_length % Q38_Q8_K_BLOCK_SIZE) return fail("input length is not a multiple of 256");
+    const uint32_t nb = (uint32_t)(input_length / 256);
+    /* launches of 2..8 tokens (see q38hip_gemm_q8_k) */
+    for (uint32_t t0 = 0; t0 < batch_size;) {
+        const uint32_t n = token_chunk(batch_size - t0, 2);
+        if (!q38::launch_gemm_q4k_tiled((int)n, static_cast<const uint8_t *>(tiled),
+                                        reinterpret_cast<const uint8_t *>(input) + (size_t)t0 * nb * sizeof(Q38Q8KBlock),
+                                        output + (size_t)t0 * rows, rows, rows, nb, static_cast<hipStream_t>(stream)))
+            return fail("unsupported tiled GEMM shape (input_length 5120, 6144, 10240 or 17408)");
+        t0 += n;
+    }
     return 1;
 }
 

@@ -668,19 +668,8 @@ bool allocate_state(Q38Model *m)
     m->drafts = m->words;
     m->targets = m->words + 16;
     m->accept = m->words + 32;
-    /* RoPE table: theta starts at the position and is multiplied by
-     * powf(1e7, -2/64) per pair; cosf/sinf of the host C library, exactly the
-     * values q38_rope computes (qwen38_model.c:697-713). */
     std::vector<float> table((size_t)ctx * 64);
-    const float theta_scale = powf(10000000.0f, -2.0f / 64.0f);
-    for (uint32_t pos = 0; pos < ctx; ++pos) {
-        float theta = (float)pos;
-        for (int pair = 0; pair < 32; ++pair) {
-            table[(size_t)pos * 64 + pair] = cosf(theta);
-            table[(size_t)pos * 64 + 32 + pair] = sinf(theta);
-            theta *= theta_scale;
-        }
-    }
+    q38::rope_table_host(table.data(), ctx);
     m->query_scale = 1.0f / sqrtf(128.0f);
     return hip_ok(hipMemcpy(m->rope, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice),
                   "rope table upload");

@@ -33,6 +33,9 @@ bool launch_gemm_q4k_t32(int m, const uint8_t *w_tiled, const uint8_t *x, float 
 bool launch_gemm_ld(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                     uint32_t nblk, const void *grid, hipStream_t stream);
 
+/* q38_abi.hip: record an argument error for q38hip_last_error(); returns 0 */
+int abi_fail(const char *message);
+
 /* q38_misc.hip */
 void launch_quantize(const float *x, uint8_t *out, uint32_t nblocks, hipStream_t stream);
 uint32_t argmax_chunks(uint32_t count);
@@ -73,6 +76,8 @@ void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, long
 /* full attention over `rows` rows at positions *position + t: prep (norms,
  * RoPE, K/V write), scores, softmax + V + gate + Q8_K of the output */
 bool configure_attention(int context);
+/* host: the RoPE cos/sin table of positions [0, context), 64 floats each */
+void rope_table_host(float *table, uint32_t context);
 void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_and_gate, const float *key,
                       const float *value, long long in_stride, const float *q_norm, const float *k_norm,
                       const float *rope, float *key_cache, float *value_cache, float *scores, int context,

@@ -9,6 +9,10 @@
  * expf/logf of q38_libm.h, and the double-precision squared sums of the norms
  * reproduce the reference's sequential loop (block_sum_finish, q38_norm.h).
  */
+#include <cmath>
+#include <mutex>
+#include <vector>
+
 #include "q38_device.h"
 #include "q38_kernels.h"
 #include "q38_libm.h"
@@ -658,11 +662,42 @@ void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, long
     deltanet_out_quant_kernel<<<dim3(kVHeads / 2, rows), 256, 0, stream>>>(attn, q_out, z, z_stride, ssm_norm);
 }
 
+/* The dynamic-LDS limit of the in-LDS output kernel is a per-device
+ * attribute of the function: it only ever grows, to the largest context
+ * configured so far on the device, so a later model or call with a smaller
+ * context never lowers it under an earlier one. */
 bool configure_attention(int context)
 {
+    static std::mutex mutex;
+    static std::vector<int> configured;
     if (context > kMaxLdsPositions) return true;
-    return hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_output_kernel<true>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, context * 4) == hipSuccess;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return false;
+    std::lock_guard<std::mutex> lock(mutex);
+    if ((int)configured.size() <= device) configured.resize(device + 1, 0);
+    if (context <= configured[device]) return true;
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_output_kernel<true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, context * 4) != hipSuccess)
+        return false;
+    configured[device] = context;
+    return true;
+}
+
+/* RoPE table of positions [0, context): cos then sin of the 32 pair angles.
+ * theta starts at the position and is multiplied by powf(1e7, -2/64) per
+ * pair; cosf/sinf of the host C library, exactly the values q38_rope
+ * computes (qwen38_model.c:697-713). */
+void rope_table_host(float *table, uint32_t context)
+{
+    const float theta_scale = powf(10000000.0f, -2.0f / 64.0f);
+    for (uint32_t pos = 0; pos < context; ++pos) {
+        float theta = (float)pos;
+        for (int pair = 0; pair < 32; ++pair) {
+            table[(size_t)pos * 64 + pair] = cosf(theta);
+            table[(size_t)pos * 64 + 32 + pair] = sinf(theta);
+            theta *= theta_scale;
+        }
+    }
 }
 
 void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_and_gate, const float *key,

@@ -49,7 +49,7 @@ def make_tensor(data_ptr, qtype, width, rows, nbytes=0):
 # Every symbol the C header declares (tests check the library exports them).
 EXPORTS = ("q38_f16_to_f32", "q38_quantize_q8_k", "q38_tensor_gemv_q8_k", "q38_tensor_gemm_q8_k",
            "q38hip_quantize_q8_k", "q38hip_gemm_q8_k", "q38hip_argmax", "q38hip_accept",
-           "q38hip_tiled_q4k_bytes", "q38hip_repack_q4k_tiles", "q38hip_gemm_q8_k_tiled",
+           "q38hip_tiled_q4k_bytes", "q38hip_repack_q4k_tiles", "q38hip_gemm_q8_k_tiled", "q38hip_attention_rows",
            "q38hip_last_error", "q38hip_synchronize",
            "q38_model_open_gguf", "q38_model_attach_mtp_gguf", "q38_model_close", "q38_model_reset",
            "q38_model_forward_token", "q38_model_prefill", "q38_model_enable_mtp", "q38_model_mtp_forward",
@@ -76,6 +76,7 @@ def load_library(path=LIB_PATH):
     lib.q38hip_gemm_q8_k_tiled.argtypes = [vp, vp, u32, u64, vp, u32, vp]
     lib.q38hip_argmax.argtypes = [vp, vp, u32, u32, vp]
     lib.q38hip_accept.argtypes = [vp, vp, vp, u32, vp]
+    lib.q38hip_attention_rows.argtypes = [vp, vp, vp, vp, vp, u64, vp, vp, vp, vp, u32, u32, u32, vp]
     lib.q38hip_last_error.restype = ctypes.c_char_p
     lib.q38hip_last_error.argtypes = []
     lib.q38hip_synchronize.argtypes = []
@@ -181,6 +182,26 @@ def accept(targets, drafts):
     _check(lib().q38hip_accept(_dev_ptr(out), _dev_ptr(targets), _dev_ptr(drafts), rows, _stream()),
            "q38hip_accept")
     return out
+
+
+def attention_rows(rows_in, q_norm, k_norm, key_cache, value_cache, position):
+    """Full-attention core over the rows of rows_in (float32 [rows, 14336] on
+    the GPU: 24 heads x (256 q | 256 gate), then key [1024], then value
+    [1024]) at positions position + t; key_cache / value_cache: float32
+    [context, 1024] on the GPU, updated in place.  Returns (attention
+    float32 [rows, 6144], its Q8_K blocks uint8 [rows * 24 * 292])."""
+    import torch
+    rows, stride = rows_in.shape
+    context = key_cache.shape[0]
+    out = torch.empty((rows, 6144), dtype=torch.float32, device=rows_in.device)
+    q8k = torch.empty(rows * 24 * Q8K_BYTES, dtype=torch.uint8, device=rows_in.device)
+    base = rows_in.data_ptr()
+    _check(lib().q38hip_attention_rows(_dev_ptr(out), _dev_ptr(q8k), _dev_ptr(rows_in),
+                                       ctypes.c_void_p(base + 12288 * 4), ctypes.c_void_p(base + 13312 * 4), stride,
+                                       _dev_ptr(q_norm), _dev_ptr(k_norm), _dev_ptr(key_cache),
+                                       _dev_ptr(value_cache), context, position, rows, _stream()),
+           "q38hip_attention_rows")
+    return out, q8k
 
 
 # ---- host-pointer drop-ins (numpy arrays) ------------------------------------

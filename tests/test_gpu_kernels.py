@@ -79,7 +79,8 @@ def test_gemm_rows_bit_exact(hip, oracle, device, qtype, rows, width):
         assert np.array_equal(bits(got), bits(want)), "M=%d" % m
 
 
-@pytest.mark.parametrize("name", sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz") and not f.startswith("model_")))
+@pytest.mark.parametrize("name", sorted(f for f in os.listdir(GOLDEN)
+                                          if f.endswith(".npz") and f.split("_")[0] in ("q4k", "q6k", "iq1m")))
 def test_gpu_matches_reference_golden(hip, device, name):
     g = np.load(os.path.join(GOLDEN, name))
     qtype, rows, width, tokens = (int(v) for v in g["meta"])
@@ -198,3 +199,39 @@ def test_tiled_gemm_full_shape_matches_row_major(hip, device, m):
         want = hip.gemm_q8_k(wd, Q4_K, width, rows, xq, m).cpu().numpy()
         got = hip.gemm_q8_k_tiled(hip.repack_q4k_tiles(wd, width, rows), width, rows, xq, m).cpu().numpy()
         assert np.array_equal(bits(got), bits(want)), (rows, width)
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, IQ1_M, Q6_K])
+def test_gemm_any_batch_size(hip, oracle, device, qtype):
+    """q38hip_gemm_q8_k and the host drop-in q38_tensor_gemm_q8_k take any
+    batch size, as the reference's GEMM (qwen38_quant.c:2950-2956): 9, 12,
+    13 and 17 tokens run as launches of up to 8 and equal the oracle's
+    per-token GEMVs bit for bit."""
+    rows, width = 520, 5120
+    w = synth.matrix(qtype, rows, width, seed=qtype + 40)
+    x = synth.activations(width, seed=qtype + 41, count=17)
+    q = oracle.quantize(x.reshape(-1))
+    nb = width // 256
+    wd = to_dev(w, device)
+    xq = hip.quantize_q8_k(to_dev(x, device))
+    for m in (9, 12, 13, 17):
+        want = oracle.gemm(qtype, w, rows, q[:m * nb], m)
+        got = hip.gemm_q8_k(wd, qtype, width, rows, xq[:m * nb * 292], m).cpu().numpy()
+        assert np.array_equal(bits(got), bits(want)), "M=%d" % m
+    host = hip.host_tensor_gemm_q8_k(qtype, w, rows, q[:12 * nb], 12)
+    assert np.array_equal(bits(host), bits(oracle.gemm(qtype, w, rows, q[:12 * nb], 12)))
+
+
+def test_tiled_gemm_any_batch_size(hip, oracle, device):
+    """The tiled entry point splits 9, 10 and 17 tokens into launches of 2..8."""
+    rows, width = 4112, 5120
+    w = synth.matrix(Q4_K, rows, width, seed=77)
+    x = synth.activations(width, seed=78, count=17)
+    q = oracle.quantize(x.reshape(-1))
+    nb = width // 256
+    tiled = hip.repack_q4k_tiles(to_dev(w, device), width, rows)
+    xq = hip.quantize_q8_k(to_dev(x, device))
+    for m in (9, 10, 17):
+        want = oracle.gemm(Q4_K, w, rows, q[:m * nb], m)
+        got = hip.gemm_q8_k_tiled(tiled, width, rows, xq[:m * nb * 292], m).cpu().numpy()
+        assert np.array_equal(bits(got), bits(want)), "M=%d" % m

@@ -248,7 +248,10 @@ def test_iq1m_grid_table_invariants(oracle):
 def _golden_files():
     if not os.path.isdir(GOLDEN):
         return []
-    return sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz") and not f.startswith("model_"))
+    # kernel fixtures of tests/golden/make_golden.py (the model, decode and
+    # attention fixtures have scripts and tests of their own)
+    return sorted(f for f in os.listdir(GOLDEN)
+                  if f.endswith(".npz") and f.split("_")[0] in ("q4k", "q6k", "iq1m"))
 
 
 @pytest.mark.parametrize("name", _golden_files())
@@ -283,3 +286,55 @@ def test_row_dequant_matches_compiled_reference(oracle, reference):
         a = oracle.row_f32(Q4_K, w, 1024, row)
         b = reference.row_f32(Q4_K, w, 1024, row, 4)
         assert a.view(np.uint32).tobytes() == b.view(np.uint32).tobytes()
+
+
+# ---- attention core (orc_attention_decode) -----------------------------------
+
+def _oracle_core(oracle):
+    def core(q_and_gate, key, value, key_cache, value_cache, q_norm, k_norm, position):
+        return oracle.attention_decode(q_and_gate, key, value, key_cache, value_cache, q_norm, k_norm, position)
+    return core
+
+
+def test_attention_oracle_position_zero_closed_form(oracle):
+    """At position 0 the softmax has one term: e = 1, probability 1, so each
+    output is fmaf(1, v, 0) * sigmoid(gate) = v * sigmoid(gate) exactly
+    (qwen38_model.c:863-882), whatever q and k are."""
+    import attention_cases as ac
+    rows_in, qn, kn, kc, vc = ac.inputs(4, 0, 1)
+    att = ac.run_rows(_oracle_core(oracle), rows_in, qn, kn, kc, vc, 0)[0]
+    gate = rows_in[0, :ac.KEY].reshape(24, 512)[:, 256:]
+    value = rows_in[0, ac.VALUE:].reshape(4, 256)
+    sig = (np.float32(1.0) / (np.float32(1.0) + np.exp(-gate.astype(np.float64)).astype(np.float32)))
+    want = (value[np.arange(24) // 6] * sig).reshape(-1)
+    # numpy's exp is not the C library's expf: compare to 1 ulp of the sigmoid
+    assert np.allclose(att, want, rtol=2e-7, atol=0)
+    assert np.array_equal(vc[0], value.reshape(-1))
+
+
+def test_attention_oracle_matches_golden(oracle):
+    """The oracle equals the reference's own q38_full_core (compiled from its
+    source, tests/golden/make_attention_golden.py) at positions 0, 1, 31,
+    32, 33, 2047 and 4100, output and written K row bit for bit."""
+    import attention_cases as ac
+    g = np.load(os.path.join(GOLDEN, "attention_ref.npz"))
+    for i, position in enumerate(g["positions"]):
+        position = int(position)
+        rows_in, qn, kn, kc, vc = ac.inputs(position + 1, position, 1)
+        att = ac.run_rows(_oracle_core(oracle), rows_in, qn, kn, kc, vc, position)[0]
+        assert np.array_equal(att[:64].view(np.uint32), g["first64"][i].view(np.uint32)), position
+        assert ac.digest(att) == g["digests"][i], position
+        assert ac.digest(kc[position]) == g["key_digests"][i], position
+
+
+def test_attention_oracle_matches_compiled_reference_rows(oracle, reference):
+    """Several consecutive rows (positions 28..35, across the 32-position
+    batch boundary), outputs and both caches, against the compiled reference."""
+    import attention_cases as ac
+    rows_in, qn, kn, kc, vc = ac.inputs(48, 28, 8)
+    kc2, vc2 = kc.copy(), vc.copy()
+    got = ac.run_rows(_oracle_core(oracle), rows_in, qn, kn, kc, vc, 28)
+    want = ac.run_rows(reference.full_core, rows_in, qn, kn, kc2, vc2, 28)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(kc.view(np.uint32), kc2.view(np.uint32))
+    assert np.array_equal(vc.view(np.uint32), vc2.view(np.uint32))
