@@ -97,6 +97,17 @@ int q38hip_gemm_q8_k(float *output, const Q38Q8KBlock *input,
 int q38hip_argmax(uint32_t *index_out, const float *values, uint32_t count,
                   uint32_t rows, void *stream);
 
+/* No counterpart in the reference: q38hip_argmax for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops or
+ * harnesses that forbid hipMalloc).  It allocates nothing: the partial
+ * maxima go to a fixed 64 KiB array in the library's device memory instead
+ * of the growable scratch, so ceil(count / 4096) * rows must be at most 8192
+ * (248320-wide rows: up to 134 rows); larger calls return 0 with a message.
+ * Every call on one device shares that array, so calls that overlap on one
+ * device (on any streams) race.  Results are those of q38hip_argmax. */
+int q38hip_argmax_noalloc(uint32_t *index_out, const float *values, uint32_t count,
+                          uint32_t rows, void *stream);
+
 /* Greedy acceptance of a verify batch (src/qwen38/qwen38_model.c:1662-1702):
  * targets[rows] are the per-row argmaxes, drafts[rows] the draft ids.
  * result[0] = consumed, result[1] = matched, result[2] = next,

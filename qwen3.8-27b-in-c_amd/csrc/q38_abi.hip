@@ -12,6 +12,14 @@
 #include "q38_iq1m_grid.inc"
 #include "q38_kernels.h"
 
+/* Fixed partials buffer of q38hip_argmax_noalloc: kNoAllocPairs partial
+ * maxima (fp32 values, then uint32 indices), 64 KiB on every device the
+ * library runs on, held until the process ends.  Host code never uses the
+ * array's name as an address: it uses the per-device address that
+ * hipGetSymbolAddress returns (g_scratch_ptr below). */
+constexpr size_t kNoAllocPairs = 8192;
+static __device__ __align__(256) uint32_t scratch[2 * kNoAllocPairs];
+
 namespace {
 
 thread_local std::string g_error;
@@ -34,6 +42,24 @@ struct DeviceState {
 
 std::mutex g_mutex;
 std::vector<DeviceState> g_devices;
+
+std::vector<uint32_t *> g_scratch_ptr;
+
+/* device address of `scratch` on the current device, looked up once per
+ * device (nullptr on failure) */
+uint32_t *noalloc_scratch()
+{
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if ((int)g_scratch_ptr.size() <= device) g_scratch_ptr.resize(device + 1, nullptr);
+    if (!g_scratch_ptr[device]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        g_scratch_ptr[device] = static_cast<uint32_t *>(ptr);
+    }
+    return g_scratch_ptr[device];
+}
 
 DeviceState *device_state()
 {
@@ -254,6 +280,20 @@ int q38hip_argmax(uint32_t *index_out, const float *values, uint32_t count, uint
         }
     }
     q38::launch_argmax(values, count, rows, state->argmax_values, state->argmax_index, index_out,
+                       static_cast<hipStream_t>(stream));
+    return 1;
+}
+
+int q38hip_argmax_noalloc(uint32_t *index_out, const float *values, uint32_t count, uint32_t rows, void *stream)
+{
+    if (!index_out || !values || !count || !rows) return fail("bad argmax arguments");
+    const size_t need = (size_t)q38::argmax_chunks(count) * rows;
+    if (need > kNoAllocPairs)
+        return fail("argmax too large for the fixed scratch: ceil(count / 4096) * rows must be at most 8192");
+    uint32_t *base = noalloc_scratch();
+    if (!base) return fail("scratch address lookup failed");
+    /* pass 1 writes every partial that pass 2 reads: nothing to clear */
+    q38::launch_argmax(values, count, rows, reinterpret_cast<float *>(base), base + kNoAllocPairs, index_out,
                        static_cast<hipStream_t>(stream));
     return 1;
 }

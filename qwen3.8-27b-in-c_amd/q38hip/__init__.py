@@ -48,7 +48,7 @@ def make_tensor(data_ptr, qtype, width, rows, nbytes=0):
 
 # Every symbol the C header declares (tests check the library exports them).
 EXPORTS = ("q38_f16_to_f32", "q38_quantize_q8_k", "q38_tensor_gemv_q8_k", "q38_tensor_gemm_q8_k",
-           "q38hip_quantize_q8_k", "q38hip_gemm_q8_k", "q38hip_argmax", "q38hip_accept",
+           "q38hip_quantize_q8_k", "q38hip_gemm_q8_k", "q38hip_argmax", "q38hip_argmax_noalloc", "q38hip_accept",
            "q38hip_tiled_q4k_bytes", "q38hip_repack_q4k_tiles", "q38hip_gemm_q8_k_tiled", "q38hip_attention_rows",
            "q38hip_last_error", "q38hip_synchronize",
            "q38_model_open_gguf", "q38_model_attach_mtp_gguf", "q38_model_close", "q38_model_reset",
@@ -75,6 +75,7 @@ def load_library(path=LIB_PATH):
     lib.q38hip_repack_q4k_tiles.argtypes = [vp, vp, u32, u64, vp]
     lib.q38hip_gemm_q8_k_tiled.argtypes = [vp, vp, u32, u64, vp, u32, vp]
     lib.q38hip_argmax.argtypes = [vp, vp, u32, u32, vp]
+    lib.q38hip_argmax_noalloc.argtypes = [vp, vp, u32, u32, vp]
     lib.q38hip_accept.argtypes = [vp, vp, vp, u32, vp]
     lib.q38hip_attention_rows.argtypes = [vp, vp, vp, vp, vp, u64, vp, vp, vp, vp, u32, u32, u32, vp]
     lib.q38hip_last_error.restype = ctypes.c_char_p
@@ -171,6 +172,18 @@ def argmax(values):
     out = torch.empty(values2.shape[0], dtype=torch.int32, device=values.device)
     _check(lib().q38hip_argmax(_dev_ptr(out), _dev_ptr(values2), values2.shape[1], values2.shape[0],
                                _stream()), "q38hip_argmax")
+    return out
+
+
+def argmax_noalloc(values, out=None):
+    """q38hip_argmax_noalloc: as argmax(), with the partial maxima in the
+    library's fixed device array (no allocation by the library)."""
+    import torch
+    values2 = values if values.dim() == 2 else values.reshape(1, -1)
+    if out is None:
+        out = torch.empty(values2.shape[0], dtype=torch.int32, device=values.device)
+    _check(lib().q38hip_argmax_noalloc(_dev_ptr(out), _dev_ptr(values2), values2.shape[1], values2.shape[0],
+                                       _stream()), "q38hip_argmax_noalloc")
     return out
 
 
