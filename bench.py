@@ -83,14 +83,17 @@ def parse():
     p.add_argument("--steps", type=int, default=None)
     p.add_argument("--warmup", type=int, default=None)
     p.add_argument("--workload", default="decode", choices=["decode"] + sorted(WORKLOADS) + ["copy"])
-    p.add_argument("--decode-tokens", type=int, default=256)
+    p.add_argument("--decode-tokens", type=int, default=None,
+                   help="tokens decoded on every run (256 for q4km, 1024 for iq1m); --steps picks the timed window")
     p.add_argument("--layout", default="q4km", choices=["q4km", "iq1m"],
                    help="decode workload: Q4_K_M layout (default) or IQ1_M layer matrices")
     p.add_argument("--prompt", type=int, default=None, help="prompt tokens (512 for q4km, 4096 for iq1m)")
     p.add_argument("--draft", type=int, default=3)
     p.add_argument("--plain-tokens", type=int, default=32, help="plain greedy tokens after the timed region")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time per thread count")
+    p.add_argument("--cpu-worker", action="store_true", help=argparse.SUPPRESS)
+    p.add_argument("--cpu-threads", default="", help=argparse.SUPPRESS)
     p.add_argument("--trace-summary", metavar="DIR", help="summarise a rocprofv3 kernel trace and exit")
     p.add_argument("--trace-transactions", type=int, default=0,
                    help="with --trace-summary of a decode run: its transaction count (warmup + steps)")
@@ -296,49 +299,123 @@ def prompt_ids(count, seed=11):
     return np.random.Generator(np.random.PCG64(seed)).integers(0, 248320, count).astype(np.uint32)
 
 
-def cpu_decode_baseline(path, draft, budget_s, label="Q4_K_M"):
-    """The reference engine (oracle/_ref, its own C sources, AVX2 build) on the
-    host cores: a 4-token prompt, then speculative_greedy(draft) transactions
-    for about `budget_s` seconds; decoded tokens per second."""
+def host_cpu_info():
+    """lscpu model name, physical cores (cores per socket x sockets), logical
+    CPUs, and the C library version of this host."""
+    import platform
+    import subprocess
+    info = {"model": platform.processor() or None, "physical_cores": None, "logical_cpus": os.cpu_count(),
+            "glibc": "-".join(platform.libc_ver())}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, check=True).stdout
+        fields = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
+        fields = {k.strip(): v.strip() for k, v in fields.items()}
+        info["model"] = fields.get("Model name", info["model"])
+        info["physical_cores"] = int(fields["Core(s) per socket"]) * int(fields.get("Socket(s)", "1"))
+    except (OSError, subprocess.CalledProcessError, KeyError, ValueError):
+        pass
+    # the CPU share this process may use (a container or job limit)
+    try:
+        info["usable_cpus"] = len(os.sched_getaffinity(0))
+    except AttributeError:
+        info["usable_cpus"] = os.cpu_count()
+    return info
+
+
+def cpu_decode_worker(args):
+    """Child process of the CPU baseline (no GPU use): the reference engine
+    (oracle/_ref, its own C sources, AVX2 + OpenMP build) prefills the same
+    prompt as the GPU run, then runs speculative_greedy(draft) transactions
+    for about `--cpu-seconds` at each thread count of --cpu-threads (OpenMP
+    threads bound to cores).  Prints one JSON line."""
+    import ctypes
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    from oracle import Reference, reference_model
+    from oracle import reference_model
+    from q38hip import synth
+    path = synth.model_path(1, args.layout)
+    threads = [int(t) for t in args.cpu_threads.split(",")]
+    gomp = ctypes.CDLL("libgomp.so.1")
+    gomp.omp_set_num_threads(threads[0])
+    model = reference_model().open(path, args.prompt + 64 * args.draft + 16)
+    model.enable_mtp()
+    t0 = time.perf_counter()
+    logits = model.prefill(prompt_ids(args.prompt))
+    prefill_s = time.perf_counter() - t0
+    token = int(np.argmax(logits))
+    runs = []
+    for n in threads:
+        gomp.omp_set_num_threads(n)
+        produced = transactions = 0
+        start = time.perf_counter()
+        while time.perf_counter() - start < args.cpu_seconds:
+            accepted, _ = model.speculative_greedy(token, 0xFFFFFFFF, args.draft)
+            produced += len(accepted)
+            token = int(accepted[-1])
+            transactions += 1
+        elapsed = time.perf_counter() - start
+        runs.append({"threads": n, "tokens": produced, "transactions": transactions, "seconds": round(elapsed, 2),
+                     "tokens_per_s": round(produced / elapsed, 4)})
+    model.close()
+    print(json.dumps({"prefill_s": round(prefill_s, 2), "runs": runs}))
+
+
+def cpu_decode_baseline(args, label="Q4_K_M"):
+    """The reference engine on the host cores, run in a child process (it
+    never touches the GPU) on the same GGUF and prompt as the GPU run: one
+    sample on all physical cores (OMP_PROC_BIND=close, OMP_PLACES=cores), one
+    at 12 threads, the reference CLI's default (src/cli/qwen38_main.c:
+    1431-1432)."""
+    import subprocess
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Reference
     if not Reference.available():
         return None
-    model = reference_model().open(path, 1024)
-    model.enable_mtp()
-    logits = model.prefill(prompt_ids(4))
-    token = int(np.argmax(logits))
-    produced = 0
-    transactions = 0
-    start = time.perf_counter()
-    while time.perf_counter() - start < budget_s:
-        accepted, _ = model.speculative_greedy(token, 0xFFFFFFFF, draft)
-        produced += len(accepted)
-        token = int(accepted[-1])
-        transactions += 1
-    elapsed = time.perf_counter() - start
-    model.close()
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(produced / elapsed, 4), "unit": "tokens/s", "cores": threads, "kind": "reference",
-            "sample": "reference engine q38_model_speculative_greedy(k=%d) on the same synthetic 27B %s "
-                      "GGUF: 4-token prompt, %d transactions, %d tokens in %.1f s, OpenMP threads=%d"
-                      % (draft, label, transactions, produced, elapsed, threads)}
+    info = host_cpu_info()
+    cores = min(info["physical_cores"] or info["usable_cpus"], info["usable_cpus"])
+    threads = [cores] + ([12] if cores != 12 else [])
+    env = dict(os.environ, OMP_NUM_THREADS=str(cores), OMP_PROC_BIND="close", OMP_PLACES="cores")
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-worker", "--layout", args.layout,
+           "--prompt", str(args.prompt), "--draft", str(args.draft), "--cpu-seconds", str(args.cpu_seconds),
+           "--cpu-threads", ",".join(str(t) for t in threads)]
+    out = subprocess.run(cmd, env=env, capture_output=True, text=True)
+    if out.returncode != 0:
+        return {"value": None, "error": out.stderr[-400:]}
+    res = json.loads(out.stdout.strip().splitlines()[-1])
+    main = res["runs"][0]
+    return {"value": main["tokens_per_s"], "unit": "tokens/s", "cores": main["threads"], "kind": "reference",
+            "sample": "reference engine (AVX2 + OpenMP build of its own sources) on the same synthetic 27B %s "
+                      "GGUF and %d-token prompt (prefill %.1f s), then q38_model_speculative_greedy(k=%d) "
+                      "transactions for %.0f s per thread count" % (label, args.prompt, res["prefill_s"], args.draft,
+                                                                      args.cpu_seconds),
+            "runs": res["runs"], "prefill_s": res["prefill_s"], "host": info}
 
 
 LAYOUTS = {
-    # layout: (matrix types, dominant kernel workload, default prompt, default transactions)
-    "q4km": ("Q4_K_M", "q4k_tiled_m3", 512, 248),
-    "iq1m": ("IQ1_M", "iq1m_gemm_m3", 4096, 1016),
+    # layout: (matrix types, dominant kernel workload, default prompt, default decoded tokens)
+    "q4km": ("Q4_K_M", "q4k_tiled_m3", 512, 256),
+    "iq1m": ("IQ1_M", "iq1m_gemm_m3", 4096, 1024),
 }
+# single-row GEMV rooflines reported beside the decode line (17408 x 5120)
+GEMV_ROOFLINES = ("q4k_gemv", "iq1m_gemv")
+
+
+def decode_fixture(layout):
+    """Token ids the reference engine produced for this workload
+    (tests/golden/decode_<layout>_s1.npz), or None."""
+    path = os.path.join(ROOT, "tests", "golden", "decode_%s_s1.npz" % layout)
+    if not os.path.exists(path):
+        return None
+    g = np.load(path)
+    return [int(t) for t in g["spec_tokens"]] if int(g["prompt_len"][0]) else None
 
 
 def run_decode(torch, args):
     from q38hip import synth
     from q38hip.model import Model
-    label, roof_workload, default_prompt, default_steps = LAYOUTS[args.layout]
+    label, roof_workload, default_prompt, default_tokens = LAYOUTS[args.layout]
     if args.prompt is None:
         args.prompt = default_prompt
-    steps = args.steps if args.steps is not None else default_steps
+    decode_tokens = args.decode_tokens if args.decode_tokens is not None else default_tokens
     warmup = args.warmup if args.warmup is not None else 8
     path = synth.model_path(1, args.layout)
     if path is None:
@@ -346,7 +423,10 @@ def run_decode(torch, args):
     t0 = time.perf_counter()
     synth.write_model_gguf(path, 1, args.layout)
     t_synth = time.perf_counter() - t0
-    context = args.prompt + args.draft * (warmup + steps) + 16
+    # every run decodes `decode_tokens` tokens; the timed window is transactions
+    # [warmup, warmup + steps) (default: all after the warm-up)
+    window = args.steps
+    context = args.prompt + max(decode_tokens, (warmup + (window or 0)) * args.draft) + 4 * args.draft + 16
     t0 = time.perf_counter()
     model = Model.open(path, context)
     t_open = time.perf_counter() - t0
@@ -356,23 +436,36 @@ def run_decode(torch, args):
     t0 = time.perf_counter()
     logits = model.prefill(prompt)
     t_prefill = time.perf_counter() - t0
-    token = int(np.argmax(logits))
-    for _ in range(warmup):
-        accepted, _ = model.speculative_greedy(token, 0xFFFFFFFF, args.draft, logits=False)
-        token = int(accepted[-1])
-    produced = 0
+    sequence = [int(np.argmax(logits))]
     counts = []
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        accepted, _ = model.speculative_greedy(token, 0xFFFFFFFF, args.draft, logits=False)
-        counts.append(len(accepted))
-        produced += len(accepted)
-        token = int(accepted[-1])
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    t_start = t_end = None
+    done = 0
+    while len(sequence) < decode_tokens or (window is not None and done < warmup + window):
+        if done == warmup:
+            torch.cuda.synchronize()
+            t_start = time.perf_counter()
+        accepted, _ = model.speculative_greedy(sequence[-1], 0xFFFFFFFF, args.draft, logits=False)
+        sequence.extend(int(t) for t in accepted)
+        done += 1
+        if done > warmup:
+            counts.append(len(accepted))
+        if window is not None and done == warmup + window:
+            torch.cuda.synchronize()
+            t_end = time.perf_counter()
+    if t_end is None:
+        torch.cuda.synchronize()
+        t_end = time.perf_counter()
+    if t_start is None:
+        raise SystemExit("the warm-up (%d transactions) covers the whole decode" % warmup)
+    wall = t_end - t_start
+    steps = len(counts) if window is None else window
+    produced = sum(counts[:steps])
+    want = decode_fixture(args.layout)
+    n = min(len(want), len(sequence)) if want else 0
+    parity = (sequence[:n] == want[:n]) if want else None
     # plain greedy decode on the same model (no MTP) for reference
     plain_n = args.plain_tokens
+    token = sequence[-1]
     t1 = time.perf_counter()
     for _ in range(plain_n):
         token = int(np.argmax(model.forward_token(token)))
@@ -380,6 +473,11 @@ def run_decode(torch, args):
     model.close()
 
     _, _, roofline, copies = kernel_roofline(torch, roof_workload, 200, 20)
+    gemv = {}
+    for workload in GEMV_ROOFLINES:
+        _, _, r, _ = kernel_roofline(torch, workload, 200, 20)
+        gemv[workload] = {k: r[k] for k in ("kernel", "achieved", "frac", "launch_us", "bytes_per_launch",
+                                            "traffic")}
     result = {
         "metric": "decode tokens/s (27B %s + MTP k=%d, greedy)" % (label, args.draft),
         "value": round(produced / wall, 3),
@@ -395,14 +493,17 @@ def run_decode(torch, args):
         "data": "synthetic (seeded random-init 27B %s GGUF, random prompt ids)" % label,
         "config": {"workload": "decode 27B %s + MTP k=%d" % (label, args.draft), "layers": 64, "hidden": 5120,
                    "ffn": 17408, "vocab": 248320, "prompt_tokens": args.prompt, "context": context,
-                   "decoded_tokens": produced, "transactions": steps,
+                   "decoded_tokens": len(sequence) - 1, "transactions": done,
+                   "timed_transactions": steps, "timed_tokens": produced,
                    "accepted_per_transaction": round(produced / steps, 4),
+                   "token_parity_with_reference": parity, "token_parity_checked": n,
                    "prefill_s": round(t_prefill, 3),
                    "prefill_tokens_per_s": round(args.prompt / t_prefill, 1), "open_upload_s": round(t_open, 3),
                    "synth_s": round(t_synth, 3),
                    "plain_greedy_tokens_per_s": round(plain_n / plain_wall, 3) if plain_n else None},
         "roofline": roofline,
-        "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(path, args.draft, args.cpu_seconds, label),
+        "gemv_rooflines": gemv,
+        "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(args, label),
     }
     print(json.dumps(result))
 
@@ -411,6 +512,9 @@ def main():
     args = parse()
     if args.trace_summary:
         trace_summary(args.trace_summary, args.trace_transactions)
+        return
+    if args.cpu_worker:
+        cpu_decode_worker(args)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",

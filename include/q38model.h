@@ -44,7 +44,10 @@ int q38_model_enable_mtp(Q38Model *model);
 int q38_model_mtp_forward(Q38Model *model, uint32_t token_id, const float **logits);
 
 /* qwen38_model.h:37-41: draft up to draft_count MTP tokens, verify them in
- * one batch, greedy acceptance; accepted_tokens needs draft_count entries */
+ * one batch, greedy acceptance; accepted_tokens needs draft_count entries.
+ * Any draft_count from 1 to context_length - position, as the reference:
+ * up to 8 the step runs as captured HIP graphs with one verify batch, above
+ * 8 the verify runs in 8-row chunks (the same results) */
 int q38_model_speculative_greedy(Q38Model *model, uint32_t token_id, uint32_t stop_token, uint32_t draft_count,
                                  uint32_t *accepted_tokens, uint32_t *accepted_count, const float **next_logits);
 

@@ -263,6 +263,23 @@ class ModelAPI:
     def reset(self):
         self.lib.q38_model_reset(self.handle)
 
+    def attach_mtp(self, path):
+        """q38_model_attach_mtp_gguf: the MTP block from a separate GGUF."""
+        if not self.lib.q38_model_attach_mtp_gguf(self.handle, path.encode()):
+            raise RuntimeError("q38_model_attach_mtp_gguf failed for %s" % path)
+
+    def try_speculative_greedy(self, token, stop_token, draft_count):
+        """The raw call: (return value, accepted ids, logits or None).  For
+        tests of the failure contract, where 0 is the expected answer."""
+        accepted = np.zeros(max(int(draft_count), 1), dtype=np.uint32)
+        count = ctypes.c_uint32(0)
+        p = _f32p()
+        ok = self.lib.q38_model_speculative_greedy(self.handle, int(token), int(stop_token), int(draft_count),
+                                                   accepted.ctypes.data, ctypes.byref(count), ctypes.byref(p))
+        if not ok:
+            return 0, None, None
+        return ok, accepted[:count.value].copy(), np.ctypeslib.as_array(p, shape=(248320,)).copy()
+
     def enable_mtp(self):
         if not self.lib.q38_model_enable_mtp(self.handle):
             raise RuntimeError("q38_model_enable_mtp failed")

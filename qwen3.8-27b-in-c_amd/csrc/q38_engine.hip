@@ -354,6 +354,9 @@ struct Q38Model {
     float *hidden = nullptr, *norm = nullptr, *branch = nullptr, *wide0 = nullptr;
     float *qbuf = nullptr, *attn = nullptr;
     float *scores = nullptr, *logits = nullptr, *target_norm = nullptr;
+    /* output-norm rows of a verify longer than kBatch rows (grown on demand) */
+    float *long_norm = nullptr;
+    uint32_t long_norm_rows = 0;
     uint8_t *q8k = nullptr;
     /* params[0] = position of row 0 of the current step, params[1 + r] = slot of recurrent layer r */
     uint32_t *tokens = nullptr, *params = nullptr, *targets = nullptr, *drafts = nullptr, *accept = nullptr;
@@ -622,7 +625,7 @@ void release(Q38Model *m)
     float **fbufs[] = {&m->conv_state, &m->delta_state, &m->key_cache, &m->value_cache, &m->mtp_hidden,
                        &m->ck_mtp_hidden, &m->rope, &m->hidden, &m->norm,
                        &m->branch, &m->wide0, &m->qbuf, &m->attn, &m->scores, &m->logits, &m->target_norm,
-                       &m->argmax_pv};
+                       &m->argmax_pv, &m->long_norm};
     for (float **p : fbufs) dfree(*p);
     uint32_t **ubufs[] = {&m->tokens, &m->params, &m->words, &m->argmax_pi};
     for (uint32_t **p : ubufs) dfree(*p);
@@ -1152,6 +1155,117 @@ bool restore_mtp(Q38Model *m)
                                  m->stream), "restore");
 }
 
+bool download_words(Q38Model *m, uint32_t *host, const uint32_t *device, uint32_t count)
+{
+    return hip_ok(hipMemcpyAsync(host, device, count * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream),
+                  "id download") &&
+           hip_ok(hipStreamSynchronize(m->stream), "id download");
+}
+
+/* q38_model_speculative_greedy for draft counts above kBatch
+ * (qwen38_model.c:1614-1714), in steps of at most kBatch rows:
+ *  - drafts in groups of kBatch MTP steps (the same per-step graphs as the
+ *    short path), each group's last draft feeding the next group, until
+ *    draft_count drafts or the stop token;
+ *  - the verify rows [token, d0 .. d_{n-2}] in chunks of kBatch rows, the
+ *    acceptance checked after each chunk.  A chunk runs only when every row
+ *    before it was accepted, so the state the result needs (after `consumed`
+ *    rows) is always in one of the slots the last chunk wrote, and the
+ *    checkpoint's slot may be reused once a whole chunk is accepted.  Rows
+ *    after the first rejected one are never needed (the reference replays
+ *    only the consumed rows), so they are not computed;
+ *  - the MTP catch-up over the consumed rows in chunks, each chunk's first
+ *    previous hidden state being the last output-norm row of the chunk
+ *    before it.
+ * Every row's arithmetic is that of the one-batch evaluation (rows are
+ * independent in the GEMMs, the recurrent and KV-cache cores run in token
+ * order), so results are the reference's.  Eager launches with host waits
+ * between chunks; the short path keeps one graph per step. */
+bool speculative_chunked(Q38Model *m, uint32_t token, uint32_t stop_token, uint32_t k, std::vector<uint32_t> *accepted,
+                         const float **next_row)
+{
+    std::vector<uint32_t> drafts;
+    drafts.reserve(k);
+    uint32_t input = token;
+    bool stopped = false;
+    while (drafts.size() < k && !stopped) {
+        const uint32_t g = (uint32_t)drafts.size(), n = std::min(kBatch, k - g);
+        for (uint32_t i = 0; i < n; ++i) write_params(m, kParamDraft0 + i, m->ck_mtp_position + g + i);
+        if (!upload_tokens(m, &input, 1, m->drafts) || !flush_params(m)) return false;
+        for (uint32_t i = 0; i < n; ++i) {
+            const Step s = step_of(m, kParamDraft0 + i, m->drafts + i);
+            if (!run_step(m, graph_key(kGraphDraft, i, 0), [&] {
+                    if (!mtp_step(m, s)) return false;
+                    q38::launch_argmax(m->logits, kVocab, 1, m->argmax_pv, m->argmax_pi, m->drafts + i + 1, m->stream);
+                    return true;
+                }))
+                return false;
+        }
+        uint32_t *hw = m->host_words + 64;
+        if (!download_words(m, hw, m->drafts + 1, n)) return false;
+        for (uint32_t i = 0; i < n && !stopped; ++i) {
+            drafts.push_back(hw[i]);
+            stopped = hw[i] == stop_token;
+        }
+        input = drafts.back();
+    }
+    const uint32_t n_rows = (uint32_t)drafts.size();
+    if (m->long_norm_rows < n_rows) {
+        dfree(m->long_norm);
+        m->long_norm_rows = 0;
+        if (!dalloc(&m->long_norm, (size_t)n_rows * kHidden)) return false;
+        m->long_norm_rows = n_rows;
+    }
+    std::vector<uint32_t> inputs(n_rows);
+    inputs[0] = token;
+    for (uint32_t i = 1; i < n_rows; ++i) inputs[i] = drafts[i - 1];
+    float *saved_norm = m->target_norm;
+    uint32_t matched = 0, next = 0;
+    bool ok = true, mismatch = false;
+    uint32_t last_chunk = 0;
+    for (uint32_t c0 = 0; ok && c0 < n_rows && !mismatch; c0 += kBatch) {
+        const uint32_t rows = std::min(kBatch, n_rows - c0);
+        last_chunk = c0;
+        write_params(m, kParamTarget, m->ck_position + c0);
+        m->target_norm = m->long_norm + (size_t)c0 * kHidden;
+        ok = upload_tokens(m, inputs.data() + c0, rows, m->tokens) && flush_params(m) &&
+             target_rows(m, step_of(m, kParamTarget, m->tokens), rows, rows);
+        if (ok) {
+            q38::launch_argmax(m->logits, kVocab, rows, m->argmax_pv, m->argmax_pi, m->targets, m->stream);
+            ok = download_words(m, m->host_words + 64, m->targets, rows);
+        }
+        for (uint32_t t = 0; ok && t < rows && !mismatch; ++t) {
+            const uint32_t target = m->host_words[64 + t];
+            if (target != drafts[c0 + t]) {
+                next = target;
+                mismatch = true;
+            } else {
+                ++matched;
+            }
+        }
+        /* the rows of this chunk advanced the recurrent slots */
+        if (ok) advance_slots(m, rows);
+    }
+    const uint32_t consumed = mismatch ? matched + 1 : n_rows;
+    restore_target(m, consumed);
+    ok = ok && restore_mtp(m);
+    for (uint32_t c0 = 0; ok && c0 < consumed; c0 += kBatch) {
+        const uint32_t rows = std::min(kBatch, consumed - c0);
+        write_params(m, kParamCatchup, m->ck_mtp_position + c0);
+        m->target_norm = m->long_norm + (size_t)c0 * kHidden;
+        ok = upload_tokens(m, inputs.data() + c0, rows, m->tokens) && flush_params(m) &&
+             mtp_catchup(m, step_of(m, kParamCatchup, m->tokens), rows) &&
+             hip_ok(hipStreamSynchronize(m->stream), "catch-up");
+    }
+    m->target_norm = saved_norm;
+    if (!ok) return false;
+    accepted->assign(drafts.begin(), drafts.begin() + matched);
+    if (mismatch) accepted->push_back(next);
+    *next_row = m->logits + (size_t)(consumed - 1 - last_chunk) * kVocab;
+    m->mtp_position = m->ck_mtp_position + consumed;
+    return true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1336,9 +1450,22 @@ int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_toke
     if (!m || !m->mtp_enabled || !accepted_tokens || !accepted_count || !next_logits || token >= kVocab ||
         draft_count == 0 || m->position != m->mtp_position || draft_count > m->context_length - m->position)
         return 0;
-    if (draft_count > kBatch) return report("draft_count above 8 is not supported"), 0;
     const uint32_t k = draft_count;
     if (!checkpoint(m)) return 0;
+    if (k > kBatch) {
+        std::vector<uint32_t> accepted;
+        const float *row = nullptr;
+        if (!speculative_chunked(m, token, stop_token, k, &accepted, &row) || !logits_to_host(m, row)) {
+            restore_target(m);
+            (void)restore_mtp(m);
+            (void)hipStreamSynchronize(m->stream);
+            return 0;
+        }
+        for (size_t i = 0; i < accepted.size(); ++i) accepted_tokens[i] = accepted[i];
+        *accepted_count = (uint32_t)accepted.size();
+        *next_logits = m->host_logits;
+        return 1;
+    }
     for (uint32_t i = 0; i < k; ++i) write_params(m, kParamDraft0 + i, m->ck_mtp_position + i);
     write_params(m, kParamTarget, m->ck_position);
     if (!upload_tokens(m, &token, 1, m->drafts) || !flush_params(m)) return 0;

@@ -17,7 +17,20 @@
  *   Q6_K  w = d*sc*(q-32), sc uniform int8;
  *   IQ1_M w = d*(2s+1)*(grid +- 1/8), grid values in {-1,0,1}.
  *
- * Usage: q38_synth_gguf OUT.gguf SEED q4km|iq1m
+ * Two more variants exercise the speculative path, whose drafts random
+ * weights almost never get accepted:
+ *   accept      the Q4_K_M layout without the MTP block (64 blocks), with an
+ *               LM head whose rows 2.. are all-zero blocks, so every logit
+ *               but the first two is exactly zero and the greedy token is 0,
+ *               1 or 2: MTP drafts and the target agree about a third of the
+ *               time;
+ *   accept_mtp  the matching separate MTP checkpoint (q38_model_attach_mtp_gguf):
+ *               65-block metadata, token_embd, the same LM head and block 64
+ *               with its nextn.* tensors.
+ * A tensor's bytes depend on its place in the full 65-block Q4_K_M list, so
+ * tensors shared between variants are byte-identical.
+ *
+ * Usage: q38_synth_gguf OUT.gguf SEED q4km|iq1m|accept|accept_mtp
  */
 #define _GNU_SOURCE
 #include <fcntl.h>
@@ -78,6 +91,9 @@ typedef struct {
     uint64_t offset;
     uint64_t nbytes;
     int kind;      /* 0 matrix, 1 norm weight, 2 conv, 3 dt bias, 4 ssm_a */
+    int live_rows; /* > 0: only the first live_rows rows are non-zero */
+    int written;   /* part of the output file */
+    uint64_t id;   /* seed index: place in the full tensor list */
 } Tensor;
 
 static Tensor tensors[1024];
@@ -95,7 +111,10 @@ static uint64_t block_bytes(uint32_t type)
 
 static void add(const char *name, uint64_t width, uint64_t rows, uint32_t type, int kind)
 {
-    Tensor *t = &tensors[tensor_count++];
+    Tensor *t = &tensors[tensor_count];
+    memset(t, 0, sizeof(*t));
+    t->id = (uint64_t)tensor_count++;
+    t->written = 1;
     snprintf(t->name, sizeof(t->name), "%s", name);
     t->n_dims = rows ? 2 : 1;
     t->shape[0] = width;
@@ -220,9 +239,14 @@ static void generate(const Tensor *t, uint64_t seed, uint64_t tid, uint64_t begi
     }
     const uint64_t bb = block_bytes(t->type);
     const double fan_in = (double)t->shape[0];
+    const uint64_t live_end = t->live_rows > 0 ? (uint64_t)t->live_rows * (t->shape[0] / 256) * bb : UINT64_MAX;
     for (uint64_t off = begin; off < end; off += bb) {
         const uint64_t index = off / bb;
         uint8_t *b = out + (off - begin);
+        if (off >= live_end) {
+            memset(b, 0, bb);          /* zero block: d = 0, every weight 0 */
+            continue;
+        }
         if (t->type == Q4_K) q4k_block(b, seed, tid, index, 1.0 / (168.0 * sqrt(fan_in)));
         else if (t->type == Q6_K) q6k_block(b, seed, tid, index, 1.0 / (1367.0 * sqrt(fan_in)));
         else iq1m_block(b, seed, tid, index, 1.0 / (7.5 * sqrt(fan_in)));
@@ -249,17 +273,35 @@ static void meta_u32(Buf *b, const char *key, uint32_t v) { put_str(b, key); put
 
 int main(int argc, char **argv)
 {
-    if (argc != 4 || (strcmp(argv[3], "q4km") && strcmp(argv[3], "iq1m"))) {
-        fprintf(stderr, "usage: %s OUT.gguf SEED q4km|iq1m\n", argv[0]);
+    const char *variant = argc == 4 ? argv[3] : "";
+    const int accept = strcmp(variant, "accept") == 0, accept_mtp = strcmp(variant, "accept_mtp") == 0;
+    if (argc != 4 || (strcmp(variant, "q4km") && strcmp(variant, "iq1m") && !accept && !accept_mtp)) {
+        fprintf(stderr, "usage: %s OUT.gguf SEED q4km|iq1m|accept|accept_mtp\n", argv[0]);
         return 2;
     }
     const uint64_t seed = strtoull(argv[2], NULL, 0);
-    const uint32_t m = strcmp(argv[3], "q4km") == 0 ? Q4_K : IQ1_M;
+    const uint32_t m = strcmp(variant, "iq1m") == 0 ? IQ1_M : Q4_K;
 
     add("token_embd.weight", HIDDEN, VOCAB, Q4_K, 0);
     add("output_norm.weight", HIDDEN, 0, F32, 1);
     add("output.weight", HIDDEN, VOCAB, Q6_K, 0);
+    const int first_mtp_tensor = tensor_count;
     for (int layer = 0; layer <= LAYERS; ++layer) add_layer(layer, m);
+    int mtp_begin = first_mtp_tensor;
+    while (mtp_begin < tensor_count && strncmp(tensors[mtp_begin].name, "blk.64.", 7) != 0) ++mtp_begin;
+    if (accept || accept_mtp) {
+        tensors[2].live_rows = 2;
+        for (int i = 0; i < tensor_count; ++i) {
+            const int mtp_part = i == 0 || i == 2 || i >= mtp_begin;
+            tensors[i].written = accept ? i < mtp_begin : mtp_part;
+        }
+    }
+    /* the written tensors, in list order */
+    int kept = 0;
+    for (int i = 0; i < tensor_count; ++i)
+        if (tensors[i].written) tensors[kept++] = tensors[i];
+    tensor_count = kept;
+    const uint32_t block_count = accept ? LAYERS : LAYERS + 1;
 
     uint64_t offset = 0;
     for (int i = 0; i < tensor_count; ++i) {
@@ -275,8 +317,8 @@ int main(int argc, char **argv)
     put_u64(&h, 14);
     put_str(&h, "general.architecture"); put_u32(&h, 8); put_str(&h, "qwen35");
     meta_u32(&h, "general.alignment", 32);
-    meta_u32(&h, "qwen35.block_count", LAYERS + 1);
-    meta_u32(&h, "qwen35.nextn_predict_layers", 1);
+    meta_u32(&h, "qwen35.block_count", block_count);
+    meta_u32(&h, "qwen35.nextn_predict_layers", block_count == LAYERS + 1 ? 1 : 0);
     meta_u32(&h, "qwen35.embedding_length", HIDDEN);
     meta_u32(&h, "qwen35.feed_forward_length", FFN);
     meta_u32(&h, "qwen35.attention.head_count", 24);
@@ -317,7 +359,7 @@ int main(int argc, char **argv)
             const uint64_t begin = (uint64_t)s * step;
             const uint64_t end = begin + step < t->nbytes ? begin + step : t->nbytes;
             uint8_t *buffer = malloc(end - begin);
-            generate(t, seed, (uint64_t)i, begin, end, buffer);
+            generate(t, seed, t->id, begin, end, buffer);
             if (pwrite(fd, buffer, end - begin, (off_t)(data_start + t->offset + begin)) != (ssize_t)(end - begin))
                 failed |= 1;
             free(buffer);
