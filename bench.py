@@ -69,6 +69,8 @@ WORKLOADS = {
     "iq1m_gemm_m3": (29, 34816, 5120, 3, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 3 tokens"),
     "q4k_tiled_m8": (12, 34816, 5120, 8, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
     "iq1m_gemm_m8": (29, 34816, 5120, 8, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
+    "q4k_wide_m256": (12, 34816, 5120, 256, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 256 tokens (prefill)"),
+    "q4k_wide_down_m256": (12, 5120, 17408, 256, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 256 tokens (prefill)"),
 }
 # dense matrix-core peaks of MI355X, TOP/s: the Q4_K GEMM runs fp16 MFMA, IQ1_M int8
 MFMA_PEAK_TOPS = {12: ("f16", 2500.0), 29: ("i8", 5000.0)}

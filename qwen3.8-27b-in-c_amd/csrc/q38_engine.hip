@@ -41,7 +41,12 @@ constexpr uint32_t kRecurrent = 48, kFullLayers = 17;
 constexpr uint32_t kQKV = 10240, kLinV = 6144, kVHeads = 48, kHeadDim = 128;
 constexpr uint32_t kQGDim = 12288, kQDim = 6144, kKVDim = 1024, kAttnHeads = 24;
 constexpr uint32_t kVocab = 248320;
-constexpr uint32_t kBatch = 8;           /* rows per batched step (GEMM limit) */
+constexpr uint32_t kBatch = 8;           /* rows per batched decode step (verify, catch-up) */
+/* rows of one prefill batch: the prompt runs through all blocks in batches
+ * of up to this many tokens (fewer at long contexts, where the attention
+ * scores of a batch take rows x 24 x context floats) */
+constexpr uint32_t kPrefillRows = 512;
+constexpr size_t kPrefillScoresBytes = (size_t)1 << 30;
 constexpr uint32_t kQ8KBytes = 292;
 
 /* device parameter blocks of kParamWords words: [0] position of row 0 of
@@ -68,6 +73,11 @@ bool hip_ok(hipError_t e, const char *what)
 
 /* elements and bytes per block of the GGML types (the GGUF format's own
  * constants; src/io/qwen38_gguf.c:129-185 lists the same) */
+/* every kernel launch of a step is checked once, at the step's end; an
+ * error left by the caller's own HIP work before the call is not ours */
+bool launches_ok() { return hip_ok(hipGetLastError(), "kernel launch"); }
+void begin_call() { (void)hipGetLastError(); }
+
 void ggml_block(uint32_t type, uint32_t *elements, uint32_t *bytes)
 {
     uint32_t e = 0, b = 0;
@@ -349,7 +359,8 @@ struct Q38Model {
     float *mtp_hidden = nullptr, *ck_mtp_hidden = nullptr;
     uint32_t slot_host[kRecurrent] = {0}, ck_slot[kRecurrent] = {0};
     float *rope = nullptr;
-    /* scratch, kBatch rows */
+    /* scratch of scratch_rows rows (the larger of kBatch and the prefill batch) */
+    uint32_t prefill_rows = kBatch, scratch_rows = kBatch;
     /* wide0 holds a group's concatenated outputs: up to 2 * kFFN floats per row */
     float *hidden = nullptr, *norm = nullptr, *branch = nullptr, *wide0 = nullptr;
     float *qbuf = nullptr, *attn = nullptr;
@@ -648,23 +659,27 @@ void release(Q38Model *m)
 bool allocate_state(Q38Model *m)
 {
     const uint32_t ctx = m->context_length;
-    const uint32_t B = kBatch;
+    const size_t by_scores = kPrefillScoresBytes / ((size_t)kAttnHeads * ctx * sizeof(float));
+    m->prefill_rows = (uint32_t)std::max<size_t>(kBatch, std::min<size_t>(kPrefillRows, by_scores));
+    m->scratch_rows = std::max(kBatch, m->prefill_rows);
+    const uint32_t B = m->scratch_rows;
     const size_t slots = q38::kRecurrentStateSlots;
     bool ok = dalloc(&m->conv_state, slots * conv_count()) && dalloc(&m->delta_state, slots * delta_count()) &&
               dalloc(&m->key_cache, kv_count(ctx)) && dalloc(&m->value_cache, kv_count(ctx)) &&
               dalloc(&m->mtp_hidden, kHidden) && dalloc(&m->rope, (size_t)ctx * 64) &&
-              dalloc(&m->hidden, (size_t)B * kHidden) && dalloc(&m->norm, (size_t)B * 2 * kHidden) &&
+              dalloc(&m->hidden, (size_t)B * kHidden) && dalloc(&m->norm, (size_t)kBatch * 2 * kHidden) &&
               dalloc(&m->branch, (size_t)B * kHidden) && dalloc(&m->wide0, (size_t)B * 2 * kFFN) &&
               dalloc(&m->qbuf, (size_t)B * kQDim) && dalloc(&m->attn, (size_t)B * kLinV) &&
               dalloc(&m->scores, (size_t)B * kAttnHeads * ctx) &&
-              dalloc(&m->logits, (size_t)B * kVocab) && dalloc(&m->target_norm, (size_t)B * kHidden) &&
+              dalloc(&m->logits, (size_t)kBatch * kVocab) && dalloc(&m->target_norm, (size_t)B * kHidden) &&
               dalloc(&m->q8k, (size_t)B * (kFFN / 256) * kQ8KBytes) && dalloc(&m->tokens, B) &&
               dalloc(&m->params, (size_t)kParamSets * kParamWords) && dalloc(&m->words, 48) &&
-              dalloc(&m->argmax_pv, (size_t)B * q38::argmax_chunks(kVocab)) &&
-              dalloc(&m->argmax_pi, (size_t)B * q38::argmax_chunks(kVocab)) &&
+              dalloc(&m->argmax_pv, (size_t)kBatch * q38::argmax_chunks(kVocab)) &&
+              dalloc(&m->argmax_pi, (size_t)kBatch * q38::argmax_chunks(kVocab)) &&
               hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_logits), kVocab * sizeof(float)),
                      "pinned logits") &&
-              hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_words), 128 * sizeof(uint32_t)), "pinned ids") &&
+              hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_words), ((size_t)B + 128) * sizeof(uint32_t)),
+                     "pinned ids") &&
               hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_params),
                                    (size_t)kParamSets * kParamWords * sizeof(uint32_t)), "pinned parameters");
     if (!ok) return false;
@@ -744,16 +759,29 @@ Step step_of(Q38Model *m, uint32_t param_set, const uint32_t *tokens)
 
 /* GEMM over `count` Q8_K rows already in m->q8k (starting at block
  * `first_block`) */
+/* row-major GEMM of `count` Q8_K rows at x: launches of up to kBatch
+ * tokens (every token's outputs are independent of the batch) */
+bool gemm_rows(Q38Model *m, const DevTensor &w, uint32_t count, const uint8_t *x, float *out, uint32_t ldy,
+               uint32_t rows, const uint8_t *wdata)
+{
+    const uint32_t nb = (uint32_t)(w.width / 256);
+    for (uint32_t t0 = 0; t0 < count; t0 += kBatch) {
+        const uint32_t n = std::min(kBatch, count - t0);
+        if (!q38::launch_gemm_ld((int)w.type, (int)n, wdata, x + (size_t)t0 * nb * kQ8KBytes, out + (size_t)t0 * ldy,
+                                 ldy, rows, nb, m->grid, m->stream))
+            return report("unsupported GEMM configuration");
+    }
+    return true;
+}
+
 bool gemm_q(Q38Model *m, const DevTensor &w, uint32_t count, float *out, size_t first_block = 0)
 {
     if (count >= 2 && w.tiled &&
         q38::launch_gemm_q4k_tiled((int)count, w.tiled, m->q8k + first_block * kQ8KBytes, out, (uint32_t)w.rows,
                                    (uint32_t)w.rows, (uint32_t)(w.width / 256), m->stream))
         return true;
-    if (!q38::launch_gemm((int)w.type, (int)count, w.data, m->q8k + first_block * kQ8KBytes, out, (uint32_t)w.rows,
-                          (uint32_t)(w.width / 256), m->grid, m->stream))
-        return report("unsupported GEMM configuration");
-    return true;
+    return gemm_rows(m, w, count, m->q8k + first_block * kQ8KBytes, out, (uint32_t)w.rows, (uint32_t)w.rows,
+                     w.data);
 }
 
 uint64_t row_bytes(const DevTensor &t)
@@ -853,9 +881,7 @@ bool gemm_group(Q38Model *m, const Group &g, int lo, int hi, uint32_t count, flo
         if (count >= 2 && a.tiled &&
             q38::launch_gemm_q4k_tiled((int)count, a.tiled, m->q8k, y, ldy, (uint32_t)rows, nb, m->stream))
             return;
-        if (!q38::launch_gemm_ld((int)a.type, (int)count, a.data, m->q8k, y, ldy, (uint32_t)rows, nb, m->grid,
-                                 m->stream))
-            ok = report("unsupported GEMM configuration");
+        if (!gemm_rows(m, a, count, m->q8k, y, ldy, (uint32_t)rows, a.data)) ok = false;
     });
     return ok;
 }
@@ -948,15 +974,18 @@ bool linear_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count
     }
     float *conv = m->conv_state + (size_t)r * kQKV * 3;
     float *delta = m->delta_state + (size_t)r * kVHeads * kHeadDim * kHeadDim;
-    if (tr) {
-        /* the layer trace prints the prepared q/k/v: separate kernels */
+    if (tr || count > kBatch) {
+        /* the layer trace prints the prepared q/k/v: separate kernels; a
+         * prefill batch keeps only the state after its last row */
+        const bool last_only = count > kBatch;
         q38::launch_deltanet_prep(m->wide0, ld, (int)g.first[2], (int)g.first[3], conv, (long long)conv_count(),
-                                  s.params + 1 + r, (int)count, L.conv.f32(), L.a.f32(), L.dt.f32(), m->stream);
+                                  s.params + 1 + r, (int)count, L.conv.f32(), L.a.f32(), L.dt.f32(), last_only,
+                                  m->stream);
         trace(m, "dn_qkv-", layer, m->wide0, kQKV);
         trace(m, "dn_beta-", layer, m->wide0 + g.first[2], kVHeads);
         trace(m, "dn_alpha-", layer, m->wide0 + g.first[3], kVHeads);
         q38::launch_deltanet_state(m->attn, delta, (long long)delta_count(), s.params + 1 + r, (int)count, m->wide0,
-                                   ld, (int)g.first[2], (int)g.first[3], m->query_scale, m->stream);
+                                   ld, (int)g.first[2], (int)g.first[3], m->query_scale, last_only, m->stream);
     } else if (!q38::launch_deltanet_fused(m->attn, delta, (long long)delta_count(), s.params + 1 + r, (int)count,
                                            m->wide0, ld, (int)g.first[2], (int)g.first[3], m->query_scale, conv,
                                            (long long)conv_count(), L.conv.f32(), L.a.f32(), L.dt.f32(),
@@ -996,7 +1025,7 @@ bool layer_rows(Q38Model *m, const Step &s, int layer, uint32_t count)
     return true;
 }
 
-/* Target model over `count` (<= kBatch) tokens at positions params[0] + t:
+/* Target model over `count` (<= scratch_rows) tokens at positions params[0] + t:
  * all 64 blocks, the output norm into m->target_norm and, if `logit_rows`,
  * the LM head of the last `logit_rows` rows into m->logits
  * (q38_batch_target_eval, qwen38_model.c:1241-1266).  Enqueue only: the
@@ -1011,7 +1040,7 @@ bool target_rows(Q38Model *m, const Step &s, uint32_t count, uint32_t logit_rows
     norm_hidden(m, m->output_norm, count, m->target_norm);
     if (logit_rows && !gemm_q(m, m->output, logit_rows, m->logits, (size_t)(count - logit_rows) * (kHidden / 256)))
         return false;
-    return true;
+    return launches_ok();
 }
 
 /* KV-cache rows of the MTP block for `count` tokens at positions
@@ -1045,7 +1074,8 @@ bool mtp_catchup(Q38Model *m, const Step &s, uint32_t count)
     const size_t kv_off = (size_t)(kLayers / 4) * m->context_length * kKVDim;
     q38::launch_kv_write(m->wide0, m->wide0 + (g.first[2] - g.first[1]), ld, L.k_norm.f32(), m->rope,
                          m->key_cache + kv_off, m->value_cache + kv_off, s.params, (int)count, m->stream);
-    return hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm + (size_t)(count - 1) * kHidden,
+    return launches_ok() &&
+           hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm + (size_t)(count - 1) * kHidden,
                                  kHidden * sizeof(float), hipMemcpyDeviceToDevice, m->stream),
                   "mtp hidden");
 }
@@ -1068,7 +1098,7 @@ bool mtp_step(Q38Model *m, const Step &s)
     q38::launch_norm_quant(m->mtp_hidden, kHidden, m->q8k, kHB, m->hidden, kHidden,
                            m->pending_branch ? m->branch : nullptr, m->shared_head_norm.f32(), 1, m->stream);
     m->pending_branch = false;
-    return gemm_q(m, m->mtp_output, 1, m->logits);
+    return gemm_q(m, m->mtp_output, 1, m->logits) && launches_ok();
 }
 
 /* ---- graphs ------------------------------------------------------------------ */
@@ -1083,8 +1113,9 @@ uint64_t graph_key(uint32_t kind, uint32_t a, uint32_t b = 0) { return ((uint64_
  * device memory, so one graph serves every position).  Graphs are off while
  * tracing or when QWEN38_NO_GRAPHS is set. */
 template <typename Body>
-bool run_step(Q38Model *m, uint64_t key, Body body)
+bool run_step(Q38Model *m, uint64_t key, Body raw_body)
 {
+    auto body = [&] { return raw_body() && launches_ok(); };
     if (!m->graphs_enabled || trace_enabled()) return body();
     auto it = m->graphs.find(key);
     if (it != m->graphs.end()) return hip_ok(hipGraphLaunch(it->second, m->stream), "graph launch");
@@ -1108,8 +1139,10 @@ bool run_step(Q38Model *m, uint64_t key, Body body)
     return hip_ok(hipGraphLaunch(exec, m->stream), "graph launch");
 }
 
+/* token ids through the pinned staging (count <= scratch_rows) */
 bool upload_tokens(Q38Model *m, const uint32_t *tokens, uint32_t count, uint32_t *device)
 {
+    if (count > m->scratch_rows) return report("token batch larger than the scratch");
     for (uint32_t i = 0; i < count; ++i) {
         if (tokens[i] >= kVocab) return report("token id out of range");
         m->host_words[i] = tokens[i];
@@ -1338,6 +1371,7 @@ void q38_model_reset(Q38Model *m)
 
 int q38_model_forward_token(Q38Model *m, uint32_t token, const float **logits)
 {
+    begin_call();
     if (!m || !logits || token >= kVocab || m->position >= m->context_length) return 0;
     write_params(m, kParamTarget, m->position);
     if (!upload_tokens(m, &token, 1, m->tokens) || !flush_params(m)) return 0;
@@ -1359,6 +1393,7 @@ int q38_model_forward_token(Q38Model *m, uint32_t token, const float **logits)
 
 int q38_model_forward_token_layers(Q38Model *m, uint32_t token, uint32_t layer_count, float *hidden_out)
 {
+    begin_call();
     if (!m || !hidden_out || token >= kVocab || layer_count > kLayers || m->position >= m->context_length) return 0;
     write_params(m, kParamTarget, m->position);
     if (!upload_tokens(m, &token, 1, m->tokens) || !flush_params(m)) return 0;
@@ -1369,7 +1404,7 @@ int q38_model_forward_token_layers(Q38Model *m, uint32_t token, uint32_t layer_c
     for (uint32_t layer = 0; layer < layer_count; ++layer)
         if (!layer_rows(m, s, (int)layer, 1)) return 0;
     flush_branch(m, 1);
-    if (!hip_ok(hipMemcpyAsync(hidden_out, m->hidden, kHidden * sizeof(float), hipMemcpyDeviceToHost, m->stream),
+    if (!launches_ok() || !hip_ok(hipMemcpyAsync(hidden_out, m->hidden, kHidden * sizeof(float), hipMemcpyDeviceToHost, m->stream),
                 "hidden download") ||
         !hip_ok(hipStreamSynchronize(m->stream), "hidden download"))
         return 0;
@@ -1380,15 +1415,16 @@ int q38_model_forward_token_layers(Q38Model *m, uint32_t token, uint32_t layer_c
 
 int q38_model_prefill(Q38Model *m, const uint32_t *tokens, uint32_t count, const float **logits)
 {
+    begin_call();
     if (!m || !tokens || !count || !logits || count > m->context_length - m->position) return 0;
     for (uint32_t i = 0; i < count; ++i)
         if (tokens[i] >= kVocab) return 0;
     const uint32_t base = m->position;
-    /* chunks of kBatch tokens through all blocks (q38_model_prefill,
-     * qwen38_model.c:1519-1560): every row's arithmetic is independent of
-     * the chunking, and state advances in token order */
-    for (uint32_t done = 0; done < count; done += kBatch) {
-        const uint32_t n = std::min(kBatch, count - done);
+    /* batches of up to prefill_rows tokens through all blocks
+     * (q38_model_prefill, qwen38_model.c:1519-1560): every row's arithmetic
+     * is independent of the batching, and state advances in token order */
+    for (uint32_t done = 0; done < count; done += m->prefill_rows) {
+        const uint32_t n = std::min(m->prefill_rows, count - done);
         const bool last = done + n == count;
         write_params(m, kParamTarget, base + done);
         write_params(m, kParamCatchup, base + done);
@@ -1421,6 +1457,7 @@ int q38_model_enable_mtp(Q38Model *m)
 
 int q38_model_mtp_forward(Q38Model *m, uint32_t token, const float **logits)
 {
+    begin_call();
     if (!m || !m->mtp_enabled || !logits || token >= kVocab || m->mtp_position >= m->context_length) return 0;
     write_params(m, kParamDraft0, m->mtp_position);
     if (!upload_tokens(m, &token, 1, m->drafts) || !flush_params(m)) return 0;
@@ -1447,6 +1484,7 @@ int q38_model_mtp_forward(Q38Model *m, uint32_t token, const float **logits)
 int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_token, uint32_t draft_count,
                                  uint32_t *accepted_tokens, uint32_t *accepted_count, const float **next_logits)
 {
+    begin_call();
     if (!m || !m->mtp_enabled || !accepted_tokens || !accepted_count || !next_logits || token >= kVocab ||
         draft_count == 0 || m->position != m->mtp_position || draft_count > m->context_length - m->position)
         return 0;

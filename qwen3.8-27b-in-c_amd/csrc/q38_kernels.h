@@ -29,6 +29,12 @@ bool launch_gemm_q4k_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, floa
 /* same product, 32 weight rows per wavefront (v_mfma_f32_32x32x16_f16) */
 bool launch_gemm_q4k_t32(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                          uint32_t nb, hipStream_t stream);
+/* q38_wide.hip: the same product for any token count (the prefill batch),
+ * 64 rows x 64 tokens per workgroup; false for unsupported shapes.
+ * launch_gemm_q4k_tiled takes it from kWideMinTokens tokens on. */
+constexpr int kWideMinTokens = 9;
+bool launch_gemm_q4k_wide(uint32_t tokens, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy,
+                          uint32_t rows, uint32_t nb, hipStream_t stream);
 /* same with the token rows of y `ldy` floats apart (ldy >= rows) */
 bool launch_gemm_ld(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                     uint32_t nblk, const void *grid, hipStream_t stream);
@@ -59,12 +65,14 @@ void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int 
  * floats apart: row t of a batch reads slot (*slot + t) and writes slot
  * (*slot + t + 1), both mod kRecurrentStateSlots, so the state after any
  * prefix of the batch stays available. */
+/* last_only: write only the state after the last row (slot *slot + rows),
+ * for prefill batches of any length */
 void launch_deltanet_prep(float *qkv, long long ld, int beta_off, int alpha_off, float *conv_state,
                           long long slot_stride, const uint32_t *slot, int rows, const float *conv_w,
-                          const float *ssm_a, const float *ssm_dt, hipStream_t stream);
+                          const float *ssm_a, const float *ssm_dt, bool last_only, hipStream_t stream);
 void launch_deltanet_state(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,
                            const float *qkv, long long ld, int beta_off, int alpha_off, float query_scale,
-                           hipStream_t stream);
+                           bool last_only, hipStream_t stream);
 /* launch_deltanet_prep + launch_deltanet_state in one kernel (1..8 rows;
  * false otherwise); q/k/v, beta and alpha in qkv stay untransformed */
 bool launch_deltanet_fused(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,

@@ -117,14 +117,16 @@ constexpr uint32_t kStateSlots = kRecurrentStateSlots;
  * 128 channels (blocks 0..31 are the 16 q heads and 16 k heads); block 80
  * does beta/alpha.  The conv state before row t is slot (*slot_ptr + t) (mod
  * kStateSlots); each row's shifted state is written to the next slot, and
- * the chain between rows stays in registers. */
+ * the chain between rows stays in registers.  With `last_only` (a prefill
+ * batch, whose intermediate states nothing reads) only the last row's state
+ * is written, to slot (*slot_ptr + rows). */
 __global__ __launch_bounds__(128) void deltanet_prep_kernel(float *__restrict__ qkv, long long ld, int beta_off,
                                                             int alpha_off, float *__restrict__ conv_state,
                                                             long long slot_stride,
                                                             const uint32_t *__restrict__ slot_ptr, int rows,
                                                             const float *__restrict__ conv_w,
                                                             const float *__restrict__ ssm_a,
-                                                            const float *__restrict__ ssm_dt)
+                                                            const float *__restrict__ ssm_dt, int last_only)
 {
     const int tid = threadIdx.x;
     if (blockIdx.x == kQKV / 128) {
@@ -154,10 +156,12 @@ __global__ __launch_bounds__(128) void deltanet_prep_kernel(float *__restrict__ 
         s0 = s1;
         s1 = s2;
         s2 = x;
-        float *st_out = conv_state + (size_t)((slot0 + t + 1) % kStateSlots) * slot_stride + (size_t)ch * 3;
-        st_out[0] = s0;
-        st_out[1] = s1;
-        st_out[2] = s2;
+        if (!last_only || t == rows - 1) {
+            float *st_out = conv_state + (size_t)((slot0 + t + 1) % kStateSlots) * slot_stride + (size_t)ch * 3;
+            st_out[0] = s0;
+            st_out[1] = s1;
+            st_out[2] = s2;
+        }
         const float y = siluf_exact(value);
         if (blockIdx.x >= 2 * kQKDim / 128) {
             row[ch] = y;
@@ -195,12 +199,14 @@ __device__ __forceinline__ float avx2_tree32(float v)
  * `rows` consecutive tokens (row t's prepared q|k|v at qkv + t * ld, beta
  * and alpha at + beta_off / alpha_off, output at out + t * kLinV): the
  * state before row t is slot (*slot_ptr + t), read once, kept in registers,
- * and each row's result is written to the next slot. */
+ * and each row's result is written to the next slot (with `last_only`, only
+ * the last row's, to slot *slot_ptr + rows). */
 __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__ out, float *__restrict__ state,
                                                              long long slot_stride,
                                                              const uint32_t *__restrict__ slot_ptr, int rows,
                                                              const float *__restrict__ qkv, long long ld,
-                                                             int beta_off, int alpha_off, float query_scale)
+                                                             int beta_off, int alpha_off, float query_scale,
+                                                             int last_only)
 {
     const int column_global = blockIdx.x * 8 + (threadIdx.x >> 5);   /* 0 .. 48*128-1 */
     const int h = column_global >> 7;
@@ -229,10 +235,11 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
         const float pred = avx2_tree32(p);
         const float delta = __fmul_rn(__fsub_rn(v[c], pred), row[beta_off + h]);
         float *s_out = state + (size_t)((slot0 + t + 1) % kStateSlots) * slot_stride + col_off;
+        const bool store = !last_only || t == rows - 1;
         float r = 0.0f;
         for (int a = 0; a < 4; ++a) {
             sv[a] = __builtin_fmaf(kv[a], delta, sv[a]);
-            s_out[32 * a + l] = sv[a];
+            if (store) s_out[32 * a + l] = sv[a];
             r = __builtin_fmaf(sv[a], qv[a], r);
         }
         const float result = avx2_tree32(r);
@@ -630,18 +637,19 @@ void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int 
 
 void launch_deltanet_prep(float *qkv, long long ld, int beta_off, int alpha_off, float *conv_state,
                           long long slot_stride, const uint32_t *slot, int rows, const float *conv_w,
-                          const float *ssm_a, const float *ssm_dt, hipStream_t stream)
+                          const float *ssm_a, const float *ssm_dt, bool last_only, hipStream_t stream)
 {
     deltanet_prep_kernel<<<kQKV / 128 + 1, 128, 0, stream>>>(qkv, ld, beta_off, alpha_off, conv_state, slot_stride,
-                                                             slot, rows, conv_w, ssm_a, ssm_dt);
+                                                             slot, rows, conv_w, ssm_a, ssm_dt, last_only ? 1 : 0);
 }
 
 void launch_deltanet_state(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,
                            const float *qkv, long long ld, int beta_off, int alpha_off, float query_scale,
-                           hipStream_t stream)
+                           bool last_only, hipStream_t stream)
 {
     deltanet_state_kernel<<<kVHeads * kHeadDim / 8, 256, 0, stream>>>(attn, delta_state, slot_stride, slot, rows,
-                                                                     qkv, ld, beta_off, alpha_off, query_scale);
+                                                                     qkv, ld, beta_off, alpha_off, query_scale,
+                                                                     last_only ? 1 : 0);
 }
 
 bool launch_deltanet_fused(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,

@@ -421,7 +421,9 @@ bool launch_tiled_nb(int m, const uint8_t *w, const uint8_t *x, float *y, uint32
 bool launch_gemm_q4k_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                            uint32_t nb, hipStream_t stream)
 {
-    if (!rows || ldy < rows) return false;
+    if (!rows || ldy < rows || m < 2) return false;
+    /* prefill batches: the 64 x 64 matrix-core tiles of q38_wide.hip */
+    if (m >= kWideMinTokens) return launch_gemm_q4k_wide((uint32_t)m, w_tiled, x, y, ldy, rows, nb, stream);
     /* 4096 rows or more: 32 rows per wavefront (measured faster there; the
      * 16-row kernel keeps the small matrices) */
     if (rows >= 4096) return launch_gemm_q4k_t32(m, w_tiled, x, y, ldy, rows, nb, stream);

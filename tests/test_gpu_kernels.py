@@ -235,3 +235,38 @@ def test_tiled_gemm_any_batch_size(hip, oracle, device):
         want = oracle.gemm(Q4_K, w, rows, q[:m * nb], m)
         got = hip.gemm_q8_k_tiled(tiled, width, rows, xq[:m * nb * 292], m).cpu().numpy()
         assert np.array_equal(bits(got), bits(want)), "M=%d" % m
+
+
+@pytest.mark.parametrize("rows,width", [(136, 5120), (64, 17408), (200, 6144), (72, 10240)])
+def test_wide_gemm_prefill_batches_bit_exact(hip, oracle, device, rows, width):
+    """Prefill batches (16 tokens and more) on the 64 x 64 matrix-core tiles:
+    every token's row equals the oracle's one-token GEMV bit for bit, with
+    ragged row counts (a padded last 16-row tile, a workgroup past the last
+    tile) and token counts that end inside a 64-token tile."""
+    w = synth.matrix(Q4_K, rows, width, seed=rows * 7 + width)
+    x = synth.activations(width, seed=rows + width, count=100)
+    q = oracle.quantize(x.reshape(-1))
+    nb = width // 256
+    tiled = hip.repack_q4k_tiles(to_dev(w, device), width, rows)
+    xq = hip.quantize_q8_k(to_dev(x, device))
+    want = oracle.gemm(Q4_K, w, rows, q, 100)
+    for m in (16, 33, 64, 100):
+        got = hip.gemm_q8_k_tiled(tiled, width, rows, xq[:m * nb * 292], m).cpu().numpy()
+        assert np.array_equal(bits(got), bits(want[:m])), "M=%d" % m
+
+
+@pytest.mark.parametrize("rows,width", [(34816, 5120), (5120, 17408), (16480, 5120)])
+def test_wide_gemm_full_shapes_match_decode_kernels(hip, device, rows, width):
+    """Full prefill shapes (gate|up, down, DeltaNet input group) at 256 tokens
+    against the 2..8-token kernels on the same activations."""
+    m = 256
+    w = synth.matrix(Q4_K, rows, width, seed=rows + 3)
+    wd = to_dev(w, device)
+    tiled = hip.repack_q4k_tiles(wd, width, rows)
+    x = synth.activations(width, seed=width + 5, count=m)
+    xq = hip.quantize_q8_k(to_dev(x, device))
+    got = hip.gemm_q8_k_tiled(tiled, width, rows, xq, m).cpu().numpy()
+    nb = width // 256
+    for t0 in (0, 8, 120, 248):
+        want = hip.gemm_q8_k_tiled(tiled, width, rows, xq[t0 * nb * 292:(t0 + 8) * nb * 292], 8).cpu().numpy()
+        assert np.array_equal(bits(got[t0:t0 + 8]), bits(want)), (rows, width, t0)
