@@ -70,6 +70,7 @@ WORKLOADS = {
     "q4k_tiled_m8": (12, 34816, 5120, 8, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
     "iq1m_gemm_m8": (29, 34816, 5120, 8, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
     "q4k_wide_m256": (12, 34816, 5120, 256, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 256 tokens (prefill)"),
+    "iq1m_wide_m256": (29, 34816, 5120, 256, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 256 tokens (prefill)"),
     "q4k_wide_down_m256": (12, 5120, 17408, 256, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 256 tokens (prefill)"),
 }
 # dense matrix-core peaks of MI355X, TOP/s: the Q4_K GEMM runs fp16 MFMA, IQ1_M int8

@@ -206,6 +206,11 @@ int q38hip_gemm_q8_k(float *output, const Q38Q8KBlock *input, uint32_t batch_siz
      * are independent of the others in the batch, so consecutive launches
      * over token chunks give the same bits as one. */
     const uint32_t rows = (uint32_t)tensor->shape[1], nb = (uint32_t)(input_length / 256);
+    /* IQ1_M prefill batches: one launch of the 256 x 64 matrix-core tiles */
+    if (tensor->type == q38::kIQ1M && batch_size >= (uint32_t)q38::kWideMinTokens &&
+        q38::launch_gemm_iq1m_wide(batch_size, tensor->data, reinterpret_cast<const uint8_t *>(input), output, rows,
+                                   rows, nb, state->grid, static_cast<hipStream_t>(stream)))
+        return 1;
     for (uint32_t t0 = 0; t0 < batch_size;) {
         const uint32_t n = token_chunk(batch_size - t0, 1);
         if (!q38::launch_gemm((int)tensor->type, (int)n, tensor->data,

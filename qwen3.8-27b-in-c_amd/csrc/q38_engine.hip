@@ -365,6 +365,7 @@ struct Q38Model {
     float *hidden = nullptr, *norm = nullptr, *branch = nullptr, *wide0 = nullptr;
     float *qbuf = nullptr, *attn = nullptr;
     float *scores = nullptr, *logits = nullptr, *target_norm = nullptr;
+    float *prep = nullptr;   /* prepared DeltaNet inputs of a prefill batch */
     /* output-norm rows of a verify longer than kBatch rows (grown on demand) */
     float *long_norm = nullptr;
     uint32_t long_norm_rows = 0;
@@ -636,7 +637,7 @@ void release(Q38Model *m)
     float **fbufs[] = {&m->conv_state, &m->delta_state, &m->key_cache, &m->value_cache, &m->mtp_hidden,
                        &m->ck_mtp_hidden, &m->rope, &m->hidden, &m->norm,
                        &m->branch, &m->wide0, &m->qbuf, &m->attn, &m->scores, &m->logits, &m->target_norm,
-                       &m->argmax_pv, &m->long_norm};
+                       &m->argmax_pv, &m->long_norm, &m->prep};
     for (float **p : fbufs) dfree(*p);
     uint32_t **ubufs[] = {&m->tokens, &m->params, &m->words, &m->argmax_pi};
     for (uint32_t **p : ubufs) dfree(*p);
@@ -670,6 +671,7 @@ bool allocate_state(Q38Model *m)
               dalloc(&m->hidden, (size_t)B * kHidden) && dalloc(&m->norm, (size_t)kBatch * 2 * kHidden) &&
               dalloc(&m->branch, (size_t)B * kHidden) && dalloc(&m->wide0, (size_t)B * 2 * kFFN) &&
               dalloc(&m->qbuf, (size_t)B * kQDim) && dalloc(&m->attn, (size_t)B * kLinV) &&
+              dalloc(&m->prep, (size_t)B * 2 * kFFN) &&
               dalloc(&m->scores, (size_t)B * kAttnHeads * ctx) &&
               dalloc(&m->logits, (size_t)kBatch * kVocab) && dalloc(&m->target_norm, (size_t)B * kHidden) &&
               dalloc(&m->q8k, (size_t)B * (kFFN / 256) * kQ8KBytes) && dalloc(&m->tokens, B) &&
@@ -765,6 +767,9 @@ bool gemm_rows(Q38Model *m, const DevTensor &w, uint32_t count, const uint8_t *x
                uint32_t rows, const uint8_t *wdata)
 {
     const uint32_t nb = (uint32_t)(w.width / 256);
+    if (w.type == IQ1_M && count >= (uint32_t)q38::kWideMinTokens &&
+        q38::launch_gemm_iq1m_wide(count, wdata, x, out, ldy, rows, nb, m->grid, m->stream))
+        return true;
     for (uint32_t t0 = 0; t0 < count; t0 += kBatch) {
         const uint32_t n = std::min(kBatch, count - t0);
         if (!q38::launch_gemm_ld((int)w.type, (int)n, wdata, x + (size_t)t0 * nb * kQ8KBytes, out + (size_t)t0 * ldy,
@@ -974,10 +979,17 @@ bool linear_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count
     }
     float *conv = m->conv_state + (size_t)r * kQKV * 3;
     float *delta = m->delta_state + (size_t)r * kVHeads * kHeadDim * kHeadDim;
-    if (tr || count > kBatch) {
-        /* the layer trace prints the prepared q/k/v: separate kernels; a
-         * prefill batch keeps only the state after its last row */
-        const bool last_only = count > kBatch;
+    if (count > kBatch) {
+        /* a prefill batch: the prep of all rows in parallel into m->prep,
+         * then the state update keeping only the state after the last row */
+        q38::launch_deltanet_prep_rows(m->prep, m->wide0, ld, (int)g.first[2], (int)g.first[3], conv,
+                                       (long long)conv_count(), s.params + 1 + r, (int)count, L.conv.f32(),
+                                       L.a.f32(), L.dt.f32(), m->stream);
+        q38::launch_deltanet_state(m->attn, delta, (long long)delta_count(), s.params + 1 + r, (int)count, m->prep,
+                                   ld, (int)g.first[2], (int)g.first[3], m->query_scale, true, m->stream);
+    } else if (tr) {
+        /* the layer trace prints the prepared q/k/v: separate kernels */
+        const bool last_only = false;
         q38::launch_deltanet_prep(m->wide0, ld, (int)g.first[2], (int)g.first[3], conv, (long long)conv_count(),
                                   s.params + 1 + r, (int)count, L.conv.f32(), L.a.f32(), L.dt.f32(), last_only,
                                   m->stream);

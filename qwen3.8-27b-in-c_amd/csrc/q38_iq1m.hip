@@ -273,6 +273,202 @@ bool launch_iq1m_nb(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_
 
 }  // namespace
 
+/* IQ1_M x Q8_K for prefill batches (any token count): the products of
+ * gemm_iq1m_mfma (per 16-row x 16-token tile and 64-element chunk,
+ * E = 8 * A.[s grid] + A.[s sign] on v_mfma_i32_16x16x64_i8, the lane
+ * (r, q) taking sub-block 4q + c of the chunk c) with the fp32 chain
+ * total += d * (float(E) * 0.125f), d = dscale * xs, in block order per
+ * (row, token) in registers.  A workgroup of 8 wavefronts covers 256 rows x
+ * 64 tokens: wavefront w takes rows 32w .. 32w + 31 (two 16-row tiles)
+ * against all 64 tokens (four token tiles), so each decoded weight operand
+ * serves four token tiles and each activation operand two row tiles; the
+ * workgroup's wavefronts read the same activations, which L1 serves after
+ * the first.  Lane (r, q) of tile pair (rt, tt) owns tokens 16 tt + 4 q + j
+ * of row 16 rt + r. */
+constexpr int kIQWideRows = 256, kIQWideTokens = 64, kIQWideWaves = 8;
+
+template <int NB>
+__global__ __launch_bounds__(64 * kIQWideWaves, 1) void gemm_iq1m_wide(const uint8_t *__restrict__ w,
+                                                                      const uint8_t *__restrict__ x,
+                                                                      float *__restrict__ y, uint32_t ldy,
+                                                                      uint32_t rows, uint32_t tokens,
+                                                                      const uint2 *__restrict__ grid)
+{
+    __shared__ uint2 grid_s[2048];
+    __shared__ float xs_s[NB * kIQWideTokens];   /* [block][token] */
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int r = lane & 15, q = lane >> 4;
+    const uint32_t row0 = blockIdx.x * kIQWideRows + 32 * wv, tok0 = blockIdx.y * kIQWideTokens;
+    const uint32_t wtok = tokens - tok0 < (uint32_t)kIQWideTokens ? tokens - tok0 : kIQWideTokens;
+
+    for (int i = threadIdx.x; i < 2048; i += 64 * kIQWideWaves) {
+        const uint2 v = grid[i];
+        grid_s[i] = make_uint2(((v.x & 0x7f7f7f7fu) + 0x01010101u) ^ (v.x & 0x80808080u),
+                               ((v.y & 0x7f7f7f7fu) + 0x01010101u) ^ (v.y & 0x80808080u));
+    }
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w), 0, rows * NB * kIQ1MBytes, kRawBuf);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(x + (size_t)tok0 * NB * kQ8KBytes), 0, wtok * NB * kQ8KBytes, kRawBuf);
+    for (int i = threadIdx.x; i < NB * kIQWideTokens; i += 64 * kIQWideWaves) {
+        const int t = i % kIQWideTokens, b = i / kIQWideTokens;
+        xs_s[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, (uint32_t)((t * NB + b) * kQ8KBytes), 0, 0));
+    }
+    __syncthreads();
+
+    /* weight rows of the lane (rows past the matrix read as zero) and the
+     * activation offsets of its token in each token tile */
+    uint32_t woff[2], xoff[4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) woff[rt] = (row0 + 16 * rt + (uint32_t)r) * NB * kIQ1MBytes;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) xoff[tt] = (uint32_t)((16 * tt + r) * NB * kQ8KBytes + 4 + 64 * q);
+
+    struct WLoad {
+        uint32_t qs[2], qh, sc[2];
+    };
+    auto load_w = [&](int rt, int b) {
+        WLoad c;
+        const int2v qs = __builtin_bit_cast(
+            int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff[rt] + 8 * q, b * kIQ1MBytes, 0));
+        c.qs[0] = (uint32_t)qs[0];
+        c.qs[1] = (uint32_t)qs[1];
+        c.qh = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, woff[rt] + 32 + 4 * q, b * kIQ1MBytes, 0);
+        const int2v sc = __builtin_bit_cast(
+            int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff[rt] + 48, b * kIQ1MBytes, 0));
+        c.sc[0] = (uint32_t)sc[0];
+        c.sc[1] = (uint32_t)sc[1];
+        return c;
+    };
+
+    float total[2][4][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) total[rt][tt][j] = 0.0f;
+
+    WLoad wc[2] = {load_w(0, 0), load_w(1, 0)};
+    int4v ac[4][4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) ac[tt][cc] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[tt] + 16 * cc, 0, 0);
+
+#pragma unroll 1
+    for (int b = 0; b < NB; ++b) {
+        const int bn = b + 1 < NB ? b + 1 : b;   /* the next block's loads (the last re-reads, unused) */
+        const WLoad wn[2] = {load_w(0, bn), load_w(1, bn)};
+        int4v d1[2][4], d2[2][4];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) d1[rt][tt] = d2[rt][tt] = (int4v){0, 0, 0, 0};
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            int4v bw[2], bs[2];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const WLoad &c = wc[rt];
+                const uint32_t scw = (q & 2 ? c.sc[1] : c.sc[0]) >> (16 * (q & 1));   /* scale word q */
+                const uint32_t ib = (c.qs[cc >> 1] >> (16 * (cc & 1))) & 0xffffu;
+                const uint32_t hb = (c.qh >> (8 * cc)) & 0xffu;
+                const uint32_t i0 = (ib & 0xffu) | ((hb & 7u) << 8);
+                const uint32_t i1 = (ib >> 8) | ((hb & 0x70u) << 4);
+                const uint32_t sv = 2u * ((scw >> (3 * cc)) & 7u) + 1u;
+                const uint2 g0 = grid_s[i0], g1 = grid_s[i1];
+                const uint32_t ns = 256u - sv;
+                const uint32_t lut = ns | (sv << 16);
+                bw[rt][0] = (int)__builtin_amdgcn_perm(0u, lut, g0.x);
+                bw[rt][1] = (int)__builtin_amdgcn_perm(0u, lut, g0.y);
+                bw[rt][2] = (int)__builtin_amdgcn_perm(0u, lut, g1.x);
+                bw[rt][3] = (int)__builtin_amdgcn_perm(0u, lut, g1.y);
+                const uint32_t c0 = __builtin_amdgcn_perm(0u, (hb & 0x08u) ? ns : sv, 0u);
+                const uint32_t c1 = __builtin_amdgcn_perm(0u, (hb & 0x80u) ? ns : sv, 0u);
+                bs[rt][0] = (int)c0;
+                bs[rt][1] = (int)c0;
+                bs[rt][2] = (int)c1;
+                bs[rt][3] = (int)c1;
+            }
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    d1[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ac[tt][cc], bw[rt], d1[rt][tt], 0, 0, 0);
+                    d2[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ac[tt][cc], bs[rt], d2[rt][tt], 0, 0, 0);
+                }
+        }
+        /* the next block's activations, then the chains of this block */
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc)
+                ac[tt][cc] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[tt] + 16 * cc, bn * kQ8KBytes, 0);
+        float dsc[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const uint32_t u0 = wc[rt].sc[0] & 0xffffu, u1 = wc[rt].sc[0] >> 16, u2 = wc[rt].sc[1] & 0xffffu,
+                           u3 = wc[rt].sc[1] >> 16;
+            const uint32_t bits = (u0 >> 12) | ((u1 >> 8) & 0x00f0u) | ((u2 >> 4) & 0x0f00u) | (u3 & 0xf000u);
+            dsc[rt] = f16_to_f32(bits);
+        }
+        const float *xsb = xs_s + b * kIQWideTokens + 4 * q;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float xsv = xsb[16 * tt + j];
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const float d = fmul_rn(dsc[rt], xsv);
+                    const float e = (float)(8 * d1[rt][tt][j] + d2[rt][tt][j]);
+                    total[rt][tt][j] = fadd_rn(total[rt][tt][j], fmul_rn(d, fmul_rn(e, 0.125f)));
+                }
+            }
+        wc[0] = wn[0];
+        wc[1] = wn[1];
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+        const uint32_t row = row0 + 16 * rt + (uint32_t)r;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t tok = tok0 + 16 * tt + 4 * q + j;
+                if (row < rows && tok < tokens) y[(size_t)tok * ldy + row] = total[rt][tt][j];
+            }
+    }
+}
+
+namespace {
+template <int NB>
+bool launch_iq1m_wide_nb(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, uint32_t tokens,
+                         const uint2 *grid, hipStream_t stream)
+{
+    hipLaunchKernelGGL(gemm_iq1m_wide<NB>,
+                       dim3((rows + kIQWideRows - 1) / kIQWideRows, (tokens + kIQWideTokens - 1) / kIQWideTokens),
+                       dim3(64 * kIQWideWaves), 0, stream, w, x, y, ldy, rows, tokens, grid);
+    return hipGetLastError() == hipSuccess;
+}
+}  // namespace
+
+bool launch_gemm_iq1m_wide(uint32_t tokens, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                           uint32_t nb, const void *grid, hipStream_t stream)
+{
+    if (!rows || !tokens || ldy < rows || !grid || tokens > 65535u * kIQWideTokens) return false;
+    const uint2 *g = static_cast<const uint2 *>(grid);
+    switch (nb) {
+    case 20: return launch_iq1m_wide_nb<20>(w, x, y, ldy, rows, tokens, g, stream);
+    case 24: return launch_iq1m_wide_nb<24>(w, x, y, ldy, rows, tokens, g, stream);
+    case 40: return launch_iq1m_wide_nb<40>(w, x, y, ldy, rows, tokens, g, stream);
+    case 68: return launch_iq1m_wide_nb<68>(w, x, y, ldy, rows, tokens, g, stream);
+    default: return false;
+    }
+}
+
 /* y[t * ldy + row] = W_row . x_t (t < m <= 8) for IQ1_M weights of the
  * Qwen3.8 row widths (5120, 6144, 10240, 17408); false otherwise. */
 bool launch_gemm_iq1m_mfma(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,

@@ -21,6 +21,10 @@ bool launch_gemv_lanes(int type, int m, const uint8_t *w, const uint8_t *x, floa
  * tokens (false when the width or token count is not supported) */
 size_t tiled_q4k_bytes(uint32_t rows, uint32_t nb);
 bool launch_repack_q4k_tiles(uint8_t *dst, const uint8_t *src, uint32_t rows, uint32_t nb, hipStream_t stream);
+/* IQ1_M x Q8_K for prefill batches (any token count, 256 rows x 64 tokens
+ * per workgroup; false for unsupported widths) */
+bool launch_gemm_iq1m_wide(uint32_t tokens, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                           uint32_t nb, const void *grid, hipStream_t stream);
 /* IQ1_M x Q8_K for 1..8 tokens on the matrix cores (row-major blocks) */
 bool launch_gemm_iq1m_mfma(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                            uint32_t nb, const void *grid, hipStream_t stream);
@@ -73,6 +77,12 @@ void launch_deltanet_prep(float *qkv, long long ld, int beta_off, int alpha_off,
 void launch_deltanet_state(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,
                            const float *qkv, long long ld, int beta_off, int alpha_off, float query_scale,
                            bool last_only, hipStream_t stream);
+/* the prep of a prefill batch, all rows in parallel: prepared q/k/v, beta
+ * and alpha of row t go to out + t * ld (qkv untouched); the conv state
+ * after the batch goes to slot *slot + rows */
+void launch_deltanet_prep_rows(float *out, const float *qkv, long long ld, int beta_off, int alpha_off,
+                               float *conv_state, long long slot_stride, const uint32_t *slot, int rows,
+                               const float *conv_w, const float *ssm_a, const float *ssm_dt, hipStream_t stream);
 /* launch_deltanet_prep + launch_deltanet_state in one kernel (1..8 rows;
  * false otherwise); q/k/v, beta and alpha in qkv stay untransformed */
 bool launch_deltanet_fused(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,

@@ -218,22 +218,36 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
     const float *s = state + (size_t)(slot0 % kStateSlots) * slot_stride + col_off;
     float sv[4];
     for (int a = 0; a < 4; ++a) sv[a] = s[32 * a + l];
-    for (int t = 0; t < rows; ++t) {
+    /* row t's inputs are loaded while row t - 1 computes */
+    struct RowIn {
+        float k[4], q[4], v, alpha, beta;
+    };
+    auto load_row = [&](int t) {
         const float *row = qkv + (long long)t * ld;
-        const float *q = row + kh * kHeadDim;
-        const float *k = row + kQKDim + kh * kHeadDim;
-        const float *v = row + 2 * kQKDim + h * kHeadDim;
-        const float decay = q38_expf(row[alpha_off + h]);
+        RowIn in;
+        for (int a = 0; a < 4; ++a) {
+            in.k[a] = row[kQKDim + kh * kHeadDim + 32 * a + l];
+            in.q[a] = row[kh * kHeadDim + 32 * a + l];
+        }
+        in.v = row[2 * kQKDim + h * kHeadDim + c];
+        in.alpha = row[alpha_off + h];
+        in.beta = row[beta_off + h];
+        return in;
+    };
+    RowIn cur = load_row(0);
+    for (int t = 0; t < rows; ++t) {
+        const RowIn nxt = load_row(t + 1 < rows ? t + 1 : t);
+        const float decay = q38_expf(cur.alpha);
         float kv[4], qv[4];
         for (int a = 0; a < 4; ++a) {
             sv[a] = __fmul_rn(sv[a], decay);
-            kv[a] = k[32 * a + l];
-            qv[a] = q[32 * a + l];
+            kv[a] = cur.k[a];
+            qv[a] = cur.q[a];
         }
         float p = 0.0f;
         for (int a = 0; a < 4; ++a) p = __builtin_fmaf(sv[a], kv[a], p);
         const float pred = avx2_tree32(p);
-        const float delta = __fmul_rn(__fsub_rn(v[c], pred), row[beta_off + h]);
+        const float delta = __fmul_rn(__fsub_rn(cur.v, pred), cur.beta);
         float *s_out = state + (size_t)((slot0 + t + 1) % kStateSlots) * slot_stride + col_off;
         const bool store = !last_only || t == rows - 1;
         float r = 0.0f;
@@ -244,6 +258,85 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
         }
         const float result = avx2_tree32(r);
         if (l == 0) out[(size_t)t * kLinV + h * kHeadDim + c] = __fmul_rn(result, query_scale);
+        cur = nxt;
+    }
+}
+
+/* Prefill form of deltanet_prep_kernel.  The conv of row t reads only the
+ * inputs of rows t-3 .. t (the conv state before the batch stands in for
+ * rows before the first), so every (channel, row) is independent: block
+ * (cb, g) runs channels 128 cb .. 128 cb + 127 over rows kPrepRows g ..,
+ * reading the untransformed projections in `qkv` and writing the prepared
+ * values to `out` (same row stride and offsets).  The arithmetic per
+ * element, including the L2 norm of each q/k head and row (the block's sum
+ * over its 128 channels), is deltanet_prep_kernel's.  The block holding the
+ * last row writes the conv state after the batch to slot *slot_ptr + rows;
+ * block kQKV / 128 does beta / alpha. */
+constexpr int kPrepRows = 8;
+
+__global__ __launch_bounds__(128) void deltanet_prep_rows_kernel(float *__restrict__ out,
+                                                                 const float *__restrict__ qkv, long long ld,
+                                                                 int beta_off, int alpha_off,
+                                                                 float *__restrict__ conv_state,
+                                                                 long long slot_stride,
+                                                                 const uint32_t *__restrict__ slot_ptr, int rows,
+                                                                 const float *__restrict__ conv_w,
+                                                                 const float *__restrict__ ssm_a,
+                                                                 const float *__restrict__ ssm_dt)
+{
+    const int tid = threadIdx.x;
+    const int t0 = blockIdx.y * kPrepRows;
+    const int tn = rows - t0 < kPrepRows ? rows - t0 : kPrepRows;
+    if (blockIdx.x == kQKV / 128) {
+        if (tid < kVHeads) {
+            for (int i = 0; i < tn; ++i) {
+                const long long base = (long long)(t0 + i) * ld;
+                out[base + beta_off + tid] = sigmoidf_exact(qkv[base + beta_off + tid]);
+                out[base + alpha_off + tid] =
+                    __fmul_rn(ssm_a[tid], softplusf_exact(__fadd_rn(qkv[base + alpha_off + tid], ssm_dt[tid])));
+            }
+        }
+        return;
+    }
+    const int ch = blockIdx.x * 128 + tid;
+    const uint32_t slot0 = *slot_ptr;
+    const float *st = conv_state + (size_t)(slot0 % kStateSlots) * slot_stride + (size_t)ch * 3;
+    const float4 k = reinterpret_cast<const float4 *>(conv_w)[ch];
+    /* inputs of rows t0 - 3 .. t0 - 1 (the state before the batch for rows < 0) */
+    float s0 = t0 >= 3 ? qkv[(long long)(t0 - 3) * ld + ch] : st[t0];
+    float s1 = t0 >= 2 ? qkv[(long long)(t0 - 2) * ld + ch] : st[t0 + 1];
+    float s2 = t0 >= 1 ? qkv[(long long)(t0 - 1) * ld + ch] : st[2];
+    float xs[kPrepRows];
+#pragma unroll
+    for (int i = 0; i < kPrepRows; ++i) xs[i] = i < tn ? qkv[(long long)(t0 + i) * ld + ch] : 0.0f;
+    __shared__ float head[128];
+    for (int i = 0; i < tn; ++i) {
+        const float x = xs[i];
+        float value = 0.0f;
+        value = __fadd_rn(value, __fmul_rn(s0, k.x));
+        value = __fadd_rn(value, __fmul_rn(s1, k.y));
+        value = __fadd_rn(value, __fmul_rn(s2, k.z));
+        value = __fadd_rn(value, __fmul_rn(x, k.w));
+        s0 = s1;
+        s1 = s2;
+        s2 = x;
+        const float y = siluf_exact(value);
+        float *o = out + (long long)(t0 + i) * ld + ch;
+        if (blockIdx.x >= 2 * kQKDim / 128) {
+            *o = y;
+            continue;
+        }
+        head[tid] = y;
+        __syncthreads();
+        const float sum = block_sum_squares<128>(head, 128, FloatPost{});
+        const float scale = div_rn(1.0f, fmaxf(sqrt_rn(sum), 1e-6f));
+        *o = __fmul_rn(y, scale);
+    }
+    if (t0 + tn == rows) {
+        float *so = conv_state + (size_t)((slot0 + rows) % kStateSlots) * slot_stride + (size_t)ch * 3;
+        so[0] = s0;
+        so[1] = s1;
+        so[2] = s2;
     }
 }
 
@@ -641,6 +734,14 @@ void launch_deltanet_prep(float *qkv, long long ld, int beta_off, int alpha_off,
 {
     deltanet_prep_kernel<<<kQKV / 128 + 1, 128, 0, stream>>>(qkv, ld, beta_off, alpha_off, conv_state, slot_stride,
                                                              slot, rows, conv_w, ssm_a, ssm_dt, last_only ? 1 : 0);
+}
+
+void launch_deltanet_prep_rows(float *out, const float *qkv, long long ld, int beta_off, int alpha_off,
+                               float *conv_state, long long slot_stride, const uint32_t *slot, int rows,
+                               const float *conv_w, const float *ssm_a, const float *ssm_dt, hipStream_t stream)
+{
+    deltanet_prep_rows_kernel<<<dim3(kQKV / 128 + 1, (rows + kPrepRows - 1) / kPrepRows), 128, 0, stream>>>(
+        out, qkv, ld, beta_off, alpha_off, conv_state, slot_stride, slot, rows, conv_w, ssm_a, ssm_dt);
 }
 
 void launch_deltanet_state(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,

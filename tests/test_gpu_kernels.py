@@ -270,3 +270,35 @@ def test_wide_gemm_full_shapes_match_decode_kernels(hip, device, rows, width):
     for t0 in (0, 8, 120, 248):
         want = hip.gemm_q8_k_tiled(tiled, width, rows, xq[t0 * nb * 292:(t0 + 8) * nb * 292], 8).cpu().numpy()
         assert np.array_equal(bits(got[t0:t0 + 8]), bits(want)), (rows, width, t0)
+
+
+@pytest.mark.parametrize("rows,width", [(300, 5120), (40, 17408), (520, 6144)])
+def test_iq1m_wide_gemm_prefill_batches_bit_exact(hip, oracle, device, rows, width):
+    """IQ1_M prefill batches (9 tokens and more, 256 x 64 matrix-core tiles):
+    every token's row equals the oracle's one-token GEMV bit for bit, with a
+    row count that ends inside a wavefront's 32 rows and token counts that
+    end inside a 64-token tile."""
+    w = synth.matrix(IQ1_M, rows, width, seed=rows * 5 + width)
+    x = synth.activations(width, seed=rows + 2 * width, count=100)
+    q = oracle.quantize(x.reshape(-1))
+    nb = width // 256
+    wd = to_dev(w, device)
+    xq = hip.quantize_q8_k(to_dev(x, device))
+    want = oracle.gemm(IQ1_M, w, rows, q, 100)
+    for m in (9, 16, 33, 64, 100):
+        got = hip.gemm_q8_k(wd, IQ1_M, width, rows, xq[:m * nb * 292], m).cpu().numpy()
+        assert np.array_equal(bits(got), bits(want[:m])), "M=%d" % m
+
+
+@pytest.mark.parametrize("rows,width", [(34816, 5120), (5120, 17408)])
+def test_iq1m_wide_gemm_full_shapes_match_decode_kernel(hip, device, rows, width):
+    m = 256
+    w = synth.matrix(IQ1_M, rows, width, seed=rows + 11)
+    wd = to_dev(w, device)
+    x = synth.activations(width, seed=width + 13, count=m)
+    xq = hip.quantize_q8_k(to_dev(x, device))
+    got = hip.gemm_q8_k(wd, IQ1_M, width, rows, xq, m).cpu().numpy()
+    nb = width // 256
+    for t0 in (0, 8, 120, 248):
+        want = hip.gemm_q8_k(wd, IQ1_M, width, rows, xq[t0 * nb * 292:(t0 + 8) * nb * 292], 8).cpu().numpy()
+        assert np.array_equal(bits(got[t0:t0 + 8]), bits(want)), (rows, width, t0)
