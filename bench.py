@@ -429,7 +429,8 @@ def run_decode(torch, args):
     # every run decodes `decode_tokens` tokens; the timed window is transactions
     # [warmup, warmup + steps) (default: all after the warm-up)
     window = args.steps
-    context = args.prompt + max(decode_tokens, (warmup + (window or 0)) * args.draft) + 4 * args.draft + 16
+    context = (args.prompt + max(decode_tokens, (warmup + (window or 0)) * args.draft) + 4 * args.draft +
+               args.plain_tokens + 16)
     t0 = time.perf_counter()
     model = Model.open(path, context)
     t_open = time.perf_counter() - t0

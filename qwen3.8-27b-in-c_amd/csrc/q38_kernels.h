@@ -33,6 +33,12 @@ bool launch_gemm_q4k_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, floa
 /* same product, 32 weight rows per wavefront (v_mfma_f32_32x32x16_f16) */
 bool launch_gemm_q4k_t32(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                          uint32_t nb, hipStream_t stream);
+/* q38_mm16.hip: the same product for 2..4 tokens on 20-block matrices of
+ * kMm16MinRows .. 36864 rows, 16 rows per wavefront
+ * (v_mfma_f32_16x16x32_f16); false for unsupported shapes */
+constexpr uint32_t kMm16MinRows = 32768;
+bool launch_gemm_q4k_mm16(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                          uint32_t nb, hipStream_t stream);
 /* q38_wide.hip: the same product for any token count (the prefill batch),
  * 64 rows x 64 tokens per workgroup; false for unsupported shapes.
  * launch_gemm_q4k_tiled takes it from kWideMinTokens tokens on. */

@@ -424,6 +424,10 @@ bool launch_gemm_q4k_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, floa
     if (!rows || ldy < rows || m < 2) return false;
     /* prefill batches: the 64 x 64 matrix-core tiles of q38_wide.hip */
     if (m >= kWideMinTokens) return launch_gemm_q4k_wide((uint32_t)m, w_tiled, x, y, ldy, rows, nb, stream);
+    /* 2..4 tokens on the widest 20-block matrices (FFN gate|up): 16 rows
+     * per wavefront, weights streamed through LDS (q38_mm16.hip) */
+    if (m <= 4 && nb == 20 && rows >= kMm16MinRows && launch_gemm_q4k_mm16(m, w_tiled, x, y, ldy, rows, nb, stream))
+        return true;
     /* 4096 rows or more: 32 rows per wavefront (measured faster there; the
      * 16-row kernel keeps the small matrices) */
     if (rows >= 4096) return launch_gemm_q4k_t32(m, w_tiled, x, y, ldy, rows, nb, stream);

@@ -190,8 +190,13 @@ def test_tiled_repack_and_gemm_bit_exact(hip, oracle, device, rows, width):
 def test_tiled_gemm_full_shape_matches_row_major(hip, device, m):
     """34816x5120 (fused gate|up) and 5120x17408 (down): tiled = row-major kernels;
     24584x5120 ends on an unpaired 16-row tile at a size where the 32-row
-    kernel's workgroups run in more than one wave over the chip."""
-    for rows, width in ((34816, 5120), (5120, 17408), (24584, 5120)):
+    kernel's workgroups run in more than one wave over the chip; 33000 and
+    36864 rows are a ragged last tile and the largest matrix of the 16-row
+    streaming kernel (q38_mm16.hip, 2..4 tokens from 32768 rows on)."""
+    shapes = ((34816, 5120), (5120, 17408), (24584, 5120))
+    if m <= 4:
+        shapes += ((33000, 5120), (36864, 5120))
+    for rows, width in shapes:
         w = synth.matrix(Q4_K, rows, width, seed=m + rows)
         wd = to_dev(w, device)
         x = synth.activations(width, seed=m * 7 + width, count=m)
