@@ -252,7 +252,8 @@ def _trace_rows(directory):
             rows.extend(csv.DictReader(f))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     for r in rows:
-        r["short"] = re.sub(r"\(.*$", "", r["Kernel_Name"].replace("void ", "").replace("q38::", ""))
+        name = r["Kernel_Name"].replace("void ", "").replace("q38::", "").replace("(anonymous namespace)::", "")
+        r["short"] = re.sub(r"\(.*$", "", name)
         r["groups"] = int(r["Grid_Size_X"]) // max(int(r["Workgroup_Size_X"]), 1)
         r["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
     return rows
@@ -262,15 +263,15 @@ def trace_summary(directory, transactions=0):
     """calls / avg / min / max ns per (kernel, grid) of a rocprofv3 kernel
     trace.  With `transactions` > 0 the trace is that of the decode workload
     and only its transactions are summarised: the dispatches after the
-    prefill's last 8-token GEMM (Q4_K tiled or IQ1_M) and before the first
+    prefill's last GEMM (a prompt-batch or 8-token Q4_K / IQ1_M GEMM) and before the first
     kernel of the roofline run that follows (its weight repack or its
     activation quantisation, which the model never launches), reported per
     transaction."""
     rows = _trace_rows(directory)
     if transactions:
         names = [r["short"] for r in rows]
-        first = max(i for i, n in enumerate(names)
-                    if n.startswith("gemm_q4k_tiled<8") or n.startswith("gemm_iq1m_mfma<8")) + 1
+        prefill = ("gemm_q4k_wide", "gemm_iq1m_wide", "gemm_q4k_tiled<8", "gemm_q4k_t32<8", "gemm_iq1m_mfma<8")
+        first = max(i for i, n in enumerate(names) if n.startswith(prefill)) + 1
         last = min(i for i, n in enumerate(names)
                    if i >= first and (n.startswith("repack_q4k_tiles") or n.startswith("quantize_q8k_kernel")))
         rows = rows[first:last]
