@@ -108,6 +108,23 @@ int q38hip_argmax(uint32_t *index_out, const float *values, uint32_t count,
 int q38hip_argmax_noalloc(uint32_t *index_out, const float *values, uint32_t count,
                           uint32_t rows, void *stream);
 
+/* Device form of q38_sample (src/qwen38/qwen38_sampler.c:51-119): the
+ * token drawn from `logits` (vocabulary_size floats, device memory) into
+ * *token (a device word).  The sampler's fields
+ * (include/qwen38/qwen38_sampler.h:10-18) come as arguments: *state is the
+ * xorshift64* state in HOST memory, read at the call and advanced before it
+ * returns exactly as q38_sample advances it (one step when temperature > 0
+ * and top_k > 1, none otherwise); presence, when not NULL, is presence_size
+ * bytes of DEVICE memory (nonzero = token observed).  Token and state are
+ * those of q38_sample on the same logits, bit for bit, NaN and infinite
+ * logits included.  Limits: vocabulary_size <= 2^20 and, when sampling,
+ * min(top_k, vocabulary_size) <= 1024; beyond them the call returns 0 with
+ * a message.  Working memory is a per-device buffer (2 MiB, allocated on
+ * the first call on a device): calls that overlap on one device race. */
+int q38hip_sample(uint32_t *token, uint64_t *state, const float *logits, uint32_t vocabulary_size,
+                  float temperature, float top_p, float presence_penalty, uint32_t top_k,
+                  const uint8_t *presence, uint32_t presence_size, void *stream);
+
 /* Greedy acceptance of a verify batch (src/qwen38/qwen38_model.c:1662-1702):
  * targets[rows] are the per-row argmaxes, drafts[rows] the draft ids.
  * result[0] = consumed, result[1] = matched, result[2] = next,

@@ -54,6 +54,29 @@ int q38_model_speculative_greedy(Q38Model *model, uint32_t token_id, uint32_t st
 /* qwen38_model.h:45-46: hidden state after the first layer_count blocks */
 int q38_model_forward_token_layers(Q38Model *model, uint32_t token_id, uint32_t layer_count, float *hidden_out);
 
+/* Library extension (no counterpart in the reference): q38_sample
+ * (src/qwen38/qwen38_sampler.c:51-119) on the device over the logits that
+ * the model's last forward_token / prefill / mtp_forward /
+ * speculative_greedy call returned (their copy in HBM; 0 when the last call
+ * returned none or failed).  The arguments are the Q38Sampler fields
+ * (include/qwen38/qwen38_sampler.h:10-18): *state is the xorshift64* state,
+ * advanced as q38_sample advances it; presence is the caller's HOST array
+ * of presence_size bytes, as the reference CLI keeps it, copied to the
+ * device when presence_penalty is nonzero.  *token and *state are those of
+ * q38_sample on the same logits, bit for bit.  Sampling calls take at most
+ * 1024 candidates (min(top_k, vocabulary)); beyond that the call returns 0. */
+int q38hip_model_sample(Q38Model *model, uint64_t *state, float temperature, float top_p, float presence_penalty,
+                        uint32_t top_k, const uint8_t *presence, uint32_t presence_size, uint32_t *token);
+
+/* Library extension: q38_model_forward_token(token_id) followed by
+ * q38hip_model_sample, without downloading the logits (the reference CLI's
+ * generation step, src/cli/qwen38_main.c:545-553 and the forward that
+ * follows it, in one call).  The logits stay in HBM, where a following
+ * q38hip_model_sample can sample them again. */
+int q38hip_model_forward_sample(Q38Model *model, uint32_t token_id, uint64_t *state, float temperature, float top_p,
+                                float presence_penalty, uint32_t top_k, const uint8_t *presence,
+                                uint32_t presence_size, uint32_t *next_token);
+
 /* qwen38_model.h:48-50 */
 uint32_t q38_model_vocab_size(const Q38Model *model);
 uint32_t q38_model_position(const Q38Model *model);

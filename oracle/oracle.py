@@ -32,6 +32,20 @@ def _ptr(array):
     return ctypes.c_void_p(array.ctypes.data)
 
 
+class Q38Sampler(ctypes.Structure):
+    """include/qwen38/qwen38_sampler.h:10-18"""
+    _fields_ = [("state", ctypes.c_uint64), ("temperature", ctypes.c_float), ("top_p", ctypes.c_float),
+                ("presence_penalty", ctypes.c_float), ("top_k", ctypes.c_uint32),
+                ("presence", ctypes.c_void_p), ("presence_size", ctypes.c_uint32)]
+
+
+def _sample_args(logits, presence):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    if presence is not None:
+        presence = np.ascontiguousarray(presence, dtype=np.uint8)
+    return logits, presence
+
+
 class GGUFString(ctypes.Structure):
     _fields_ = [("data", ctypes.c_char_p), ("length", ctypes.c_uint64)]
 
@@ -79,6 +93,9 @@ class Oracle:
                                    _u32p, _u32p, ctypes.c_void_p]
         lib.orc_iq1m_grid_entry.argtypes = [ctypes.c_uint32, ctypes.c_void_p]
         lib.orc_attention_decode.argtypes = [ctypes.c_void_p] * 8 + [ctypes.c_uint32]
+        lib.orc_sample.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64), ctypes.c_void_p,
+                                   ctypes.c_uint32, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                   ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint32]
         self.lib = lib
 
     def f16_to_f32(self, bits):
@@ -129,6 +146,17 @@ class Oracle:
                                        ctypes.byref(matched), ctypes.byref(nxt), _ptr(accepted))
         return int(consumed), int(matched.value), int(nxt.value), accepted[:consumed].copy()
 
+    def sample(self, logits, state, temperature, top_p, presence_penalty, top_k, presence=None):
+        """orc_sample: (token, state after the call)."""
+        logits, presence = _sample_args(logits, presence)
+        token = np.zeros(1, dtype=np.uint32)
+        st = ctypes.c_uint64(state)
+        if not self.lib.orc_sample(_ptr(token), ctypes.byref(st), _ptr(logits), logits.size, temperature, top_p,
+                                   presence_penalty, top_k, None if presence is None else _ptr(presence),
+                                   0 if presence is None else presence.size):
+            raise ValueError("orc_sample refused its arguments")
+        return int(token[0]), st.value
+
     def grid_entry(self, index):
         out = np.zeros(8, dtype=np.int8)
         self.lib.orc_iq1m_grid_entry(index, _ptr(out))
@@ -162,6 +190,8 @@ class Reference:
         lib.q38_tensor_row_f32.argtypes = [ctypes.c_void_p, ctypes.POINTER(GGUFTensor), ctypes.c_uint64]
         lib.q38ref_full_core.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_uint32, ctypes.c_void_p,
                                                                   ctypes.c_void_p, ctypes.c_uint32]
+        lib.q38_sampler_init.argtypes = [ctypes.POINTER(Q38Sampler), ctypes.c_uint64]
+        lib.q38_sample.argtypes = [ctypes.POINTER(Q38Sampler), ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p]
         self.lib = lib
 
     @staticmethod
@@ -201,6 +231,23 @@ class Reference:
             raise ValueError("row decode failed")
         return out
 
+
+    def sampler_init(self, seed):
+        """q38_sampler_init (qwen38_sampler.c:22-32) -> the Q38Sampler fields."""
+        sampler = Q38Sampler()
+        self.lib.q38_sampler_init(ctypes.byref(sampler), seed)
+        return {f: getattr(sampler, f) for f in ("state", "temperature", "top_p", "presence_penalty", "top_k")}
+
+    def sample(self, logits, state, temperature, top_p, presence_penalty, top_k, presence=None):
+        """q38_sample (qwen38_sampler.c:51-119): (token, state after the call)."""
+        logits, presence = _sample_args(logits, presence)
+        sampler = Q38Sampler(state, temperature, top_p, presence_penalty, top_k,
+                             None if presence is None else presence.ctypes.data,
+                             0 if presence is None else presence.size)
+        token = np.zeros(1, dtype=np.uint32)
+        if not self.lib.q38_sample(ctypes.byref(sampler), _ptr(logits), logits.size, _ptr(token)):
+            raise ValueError("q38_sample refused its arguments")
+        return int(token[0]), sampler.state
 
     def full_core(self, q_and_gate, key, value, key_cache, value_cache, q_norm, k_norm, position):
         """The reference's static q38_full_core (qwen38_model.c:816-885)

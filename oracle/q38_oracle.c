@@ -7,7 +7,9 @@
  */
 #include "q38_oracle.h"
 
+#include <float.h>
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "../qwen3.8-27b-in-c_amd/csrc/q38_iq1m_grid.inc"
@@ -436,4 +438,123 @@ void orc_attention_decode(float *attention, const float *q_and_gate,
         const float *g = gate + h * 256;
         for (int i = 0; i < 256; ++i) out[i] *= sigmoidf_ref(g[i]);
     }
+}
+
+/* ---- token sampler ------------------------------------------------------ */
+
+typedef struct {
+    uint32_t id;
+    float logit;
+} OrcCandidate;
+
+/* higher logit first, lower id among equal logits (no NaN reaches here) */
+static int candidate_order(const void *pa, const void *pb)
+{
+    const OrcCandidate *a = (const OrcCandidate *)pa, *b = (const OrcCandidate *)pb;
+    if (a->logit != b->logit) return a->logit > b->logit ? -1 : 1;
+    return a->id < b->id ? -1 : (a->id > b->id);
+}
+
+/* qwen38_sampler.c:38-46: the presence penalty is one fp32 subtraction */
+static float penalised(const float *logits, const uint8_t *presence,
+                       uint32_t presence_size, float penalty, uint32_t id)
+{
+    if (penalty == 0.0f || !presence || id >= presence_size || !presence[id])
+        return logits[id];
+    return logits[id] - penalty;
+}
+
+/* Restated by what it selects rather than by the reference's loops:
+ *  - greedy (temperature <= 0 or top_k <= 1, :55): the first maximum of the
+ *    adjusted logits, NaN never winning, except that a NaN at index 0 makes
+ *    every comparison of the reference's strict > scan false (:57-60) and
+ *    index 0 is kept;
+ *  - sampling: the count = min(top_k, vocab) best adjusted logits that lie
+ *    above -FLT_MAX, ordered by (logit descending, id ascending) and padded
+ *    with (id 0, -FLT_MAX) -- the list the insertion of :74-83 leaves, found
+ *    here by sorting.  With a NaN among the logits no such order exists and
+ *    the list depends on where the NaN falls in the insertion sequence, so
+ *    that sequence is stated as it is (a NaN fails every comparison and
+ *    enters the last slot);
+ *  - then :84-115 in fp32, sequential sums, expf of the C library, one
+ *    xorshift64* draw (:12-20) as (double)(r >> 11) * 2^-53. */
+int orc_sample(uint32_t *token, uint64_t *state, const float *logits,
+               uint32_t vocab, float temperature, float top_p,
+               float penalty, uint32_t top_k, const uint8_t *presence,
+               uint32_t presence_size)
+{
+    if (!token || !state || !logits || vocab == 0) return 0;
+    if (temperature <= 0.0f || top_k <= 1) {
+        uint32_t best = 0;
+        float best_value = penalised(logits, presence, presence_size, penalty, 0);
+        if (!isnan(best_value)) {
+            for (uint32_t id = 1; id < vocab; ++id) {
+                const float v = penalised(logits, presence, presence_size, penalty, id);
+                if (!isnan(v) && v > best_value) { best = id; best_value = v; }
+            }
+        }
+        *token = best;
+        return 1;
+    }
+    const uint32_t count = top_k < vocab ? top_k : vocab;
+    OrcCandidate *all = (OrcCandidate *)malloc((size_t)vocab * sizeof(*all));
+    float *prob = (float *)malloc((size_t)count * sizeof(float));
+    if (!all || !prob) { free(all); free(prob); return 0; }
+    int any_nan = 0;
+    uint32_t eligible = 0;
+    for (uint32_t id = 0; id < vocab; ++id) {
+        const float v = penalised(logits, presence, presence_size, penalty, id);
+        any_nan |= isnan(v);
+        if (v > -FLT_MAX) { all[eligible].id = id; all[eligible].logit = v; ++eligible; }
+    }
+    OrcCandidate *list = all;   /* count entries */
+    if (any_nan) {
+        list = (OrcCandidate *)malloc((size_t)count * sizeof(*list));
+        if (!list) { free(all); free(prob); return 0; }
+        for (uint32_t i = 0; i < count; ++i) { list[i].id = 0; list[i].logit = -FLT_MAX; }
+        for (uint32_t id = 0; id < vocab; ++id) {
+            const float v = penalised(logits, presence, presence_size, penalty, id);
+            /* a NaN on either side fails <=, so it enters */
+            if (v <= list[count - 1].logit) continue;
+            uint32_t at = count - 1;
+            for (; at > 0 && v > list[at - 1].logit; --at) list[at] = list[at - 1];
+            list[at].id = id;
+            list[at].logit = v;
+        }
+    } else {
+        qsort(all, eligible, sizeof(*all), candidate_order);
+        for (uint32_t i = eligible; i < count; ++i) { all[i].id = 0; all[i].logit = -FLT_MAX; }
+    }
+    float total = 0.0f;
+    for (uint32_t i = 0; i < count; ++i) {
+        prob[i] = expf((list[i].logit - list[0].logit) / temperature);
+        total += prob[i];
+    }
+    const float keep = top_p > 0.0f && top_p < 1.0f ? top_p : 1.0f;
+    uint32_t retained = count;
+    float cumulative = 0.0f;
+    for (uint32_t i = 0; i < count; ++i) {
+        cumulative += prob[i] / total;
+        if (cumulative >= keep) { retained = i + 1; break; }
+    }
+    float retained_total = 0.0f;
+    for (uint32_t i = 0; i < retained; ++i) retained_total += prob[i];
+    uint64_t r = *state;
+    r ^= r >> 12;
+    r ^= r << 25;
+    r ^= r >> 27;
+    *state = r;
+    const double unit = (double)((r * UINT64_C(2685821657736338717)) >> 11) * 0x1.0p-53;
+    const float target = (float)unit * retained_total;
+    uint32_t selected = list[retained - 1].id;
+    float running = 0.0f;
+    for (uint32_t i = 0; i < retained; ++i) {
+        running += prob[i];
+        if (target < running) { selected = list[i].id; break; }
+    }
+    if (list != all) free(list);
+    free(all);
+    free(prob);
+    *token = selected;
+    return 1;
 }

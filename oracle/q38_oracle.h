@@ -72,6 +72,15 @@ void orc_attention_decode(float *attention, const float *q_and_gate,
                           const float *q_norm, const float *k_norm,
                           uint32_t position);
 
+/* Token sampler (src/qwen38/qwen38_sampler.c:51-119): the token drawn from
+ * `logits` [vocab] with the Q38Sampler fields as arguments; *state is the
+ * xorshift64* state, advanced by one step on the sampling path.  presence
+ * may be NULL.  Returns 0 on bad arguments, as the reference does. */
+int orc_sample(uint32_t *token, uint64_t *state, const float *logits,
+               uint32_t vocab, float temperature, float top_p,
+               float presence_penalty, uint32_t top_k,
+               const uint8_t *presence, uint32_t presence_size);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,13 +31,15 @@ int fail(const char *message)
 }
 
 /* Per-device constant state: the IQ1_M codebook as 2048 x 8 int8 values
- * (the form the GEMM kernel stages into LDS), and a growable argmax
- * partials buffer. */
+ * (the form the GEMM kernel stages into LDS), a growable argmax
+ * partials buffer and the sampler's candidate lists (allocated once, at the
+ * largest size the sampler accepts). */
 struct DeviceState {
     int8_t *grid = nullptr;
     float *argmax_values = nullptr;
     uint32_t *argmax_index = nullptr;
     size_t argmax_capacity = 0;
+    void *sample_scratch = nullptr;
 };
 
 std::mutex g_mutex;
@@ -288,6 +290,29 @@ int q38hip_argmax(uint32_t *index_out, const float *values, uint32_t count, uint
     }
     q38::launch_argmax(values, count, rows, state->argmax_values, state->argmax_index, index_out,
                        static_cast<hipStream_t>(stream));
+    return 1;
+}
+
+int q38hip_sample(uint32_t *token, uint64_t *state, const float *logits, uint32_t vocabulary_size,
+                  float temperature, float top_p, float presence_penalty, uint32_t top_k,
+                  const uint8_t *presence, uint32_t presence_size, void *stream)
+{
+    if (!token || !state || !logits) return fail("bad sample arguments");
+    if (const char *why = q38::check_sample(vocabulary_size, temperature, top_k)) return fail(why);
+    DeviceState *dev = device_state();
+    if (!dev) return fail("device initialisation failed");
+    {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        if (!dev->sample_scratch &&
+            hipMalloc(&dev->sample_scratch, q38::sample_scratch_bytes(q38::kMaxSampleVocab, q38::kMaxSampleTopK)) !=
+                hipSuccess) {
+            dev->sample_scratch = nullptr;
+            return fail("sampler scratch allocation failed");
+        }
+    }
+    if (!q38::launch_sample(token, state, logits, vocabulary_size, presence, presence ? presence_size : 0, temperature,
+                            top_p, presence_penalty, top_k, dev->sample_scratch, static_cast<hipStream_t>(stream)))
+        return fail("sampler launch failed");
     return 1;
 }
 

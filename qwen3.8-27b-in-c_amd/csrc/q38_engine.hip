@@ -372,13 +372,21 @@ struct Q38Model {
     uint8_t *q8k = nullptr;
     /* params[0] = position of row 0 of the current step, params[1 + r] = slot of recurrent layer r */
     uint32_t *tokens = nullptr, *params = nullptr, *targets = nullptr, *drafts = nullptr, *accept = nullptr;
-    uint32_t *words = nullptr;   /* one allocation: drafts [0, 16), targets [16, 32), accept [32, 48) */
+    /* one allocation: drafts [0, 16), targets [16, 32), accept [32, 48),
+     * sampled token [48] */
+    uint32_t *words = nullptr, *sampled = nullptr;
     float *argmax_pv = nullptr;
     uint32_t *argmax_pi = nullptr;
+    /* device sampling: the row of the logits the last call returned (valid
+     * until the next call), a device copy of the sampler's presence bytes
+     * and the sampler's candidate lists */
+    const float *last_logits = nullptr;
+    uint8_t *presence = nullptr, *sample_scratch = nullptr;
     /* host side */
     float *host_logits = nullptr;
     uint32_t *host_words = nullptr;
     uint32_t *host_params = nullptr;   /* pinned staging of the device parameter blocks */
+    uint32_t *host_sampled = nullptr;  /* pinned word of a sampled token */
     float query_scale = 0.0f;
     bool pending_branch = false;   /* m->branch holds an FFN output not yet added to m->hidden */
     /* instantiated HIP graphs of the step sequences, by key; `seen` marks
@@ -642,6 +650,8 @@ void release(Q38Model *m)
     uint32_t **ubufs[] = {&m->tokens, &m->params, &m->words, &m->argmax_pi};
     for (uint32_t **p : ubufs) dfree(*p);
     dfree(m->q8k);
+    dfree(m->presence);
+    dfree(m->sample_scratch);
     if (m->weights) (void)hipFree(m->weights);
     if (m->mtp_weights) (void)hipFree(m->mtp_weights);
     if (m->tiled_weights) (void)hipFree(m->tiled_weights);
@@ -649,6 +659,7 @@ void release(Q38Model *m)
     if (m->host_logits) (void)hipHostFree(m->host_logits);
     if (m->host_words) (void)hipHostFree(m->host_words);
     if (m->host_params) (void)hipHostFree(m->host_params);
+    if (m->host_sampled) (void)hipHostFree(m->host_sampled);
     for (auto &g : m->graphs) (void)hipGraphExecDestroy(g.second);
     if (m->copy_stream) (void)hipStreamSynchronize(m->copy_stream);
     if (m->logits_ready) (void)hipEventDestroy(m->logits_ready);
@@ -675,9 +686,13 @@ bool allocate_state(Q38Model *m)
               dalloc(&m->scores, (size_t)B * kAttnHeads * ctx) &&
               dalloc(&m->logits, (size_t)kBatch * kVocab) && dalloc(&m->target_norm, (size_t)B * kHidden) &&
               dalloc(&m->q8k, (size_t)B * (kFFN / 256) * kQ8KBytes) && dalloc(&m->tokens, B) &&
-              dalloc(&m->params, (size_t)kParamSets * kParamWords) && dalloc(&m->words, 48) &&
+              dalloc(&m->params, (size_t)kParamSets * kParamWords) && dalloc(&m->words, 64) &&
               dalloc(&m->argmax_pv, (size_t)kBatch * q38::argmax_chunks(kVocab)) &&
               dalloc(&m->argmax_pi, (size_t)kBatch * q38::argmax_chunks(kVocab)) &&
+              dalloc(&m->presence, kVocab) &&
+              dalloc(&m->sample_scratch, q38::sample_scratch_bytes(kVocab, q38::kMaxSampleTopK)) &&
+              hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_sampled), 16 * sizeof(uint32_t)),
+                     "pinned token") &&
               hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_logits), kVocab * sizeof(float)),
                      "pinned logits") &&
               hip_ok(hipHostMalloc(reinterpret_cast<void **>(&m->host_words), ((size_t)B + 128) * sizeof(uint32_t)),
@@ -688,6 +703,7 @@ bool allocate_state(Q38Model *m)
     m->drafts = m->words;
     m->targets = m->words + 16;
     m->accept = m->words + 32;
+    m->sampled = m->words + 48;
     std::vector<float> table((size_t)ctx * 64);
     q38::rope_table_host(table.data(), ctx);
     m->query_scale = 1.0f / sqrtf(128.0f);
@@ -1165,6 +1181,7 @@ bool upload_tokens(Q38Model *m, const uint32_t *tokens, uint32_t count, uint32_t
 
 bool logits_to_host(Q38Model *m, const float *device_row)
 {
+    m->last_logits = device_row;
     return hip_ok(hipMemcpyAsync(m->host_logits, device_row, kVocab * sizeof(float), hipMemcpyDeviceToHost,
                                  m->stream),
                   "logits download") &&
@@ -1313,6 +1330,74 @@ bool speculative_chunked(Q38Model *m, uint32_t token, uint32_t stop_token, uint3
 
 }  // namespace
 
+namespace {
+
+/* q38_model_forward_token without the logits download: the logits of the
+ * token are in m->logits row 0 when it returns true */
+bool forward_device(Q38Model *m, uint32_t token)
+{
+    m->last_logits = nullptr;
+    write_params(m, kParamTarget, m->position);
+    if (!upload_tokens(m, &token, 1, m->tokens) || !flush_params(m)) return false;
+    const Step s = step_of(m, kParamTarget, m->tokens);
+    const bool mtp = m->mtp_enabled;
+    const bool ok = run_step(m, graph_key(kGraphTarget, 1, mtp), [&] {
+        /* q38_model_forward_token (qwen38_model.c:1494-1517): the normed final
+         * hidden becomes the MTP input when MTP is enabled */
+        return target_rows(m, s, 1, 1) &&
+               (!mtp || hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm, kHidden * sizeof(float),
+                                              hipMemcpyDeviceToDevice, m->stream), "mtp hidden"));
+    });
+    if (!ok) return false;
+    advance_slots(m, 1);
+    ++m->position;
+    m->last_logits = m->logits;
+    return true;
+}
+
+/* the Q38Sampler fields (include/qwen38/qwen38_sampler.h:10-18) */
+struct SampleArgs {
+    uint64_t *state;
+    float temperature, top_p, presence_penalty;
+    uint32_t top_k;
+    const uint8_t *presence;
+    uint32_t presence_size;
+};
+
+/* q38_sample (qwen38_sampler.c:51-119) over the device logits row `row`;
+ * the caller's host presence bytes are copied to the device when the
+ * penalty applies (tokens at or above presence_size are never penalised,
+ * nor are ids beyond the vocabulary ever read) */
+bool sample_row(Q38Model *m, const float *row, const SampleArgs &a, uint32_t *token)
+{
+    if (const char *why = q38::check_sample(kVocab, a.temperature, a.top_k)) {
+        fprintf(stderr, "qwen38: sampler: %s\n", why);
+        return false;
+    }
+    const uint8_t *presence = nullptr;
+    uint32_t presence_size = 0;
+    if (a.presence_penalty != 0.0f && a.presence && a.presence_size) {
+        presence_size = std::min(a.presence_size, kVocab);
+        if (!hip_ok(hipMemcpyAsync(m->presence, a.presence, presence_size, hipMemcpyHostToDevice, m->stream),
+                    "presence upload"))
+            return false;
+        presence = m->presence;
+    }
+    if (!q38::launch_sample(m->sampled, a.state, row, kVocab, presence, presence_size, a.temperature, a.top_p,
+                            a.presence_penalty, a.top_k, m->sample_scratch, m->stream)) {
+        fprintf(stderr, "qwen38: sampler launch failed\n");
+        return false;
+    }
+    if (!hip_ok(hipMemcpyAsync(m->host_sampled, m->sampled, sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream),
+                "token download") ||
+        !hip_ok(hipStreamSynchronize(m->stream), "token download"))
+        return false;
+    *token = m->host_sampled[0];
+    return true;
+}
+
+}  // namespace
+
 extern "C" {
 
 Q38Model *q38_model_open_gguf(const char *path, uint32_t context_length)
@@ -1379,34 +1464,43 @@ void q38_model_reset(Q38Model *m)
     (void)clear_state(m);
     m->position = 0;
     m->mtp_position = 0;
+    m->last_logits = nullptr;
 }
 
 int q38_model_forward_token(Q38Model *m, uint32_t token, const float **logits)
 {
     begin_call();
     if (!m || !logits || token >= kVocab || m->position >= m->context_length) return 0;
-    write_params(m, kParamTarget, m->position);
-    if (!upload_tokens(m, &token, 1, m->tokens) || !flush_params(m)) return 0;
-    const Step s = step_of(m, kParamTarget, m->tokens);
-    const bool mtp = m->mtp_enabled;
-    const bool ok = run_step(m, graph_key(kGraphTarget, 1, mtp), [&] {
-        /* q38_model_forward_token (qwen38_model.c:1494-1517): the normed final
-         * hidden becomes the MTP input when MTP is enabled */
-        return target_rows(m, s, 1, 1) &&
-               (!mtp || hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm, kHidden * sizeof(float),
-                                              hipMemcpyDeviceToDevice, m->stream), "mtp hidden"));
-    });
-    if (!ok || !logits_to_host(m, m->logits)) return 0;
-    advance_slots(m, 1);
-    ++m->position;
+    if (!forward_device(m, token) || !logits_to_host(m, m->logits)) return 0;
     *logits = m->host_logits;
     return 1;
+}
+
+int q38hip_model_sample(Q38Model *m, uint64_t *state, float temperature, float top_p, float presence_penalty,
+                        uint32_t top_k, const uint8_t *presence, uint32_t presence_size, uint32_t *token)
+{
+    begin_call();
+    if (!m || !state || !token || !m->last_logits) return 0;
+    return sample_row(m, m->last_logits, {state, temperature, top_p, presence_penalty, top_k, presence, presence_size},
+                      token) ? 1 : 0;
+}
+
+int q38hip_model_forward_sample(Q38Model *m, uint32_t token_id, uint64_t *state, float temperature, float top_p,
+                                float presence_penalty, uint32_t top_k, const uint8_t *presence,
+                                uint32_t presence_size, uint32_t *next_token)
+{
+    begin_call();
+    if (!m || !state || !next_token || token_id >= kVocab || m->position >= m->context_length) return 0;
+    if (!forward_device(m, token_id)) return 0;
+    return sample_row(m, m->logits, {state, temperature, top_p, presence_penalty, top_k, presence, presence_size},
+                      next_token) ? 1 : 0;
 }
 
 int q38_model_forward_token_layers(Q38Model *m, uint32_t token, uint32_t layer_count, float *hidden_out)
 {
     begin_call();
     if (!m || !hidden_out || token >= kVocab || layer_count > kLayers || m->position >= m->context_length) return 0;
+    m->last_logits = nullptr;
     write_params(m, kParamTarget, m->position);
     if (!upload_tokens(m, &token, 1, m->tokens) || !flush_params(m)) return 0;
     const Step s = step_of(m, kParamTarget, m->tokens);
@@ -1431,6 +1525,7 @@ int q38_model_prefill(Q38Model *m, const uint32_t *tokens, uint32_t count, const
     if (!m || !tokens || !count || !logits || count > m->context_length - m->position) return 0;
     for (uint32_t i = 0; i < count; ++i)
         if (tokens[i] >= kVocab) return 0;
+    m->last_logits = nullptr;
     const uint32_t base = m->position;
     /* batches of up to prefill_rows tokens through all blocks
      * (q38_model_prefill, qwen38_model.c:1519-1560): every row's arithmetic
@@ -1471,6 +1566,7 @@ int q38_model_mtp_forward(Q38Model *m, uint32_t token, const float **logits)
 {
     begin_call();
     if (!m || !m->mtp_enabled || !logits || token >= kVocab || m->mtp_position >= m->context_length) return 0;
+    m->last_logits = nullptr;
     write_params(m, kParamDraft0, m->mtp_position);
     if (!upload_tokens(m, &token, 1, m->drafts) || !flush_params(m)) return 0;
     const Step s = step_of(m, kParamDraft0, m->drafts);
@@ -1501,11 +1597,13 @@ int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_toke
         draft_count == 0 || m->position != m->mtp_position || draft_count > m->context_length - m->position)
         return 0;
     const uint32_t k = draft_count;
+    m->last_logits = nullptr;
     if (!checkpoint(m)) return 0;
     if (k > kBatch) {
         std::vector<uint32_t> accepted;
         const float *row = nullptr;
         if (!speculative_chunked(m, token, stop_token, k, &accepted, &row) || !logits_to_host(m, row)) {
+            m->last_logits = nullptr;
             restore_target(m);
             (void)restore_mtp(m);
             (void)hipStreamSynchronize(m->stream);
@@ -1600,6 +1698,7 @@ int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_toke
         return 0;
     }
     m->mtp_position = m->ck_mtp_position + consumed;
+    m->last_logits = m->logits + (size_t)(consumed - 1) * kVocab;
     for (uint32_t i = 0; i < consumed; ++i) accepted_tokens[i] = accepted[i];
     *accepted_count = consumed;
     *next_logits = m->host_logits;

@@ -60,6 +60,24 @@ void launch_argmax(const float *values, uint32_t count, uint32_t rows, float *pv
 void launch_accept(uint32_t *result, const uint32_t *targets, const uint32_t *drafts, uint32_t rows,
                    hipStream_t stream);
 
+/* q38_sample.hip: q38_sample (qwen38_sampler.c:51-119) on a device logits
+ * row; *token_out is a device word written on `stream`.  *state is the
+ * caller's xorshift64* state in host memory: a sampling call (temperature
+ * > 0 and top_k > 1) draws once from it, and launch_sample advances it as
+ * q38_sample does.  presence is a device byte per token or null.
+ * check_sample names what a call exceeds (at most kMaxSampleTopK
+ * candidates, kMaxSampleVocab logits), or null; launch_sample returns false
+ * for such calls.  `scratch` holds sample_scratch_bytes(vocab, top_k)
+ * bytes. */
+constexpr uint32_t kMaxSampleTopK = 1024;
+constexpr uint32_t kMaxSampleVocab = 1u << 20;
+constexpr uint32_t kMaxSampleChunks = 256;
+size_t sample_scratch_bytes(uint32_t vocab, uint32_t top_k);
+const char *check_sample(uint32_t vocab, float temperature, uint32_t top_k);
+bool launch_sample(uint32_t *token_out, uint64_t *state, const float *logits, uint32_t vocab, const uint8_t *presence,
+                   uint32_t presence_size, float temperature, float top_p, float presence_penalty, uint32_t top_k,
+                   void *scratch, hipStream_t stream);
+
 /* q38_model.hip.  Rows of a batch are contiguous; q_out receives Q8_K blocks. */
 void launch_norm_quant(float *norm_out, long long norm_stride, uint8_t *q_out, int q_stride_blocks, float *hidden,
                        long long in_stride, const float *branch, const float *weight, int rows, hipStream_t stream);

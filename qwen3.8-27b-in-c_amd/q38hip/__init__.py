@@ -50,11 +50,12 @@ def make_tensor(data_ptr, qtype, width, rows, nbytes=0):
 EXPORTS = ("q38_f16_to_f32", "q38_quantize_q8_k", "q38_tensor_gemv_q8_k", "q38_tensor_gemm_q8_k",
            "q38hip_quantize_q8_k", "q38hip_gemm_q8_k", "q38hip_argmax", "q38hip_argmax_noalloc", "q38hip_accept",
            "q38hip_tiled_q4k_bytes", "q38hip_repack_q4k_tiles", "q38hip_gemm_q8_k_tiled", "q38hip_attention_rows",
-           "q38hip_last_error", "q38hip_synchronize",
+           "q38hip_sample", "q38hip_last_error", "q38hip_synchronize",
            "q38_model_open_gguf", "q38_model_attach_mtp_gguf", "q38_model_close", "q38_model_reset",
            "q38_model_forward_token", "q38_model_prefill", "q38_model_enable_mtp", "q38_model_mtp_forward",
            "q38_model_speculative_greedy", "q38_model_forward_token_layers", "q38_model_vocab_size",
-           "q38_model_position", "q38_model_context_length")
+           "q38_model_position", "q38_model_context_length", "q38hip_model_sample",
+           "q38hip_model_forward_sample")
 
 
 def load_library(path=LIB_PATH):
@@ -78,6 +79,8 @@ def load_library(path=LIB_PATH):
     lib.q38hip_argmax_noalloc.argtypes = [vp, vp, u32, u32, vp]
     lib.q38hip_accept.argtypes = [vp, vp, vp, u32, vp]
     lib.q38hip_attention_rows.argtypes = [vp, vp, vp, vp, vp, u64, vp, vp, vp, vp, u32, u32, u32, vp]
+    lib.q38hip_sample.argtypes = [vp, ctypes.POINTER(ctypes.c_uint64), vp, u32, ctypes.c_float, ctypes.c_float,
+                                  ctypes.c_float, u32, vp, u32, vp]
     lib.q38hip_last_error.restype = ctypes.c_char_p
     lib.q38hip_last_error.argtypes = []
     lib.q38hip_synchronize.argtypes = []
@@ -114,6 +117,29 @@ def _dev_ptr(tensor):
     if not tensor.is_contiguous():
         raise ValueError("expected a contiguous tensor")
     return ctypes.c_void_p(tensor.data_ptr())
+
+
+# ---- sampler state (host side of include/qwen38/qwen38_sampler.h) ----------
+
+class Sampler:
+    """The Q38Sampler fields (include/qwen38/qwen38_sampler.h:10-18) with
+    q38_sampler_init's defaults (src/qwen38/qwen38_sampler.c:22-32) and
+    q38_sampler_observe (:34-38).  `presence` is a numpy uint8 array or None;
+    `state` advances with every sampling call made through it."""
+
+    GOLDEN = 0x9E3779B97F4A7C15
+
+    def __init__(self, seed=0, temperature=1.0, top_p=0.95, presence_penalty=0.0, top_k=20, presence=None):
+        self.state = int(seed) if seed else self.GOLDEN
+        self.temperature = float(temperature)
+        self.top_p = float(top_p)
+        self.presence_penalty = float(presence_penalty)
+        self.top_k = int(top_k)
+        self.presence = presence
+
+    def observe(self, token):
+        if self.presence is not None and 0 <= token < self.presence.size:
+            self.presence[token] = 1
 
 
 # ---- device-resident API (torch tensors on the GPU) --------------------------
@@ -184,6 +210,26 @@ def argmax_noalloc(values, out=None):
         out = torch.empty(values2.shape[0], dtype=torch.int32, device=values.device)
     _check(lib().q38hip_argmax_noalloc(_dev_ptr(out), _dev_ptr(values2), values2.shape[1], values2.shape[0],
                                        _stream()), "q38hip_argmax_noalloc")
+    return out
+
+
+def sample(logits, sampler, presence=None, out=None):
+    """q38hip_sample: one token from float32 logits [vocabulary] on the GPU,
+    drawn as q38_sample draws it; `sampler` (a Sampler) supplies the
+    parameters and its state advances.  presence: a uint8 device tensor or
+    None (then sampler.presence is not used).  Returns an int32 [1] device
+    tensor."""
+    import torch
+    if logits.dtype != torch.float32:
+        raise ValueError("expected float32 logits")
+    if out is None:
+        out = torch.empty(1, dtype=torch.int32, device=logits.device)
+    state = ctypes.c_uint64(sampler.state)
+    _check(lib().q38hip_sample(_dev_ptr(out), ctypes.byref(state), _dev_ptr(logits), logits.numel(),
+                               sampler.temperature, sampler.top_p, sampler.presence_penalty, sampler.top_k,
+                               None if presence is None else _dev_ptr(presence),
+                               0 if presence is None else presence.numel(), _stream()), "q38hip_sample")
+    sampler.state = state.value
     return out
 
 

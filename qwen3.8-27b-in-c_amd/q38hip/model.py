@@ -36,6 +36,9 @@ def _bind(lib):
     lib.q38_model_mtp_forward.argtypes = [vp, u32, ctypes.POINTER(_f32p)]
     lib.q38_model_speculative_greedy.argtypes = [vp, u32, u32, u32, vp, _u32p, ctypes.POINTER(_f32p)]
     lib.q38_model_forward_token_layers.argtypes = [vp, u32, u32, vp]
+    f32, u64p = ctypes.c_float, ctypes.POINTER(ctypes.c_uint64)
+    lib.q38hip_model_sample.argtypes = [vp, u64p, f32, f32, f32, u32, vp, u32, _u32p]
+    lib.q38hip_model_forward_sample.argtypes = [vp, u32, u64p, f32, f32, f32, u32, vp, u32, _u32p]
     for name in ("q38_model_vocab_size", "q38_model_position", "q38_model_context_length"):
         getattr(lib, name).restype = u32
         getattr(lib, name).argtypes = [vp]
@@ -125,6 +128,37 @@ class Model:
                                                      accepted.ctypes.data, ctypes.byref(count), ctypes.byref(p)):
             raise RuntimeError("q38_model_speculative_greedy failed")
         return accepted[:count.value].copy(), (self._copy(p) if logits else None)
+
+    @staticmethod
+    def _sampler_args(sampler):
+        presence = sampler.presence
+        if presence is not None:
+            if not (isinstance(presence, np.ndarray) and presence.dtype == np.uint8 and presence.flags.c_contiguous):
+                raise ValueError("presence must be a contiguous numpy uint8 array")
+        return (sampler.temperature, sampler.top_p, sampler.presence_penalty, sampler.top_k,
+                None if presence is None else presence.ctypes.data, 0 if presence is None else presence.size)
+
+    def sample(self, sampler):
+        """q38hip_model_sample: q38_sample over the last returned logits, on
+        the device; sampler.state advances.  Returns the token id."""
+        state = ctypes.c_uint64(sampler.state)
+        token = ctypes.c_uint32(0)
+        if not self.lib.q38hip_model_sample(self.handle, ctypes.byref(state), *self._sampler_args(sampler),
+                                            ctypes.byref(token)):
+            raise RuntimeError("q38hip_model_sample failed")
+        sampler.state = state.value
+        return token.value
+
+    def forward_sample(self, token, sampler):
+        """q38hip_model_forward_sample: forward_token(token) then sample,
+        without downloading the logits.  Returns the sampled token id."""
+        state = ctypes.c_uint64(sampler.state)
+        out = ctypes.c_uint32(0)
+        if not self.lib.q38hip_model_forward_sample(self.handle, int(token), ctypes.byref(state),
+                                                    *self._sampler_args(sampler), ctypes.byref(out)):
+            raise RuntimeError("q38hip_model_forward_sample failed")
+        sampler.state = state.value
+        return out.value
 
     def forward_token_layers(self, token, layers):
         hidden = np.zeros(HIDDEN, dtype=np.float32)

@@ -12,7 +12,11 @@ Bar: bit-identical.  The prefill logits, every transaction's logits and
 every greedy step's logits compare by SHA-256 of their float32 bytes; the
 token ids and accepted counts compare exactly.  The call sequence is the
 reference's own speculative bench (src/cli/qwen38_spec_bench.c:37-83,
-100-119)."""
+100-119).
+
+The device sampler entry points (q38hip_model_sample,
+q38hip_model_forward_sample) are checked on the same model against
+q38_sample on the host logits: same tokens, same RNG states."""
 import hashlib
 import os
 import time
@@ -78,3 +82,53 @@ def test_greedy_decode_matches_reference(case):
         assert digest(logits) == str(want_digest), "step %d: logits differ" % i
         tokens.append(int(np.argmax(logits)))
     assert tokens == [int(t) for t in golden["greedy_tokens"]]
+
+
+def test_device_sampling_matches_reference(case):
+    """Sampling on the device from the model's logits, against the
+    reference's q38_sample over the downloaded logits: the reference CLI's
+    generation loop (src/cli/qwen38_main.c:545-553: sample, observe,
+    forward) run both ways for 24 tokens with the presence penalty on, and
+    single draws with several sampler settings."""
+    from oracle import Oracle, Reference
+    from q38hip import Sampler
+    golden, model, prompt, _ = case
+    checker = Reference() if Reference.available() else Oracle()
+    vocab = model.lib.q38_model_vocab_size(model.handle)
+    model.reset()
+    logits = model.prefill(prompt[:32])
+    presence = np.zeros(vocab, np.uint8)
+    presence[np.argsort(-logits)[:5]] = 1
+    for s in (Sampler(seed=7, temperature=0.8, top_k=40, top_p=0.9), Sampler(seed=0),
+              Sampler(seed=3, temperature=0.0), Sampler(seed=5, temperature=1.0, top_k=1),
+              Sampler(seed=11, temperature=1.3, top_k=256, top_p=1.0, presence_penalty=1.5, presence=presence),
+              Sampler(seed=13, temperature=0.6, top_k=1024, top_p=0.99, presence_penalty=-0.5, presence=presence)):
+        want = checker.sample(logits, s.state, s.temperature, s.top_p, s.presence_penalty, s.top_k, s.presence)
+        got = model.sample(s)
+        assert (got, s.state) == want, vars(s)
+
+    def settings(presence):
+        return Sampler(seed=21, temperature=0.9, top_k=20, top_p=0.95, presence_penalty=0.7, presence=presence)
+
+    host = settings(np.zeros(vocab, np.uint8))
+    model.reset()
+    logits = model.prefill(prompt[:32])
+    token, host.state = checker.sample(logits, host.state, host.temperature, host.top_p, host.presence_penalty,
+                                       host.top_k, host.presence)
+    want = [token]
+    for _ in range(24):
+        host.observe(token)
+        logits = model.forward_token(token)
+        token, host.state = checker.sample(logits, host.state, host.temperature, host.top_p,
+                                           host.presence_penalty, host.top_k, host.presence)
+        want.append(token)
+
+    dev = settings(np.zeros(vocab, np.uint8))
+    model.reset()
+    model.prefill(prompt[:32])
+    got = [model.sample(dev)]
+    for _ in range(24):
+        dev.observe(got[-1])
+        got.append(model.forward_sample(got[-1], dev))
+    assert got == want
+    assert dev.state == host.state
