@@ -20,6 +20,28 @@ REF_SO = os.path.join(HERE, "_ref", "libq38ref.so")
 Q4_K, Q6_K, IQ1_M = 12, 14, 29
 BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, IQ1_M: 56}
 
+# Every matrix format the reference model accepts (src/qwen38/qwen38_model.c:
+# 172-189): GGML type id -> (elements per block, bytes per block).
+F32, F16, Q8_0, Q2_K, Q3_K, Q5_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, BF16 = (
+    0, 1, 8, 10, 11, 13, 16, 17, 18, 19, 20, 21, 22, 23, 30)
+FORMATS = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q8_0: (32, 34), Q2_K: (256, 84), Q3_K: (256, 110),
+           Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), IQ2_XXS: (256, 66), IQ2_XS: (256, 74),
+           IQ2_S: (256, 82), IQ3_XXS: (256, 98), IQ3_S: (256, 110), IQ4_XS: (256, 136), IQ4_NL: (32, 18),
+           IQ1_S: (256, 50), IQ1_M: (256, 56)}
+FORMAT_NAMES = {F32: "F32", F16: "F16", BF16: "BF16", Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_K: "Q3_K", Q4_K: "Q4_K",
+                Q5_K: "Q5_K", Q6_K: "Q6_K", IQ2_XXS: "IQ2_XXS", IQ2_XS: "IQ2_XS", IQ2_S: "IQ2_S",
+                IQ3_XXS: "IQ3_XXS", IQ3_S: "IQ3_S", IQ4_XS: "IQ4_XS", IQ4_NL: "IQ4_NL", IQ1_S: "IQ1_S",
+                IQ1_M: "IQ1_M"}
+# formats whose GEMV takes Q8_K activations (q38_matrix_type_q8_k, :172-182);
+# the rest take fp32 activations through q38_tensor_gemv_f32
+Q8K_FORMATS = (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, IQ1_S, IQ1_M)
+F32_FORMATS = (F32, F16, BF16, Q8_0)
+
+
+def row_bytes(qtype, width):
+    elements, nbytes = FORMATS[qtype]
+    return width // elements * nbytes
+
 # Q38Q8KBlock (include/qwen38/qwen38_quant.h:14-18): 292 bytes, no padding.
 Q8K_DTYPE = np.dtype([("scale", "<f4"), ("quants", "i1", (256,)), ("sums", "<i2", (16,))])
 assert Q8K_DTYPE.itemsize == 292
@@ -93,6 +115,12 @@ class Oracle:
                                    _u32p, _u32p, ctypes.c_void_p]
         lib.orc_iq1m_grid_entry.argtypes = [ctypes.c_uint32, ctypes.c_void_p]
         lib.orc_attention_decode.argtypes = [ctypes.c_void_p] * 8 + [ctypes.c_uint32]
+        vp, u32, u64 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64
+        lib.orc_format_gemv_q8_k.argtypes = [vp, vp, u64, u32, vp, u64]
+        lib.orc_format_gemv_f32.argtypes = [vp, vp, u64, u32, vp, u64]
+        lib.orc_format_row_f32.argtypes = [vp, u32, vp, u64, u64]
+        lib.orc_format_block_lanes.argtypes = [u32, vp, vp, vp, ctypes.POINTER(ctypes.c_int32)]
+        lib.orc_format_block_decode.argtypes = [u32, vp, vp, vp]
         lib.orc_sample.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64), ctypes.c_void_p,
                                    ctypes.c_uint32, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                                    ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint32]
@@ -115,9 +143,40 @@ class Oracle:
 
     def gemv(self, qtype, data, rows, q8k):
         out = np.zeros(rows, dtype=np.float32)
-        if not self.lib.orc_gemv_q8_k(_ptr(out), _ptr(q8k), q8k.size * 256, qtype, _ptr(data), rows):
+        if not self.lib.orc_format_gemv_q8_k(_ptr(out), _ptr(q8k), q8k.size * 256, qtype, _ptr(data), rows):
             raise ValueError("bad GEMV arguments")
         return out
+
+    def gemv_f32(self, qtype, data, rows, x):
+        """q38_tensor_gemv_f32 restated: fp32 input x [width]."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros(rows, dtype=np.float32)
+        if not self.lib.orc_format_gemv_f32(_ptr(out), _ptr(x), x.size, qtype, _ptr(data), rows):
+            raise ValueError("bad float GEMV arguments")
+        return out
+
+    def format_row_f32(self, qtype, data, width, row):
+        """q38_tensor_row_f32 restated, any format."""
+        out = np.zeros(width, dtype=np.float32)
+        if not self.lib.orc_format_row_f32(_ptr(out), qtype, _ptr(data), width, row):
+            raise ValueError("unsupported row type")
+        return out
+
+    def block_lanes(self, qtype, block, q8k_block):
+        """(eight int32 lanes, integer min / correction term) of one super-block."""
+        lanes = np.zeros(8, dtype=np.int32)
+        extra = ctypes.c_int32(0)
+        if not self.lib.orc_format_block_lanes(qtype, _ptr(block), _ptr(q8k_block), _ptr(lanes), ctypes.byref(extra)):
+            raise ValueError("not a Q8_K-path format")
+        return lanes, extra.value
+
+    def block_decode(self, qtype, block):
+        """(q[256], s16[16]) integer weights and 16-element scales."""
+        q = np.zeros(256, dtype=np.int32)
+        s16 = np.zeros(16, dtype=np.int32)
+        if not self.lib.orc_format_block_decode(qtype, _ptr(block), _ptr(q), _ptr(s16)):
+            raise ValueError("not a Q8_K-path format")
+        return q, s16
 
     def gemm(self, qtype, data, rows, q8k, batch):
         out = np.zeros(batch * rows, dtype=np.float32)
@@ -188,6 +247,9 @@ class Reference:
         lib.q38_tensor_gemm_q8_k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
                                              ctypes.c_uint64, ctypes.POINTER(GGUFTensor)]
         lib.q38_tensor_row_f32.argtypes = [ctypes.c_void_p, ctypes.POINTER(GGUFTensor), ctypes.c_uint64]
+        lib.q38_tensor_gemv_f32.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(GGUFTensor)]
+        lib.q38_tensor_gemm_f32.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64,
+                                            ctypes.POINTER(GGUFTensor)]
         lib.q38ref_full_core.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_uint32, ctypes.c_void_p,
                                                                   ctypes.c_void_p, ctypes.c_uint32]
         lib.q38_sampler_init.argtypes = [ctypes.POINTER(Q38Sampler), ctypes.c_uint64]
@@ -222,6 +284,24 @@ class Reference:
         out = np.zeros(batch * rows, dtype=np.float32)
         if not self.lib.q38_tensor_gemm_q8_k(_ptr(out), _ptr(q8k), batch, width, ctypes.byref(tensor)):
             raise ValueError("bad GEMM arguments")
+        return out.reshape(batch, rows)
+
+    def gemv_f32(self, qtype, data, rows, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        tensor = make_tensor(data, qtype, x.size, rows)
+        out = np.zeros(rows, dtype=np.float32)
+        if not self.lib.q38_tensor_gemv_f32(_ptr(out), _ptr(x), ctypes.byref(tensor)):
+            raise ValueError("bad float GEMV arguments")
+        return out
+
+    def gemm_f32(self, qtype, data, rows, x):
+        """x: [batch, width] fp32 -> [batch, rows]"""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        batch, width = x.shape
+        tensor = make_tensor(data, qtype, width, rows)
+        out = np.zeros(batch * rows, dtype=np.float32)
+        if not self.lib.q38_tensor_gemm_f32(_ptr(out), _ptr(x), batch, width, ctypes.byref(tensor)):
+            raise ValueError("bad float GEMM arguments")
         return out.reshape(batch, rows)
 
     def row_f32(self, qtype, data, width, row, rows):
