@@ -62,8 +62,32 @@ float q38_f16_to_f32(uint16_t value);
 int q38_quantize_q8_k(Q38Q8KBlock *output, const float *input,
                       uint64_t length);
 
+/* replaces q38_tensor_row_f32, include/qwen38/qwen38_quant.h:27-28: row
+ * `row` as fp32 (F32 copied, F16 / BF16 converted, Q8_0, IQ4_NL and
+ * Q2_K..Q6_K decoded; other types give NaN, as in the reference) */
+int q38_tensor_row_f32(float *output, const Q38GGUFTensor *tensor,
+                       uint64_t row);
+
+/* replaces q38_tensor_dot_row_f32, include/qwen38/qwen38_quant.h:30-31:
+ * one row's float dot; returns 1 only for a finite result */
+int q38_tensor_dot_row_f32(float *output, const float *input,
+                           const Q38GGUFTensor *tensor, uint64_t row);
+
+/* replaces q38_tensor_gemv_f32, include/qwen38/qwen38_quant.h:34-35: fp32
+ * input (F32, F16, BF16, Q8_0, IQ4_NL, Q2_K..Q6_K; NaN rows for the other
+ * types, as in the reference) */
+int q38_tensor_gemv_f32(float *output, const float *input,
+                        const Q38GGUFTensor *tensor);
+
+/* replaces q38_tensor_gemm_f32, include/qwen38/qwen38_quant.h:44-46;
+ * batch-major output, any batch_size >= 1 */
+int q38_tensor_gemm_f32(float *output, const float *input,
+                        uint32_t batch_size, uint64_t input_length,
+                        const Q38GGUFTensor *tensor);
+
 /* replaces q38_tensor_gemv_q8_k, include/qwen38/qwen38_quant.h:38-40
- * (Q4_K, Q6_K and IQ1_M tensors) */
+ * (every Q8_K-path format: Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ1_S, IQ1_M,
+ * IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ4_NL, IQ4_XS) */
 int q38_tensor_gemv_q8_k(float *output, const Q38Q8KBlock *input,
                          uint64_t input_length,
                          const Q38GGUFTensor *tensor);
@@ -73,6 +97,13 @@ int q38_tensor_gemv_q8_k(float *output, const Q38Q8KBlock *input,
 int q38_tensor_gemm_q8_k(float *output, const Q38Q8KBlock *input,
                          uint32_t batch_size, uint64_t input_length,
                          const Q38GGUFTensor *tensor);
+
+/* replace q38_prepare_iq1_s_repacks / q38_release_iq1_s_repacks,
+ * include/qwen38/qwen38_quant.h:54-55 (argument: the caller's Q38GGUF).
+ * The GPU kernels read IQ1_S blocks as stored, so no view is built:
+ * prepare returns 1 for a non-NULL argument and changes nothing. */
+int q38_prepare_iq1_s_repacks(void *gguf);
+void q38_release_iq1_s_repacks(void *gguf);
 
 /* ---- 2. device-resident variants ---------------------------------------- */
 
@@ -89,6 +120,19 @@ int q38hip_quantize_q8_k(Q38Q8KBlock *output, const float *input,
 int q38hip_gemm_q8_k(float *output, const Q38Q8KBlock *input,
                      uint32_t batch_size, uint64_t input_length,
                      const Q38GGUFTensor *tensor, void *stream);
+
+/* Device form of q38_tensor_gemm_f32 (src/qwen38/qwen38_quant.c:2924-2948):
+ * input is batch_size rows of input_length fp32 values; batch_size = 1 is
+ * q38_tensor_gemv_f32 (:2812-2831).  Each output is the row's single fmaf
+ * chain in the reference's element order (q38_dot_row, :2768-2810). */
+int q38hip_gemm_f32(float *output, const float *input, uint32_t batch_size,
+                    uint64_t input_length, const Q38GGUFTensor *tensor,
+                    void *stream);
+
+/* Device form of q38_tensor_row_f32 (src/qwen38/qwen38_quant.c:3185-3223)
+ * for rows first_row .. first_row + row_count - 1: output[r * width + e]. */
+int q38hip_row_f32(float *output, const Q38GGUFTensor *tensor,
+                   uint64_t first_row, uint32_t row_count, void *stream);
 
 /* Row-wise first-maximum index (q38_argmax, src/qwen38/qwen38_model.c:
  * 1228-1239) of `rows` rows of `count` floats; index_out[rows].  Partial

@@ -1,6 +1,8 @@
 /* C ABI of libq38hip (declared in include/q38hip.h). */
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -82,20 +84,19 @@ DeviceState *device_state()
     return &s;
 }
 
-bool supported_type(uint32_t type)
+/* the Q8_K-path matrix formats (q38_matrix_type_q8_k, src/qwen38/qwen38_model.c:172-182) */
+bool supported_type(uint32_t type) { return q38::format_takes_q8k((int)type); }
+
+/* bytes of `length` elements of `type` (0 for unknown types) */
+uint64_t span_bytes(uint32_t type, uint64_t length)
 {
-    return type == q38::kQ4K || type == q38::kQ6K || type == q38::kIQ1M;
+    uint32_t e = 0, b = 0;
+    if (!q38::format_block_shape((int)type, &e, &b) || length % e) return 0;
+    return length / e * b;
 }
 
-uint64_t block_bytes(uint32_t type)
-{
-    switch (type) {
-    case q38::kQ4K: return 144;
-    case q38::kQ6K: return 210;
-    case q38::kIQ1M: return 56;
-    default: return 0;
-    }
-}
+/* types with a dedicated kernel family (the decode path's formats) */
+bool tuned_type(uint32_t type) { return type == q38::kQ4K || type == q38::kQ6K || type == q38::kIQ1M; }
 
 /* Argument checks of q38_tensor_gemm_q8_k (src/qwen38/qwen38_quant.c:2950-2974). */
 int check_gemm(const void *output, const void *input, uint32_t batch, uint64_t input_length,
@@ -105,7 +106,8 @@ int check_gemm(const void *output, const void *input, uint32_t batch, uint64_t i
     if (tensor->n_dims != 2) return fail("tensor must be 2-D");
     if (tensor->shape[0] != input_length) return fail("tensor width differs from input length");
     if (input_length % Q38_Q8_K_BLOCK_SIZE) return fail("input length is not a multiple of 256");
-    if (!supported_type(tensor->type)) return fail("tensor type is not Q4_K, Q6_K or IQ1_M");
+    if (!supported_type(tensor->type))
+        return fail("tensor type is not a Q8_K-path format (Q2_K..Q6_K, IQ1_S, IQ1_M, IQ2_*, IQ3_*, IQ4_*)");
     if (!tensor->data) return fail("tensor has no data");
     if (tensor->shape[1] == 0 || tensor->shape[1] > 0xffffffffull) return fail("bad row count");
     if (input_length / 256 > 0xffffffffull) return fail("input too long");
@@ -215,13 +217,66 @@ int q38hip_gemm_q8_k(float *output, const Q38Q8KBlock *input, uint32_t batch_siz
         return 1;
     for (uint32_t t0 = 0; t0 < batch_size;) {
         const uint32_t n = token_chunk(batch_size - t0, 1);
-        if (!q38::launch_gemm((int)tensor->type, (int)n, tensor->data,
-                              reinterpret_cast<const uint8_t *>(input) + (size_t)t0 * nb * sizeof(Q38Q8KBlock),
-                              output + (size_t)t0 * rows, rows, nb, state->grid, static_cast<hipStream_t>(stream)))
-            return fail("unsupported GEMM configuration");
+        const uint8_t *x = reinterpret_cast<const uint8_t *>(input) + (size_t)t0 * nb * sizeof(Q38Q8KBlock);
+        const bool ok = tuned_type(tensor->type)
+                            ? q38::launch_gemm((int)tensor->type, (int)n, tensor->data, x, output + (size_t)t0 * rows,
+                                               rows, nb, state->grid, static_cast<hipStream_t>(stream))
+                            : q38::launch_gemm_format((int)tensor->type, (int)n, tensor->data, x,
+                                                      output + (size_t)t0 * rows, rows, rows, nb, state->grid,
+                                                      static_cast<hipStream_t>(stream));
+        if (!ok) return fail("unsupported GEMM configuration");
         t0 += n;
     }
     return 1;
+}
+
+int q38hip_gemm_f32(float *output, const float *input, uint32_t batch_size, uint64_t input_length,
+                    const Q38GGUFTensor *tensor, void *stream)
+{
+    /* argument checks of q38_tensor_gemm_f32 (qwen38_quant.c:2928-2936) */
+    if (!output || !input || !batch_size || !tensor || tensor->n_dims != 2 || tensor->shape[0] != input_length)
+        return fail("bad float GEMM arguments");
+    if (!span_bytes(tensor->type, input_length) || !input_length) return fail("unsupported tensor type or width");
+    if (!tensor->data) return fail("tensor has no data");
+    if (tensor->shape[1] == 0 || tensor->shape[1] > 0xffffffffull || input_length > 0xffffffffull)
+        return fail("bad tensor shape");
+    if (!device_state()) return fail("device initialisation failed");
+    const uint32_t rows = (uint32_t)tensor->shape[1];
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!q38::format_row_decodable((int)tensor->type)) {
+        /* the reference's float dot has no case for this type: NaN rows */
+        q38::launch_fill_f32(output, (uint64_t)batch_size * rows, __builtin_nanf(""), s);
+        return 1;
+    }
+    for (uint32_t t0 = 0; t0 < batch_size;) {
+        const uint32_t n = std::min<uint32_t>(4, batch_size - t0);
+        if (!q38::launch_gemm_float((int)tensor->type, (int)n, tensor->data, input + (size_t)t0 * input_length,
+                                    output + (size_t)t0 * rows, rows, rows, (uint32_t)input_length, s))
+            return fail("unsupported float GEMM configuration");
+        t0 += n;
+    }
+    return 1;
+}
+
+int q38hip_row_f32(float *output, const Q38GGUFTensor *tensor, uint64_t first_row, uint32_t row_count, void *stream)
+{
+    /* argument checks of q38_tensor_row_f32 (qwen38_quant.c:3185-3194) */
+    if (!output || !tensor || tensor->n_dims != 2 || !row_count || first_row >= tensor->shape[1] ||
+        row_count > tensor->shape[1] - first_row)
+        return fail("bad row arguments");
+    const uint64_t width = tensor->shape[0];
+    if (!span_bytes(tensor->type, width) || width > 0xffffffffull || tensor->shape[1] > 0xffffffffull)
+        return fail("unsupported tensor type or width");
+    if (!tensor->data) return fail("tensor has no data");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!q38::format_row_decodable((int)tensor->type)) {
+        q38::launch_fill_f32(output, (uint64_t)row_count * width, __builtin_nanf(""), s);
+        return 1;
+    }
+    return q38::launch_row_decode((int)tensor->type, tensor->data, nullptr, (uint32_t)first_row, row_count,
+                                  (uint32_t)tensor->shape[1], output, (uint32_t)width, s)
+               ? 1
+               : fail("row decode launch failed");
 }
 
 uint64_t q38hip_tiled_q4k_bytes(uint32_t rows, uint64_t input_length)
@@ -363,7 +418,7 @@ int q38_tensor_gemm_q8_k(float *output, const Q38Q8KBlock *input, uint32_t batch
     if (!check_gemm(output, input, batch_size, input_length, tensor)) return 0;
     const uint64_t rows = tensor->shape[1];
     const uint64_t blocks = input_length / 256;
-    const uint64_t wbytes = rows * blocks * block_bytes(tensor->type);
+    const uint64_t wbytes = rows * span_bytes(tensor->type, input_length);
     const uint64_t xbytes = (uint64_t)batch_size * blocks * sizeof(Q38Q8KBlock);
     const uint64_t ybytes = (uint64_t)batch_size * rows * sizeof(float);
     DeviceBuffer dw(wbytes), dx(xbytes), dy(ybytes);
@@ -386,5 +441,73 @@ int q38_tensor_gemv_q8_k(float *output, const Q38Q8KBlock *input, uint64_t input
 {
     return q38_tensor_gemm_q8_k(output, input, 1, input_length, tensor);
 }
+
+int q38_tensor_gemm_f32(float *output, const float *input, uint32_t batch_size, uint64_t input_length,
+                        const Q38GGUFTensor *tensor)
+{
+    if (!output || !input || !batch_size || !tensor || tensor->n_dims != 2 || tensor->shape[0] != input_length)
+        return fail("bad float GEMM arguments");
+    const uint64_t rows = tensor->shape[1];
+    const uint64_t wbytes = rows * span_bytes(tensor->type, input_length);
+    if (!wbytes || !tensor->data) return fail("unsupported tensor type or width");
+    const uint64_t xbytes = (uint64_t)batch_size * input_length * sizeof(float);
+    const uint64_t ybytes = (uint64_t)batch_size * rows * sizeof(float);
+    DeviceBuffer dw(wbytes), dx(xbytes), dy(ybytes);
+    if (!dw.ptr || !dx.ptr || !dy.ptr) return fail("device allocation failed");
+    if (hipMemcpy(dw.ptr, tensor->data, wbytes, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(dx.ptr, input, xbytes, hipMemcpyHostToDevice) != hipSuccess)
+        return fail("copy to device failed");
+    Q38GGUFTensor dev = *tensor;
+    dev.data = static_cast<const uint8_t *>(dw.ptr);
+    if (!q38hip_gemm_f32(static_cast<float *>(dy.ptr), static_cast<const float *>(dx.ptr), batch_size,
+                         input_length, &dev, nullptr))
+        return 0;
+    if (hipMemcpy(output, dy.ptr, ybytes, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("copy from device failed");
+    return 1;
+}
+
+int q38_tensor_gemv_f32(float *output, const float *input, const Q38GGUFTensor *tensor)
+{
+    if (!tensor) return fail("bad float GEMV arguments");
+    return q38_tensor_gemm_f32(output, input, 1, tensor->shape[0], tensor);
+}
+
+int q38_tensor_dot_row_f32(float *output, const float *input, const Q38GGUFTensor *tensor, uint64_t row)
+{
+    if (!output || !input || !tensor || tensor->n_dims != 2 || row >= tensor->shape[1])
+        return fail("bad row dot arguments");
+    const uint64_t bytes = span_bytes(tensor->type, tensor->shape[0]);
+    if (!bytes || !tensor->data) return fail("unsupported tensor type or width");
+    Q38GGUFTensor one = *tensor;
+    one.shape[1] = 1;
+    one.data = tensor->data + row * bytes;
+    if (!q38_tensor_gemv_f32(output, input, &one)) return 0;
+    return std::isfinite(*output) ? 1 : 0;
+}
+
+int q38_tensor_row_f32(float *output, const Q38GGUFTensor *tensor, uint64_t row)
+{
+    if (!output || !tensor || tensor->n_dims != 2 || row >= tensor->shape[1]) return fail("bad row arguments");
+    const uint64_t width = tensor->shape[0];
+    const uint64_t bytes = span_bytes(tensor->type, width);
+    if (!bytes || !tensor->data) return fail("unsupported tensor type or width");
+    DeviceBuffer dw(bytes), dy(width * sizeof(float));
+    if (!dw.ptr || !dy.ptr) return fail("device allocation failed");
+    if (hipMemcpy(dw.ptr, tensor->data + row * bytes, bytes, hipMemcpyHostToDevice) != hipSuccess)
+        return fail("copy to device failed");
+    Q38GGUFTensor dev = *tensor;
+    dev.shape[1] = 1;
+    dev.data = static_cast<const uint8_t *>(dw.ptr);
+    if (!q38hip_row_f32(static_cast<float *>(dy.ptr), &dev, 0, 1, nullptr)) return 0;
+    if (hipMemcpy(output, dy.ptr, width * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("copy from device failed");
+    return 1;
+}
+
+/* The GPU kernels read the GGUF blocks as they are, so there is no IQ1_S
+ * view to build: both calls succeed and leave every tensor unchanged. */
+int q38_prepare_iq1_s_repacks(void *gguf) { return gguf ? 1 : 0; }
+void q38_release_iq1_s_repacks(void *gguf) { (void)gguf; }
 
 }  // extern "C"

@@ -49,6 +49,30 @@ bool launch_gemm_q4k_wide(uint32_t tokens, const uint8_t *w_tiled, const uint8_t
 bool launch_gemm_ld(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                     uint32_t nblk, const void *grid, hipStream_t stream);
 
+/* q38_formats.hip: every other matrix format of the reference model.
+ * format_block_shape: elements and bytes of one GGUF block of any type the
+ * GGUF reader sizes (q38_ggml_block_elements / _bytes,
+ * src/io/qwen38_gguf.c:129-184; false otherwise).  format_takes_q8k: the GEMV takes Q8_K
+ * activations (else fp32).  launch_gemm_format: y[t * ldy + row] for t < m
+ * (1..8) against Q8_K activations, for Q2_K, Q3_K, Q5_K, IQ2_XXS, IQ2_XS,
+ * IQ2_S, IQ3_XXS, IQ3_S, IQ4_XS, IQ4_NL and IQ1_S (`grid`: the IQ1_M/IQ1_S
+ * codebook as 2048 x 8 int8); false for other types.  launch_gemm_float:
+ * the same against fp32 activations x[t * width + e] (m 1..4) for F32, F16,
+ * BF16, Q8_0, IQ4_NL and Q2_K..Q6_K.  launch_row_decode: rows of such a
+ * matrix as fp32 (q38_tensor_row_f32), output row r from matrix row ids[r]
+ * (clamped below `limit`) or first + r. */
+bool format_block_shape(int type, uint32_t *elements, uint32_t *bytes);
+bool format_takes_q8k(int type);
+bool format_row_decodable(int type);
+bool launch_gemm_format(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                        uint32_t nb, const void *grid, hipStream_t stream);
+bool launch_gemm_float(int type, int m, const uint8_t *w, const float *x, float *y, uint32_t ldy, uint32_t rows,
+                       uint32_t width, hipStream_t stream);
+bool launch_row_decode(int type, const uint8_t *w, const uint32_t *ids, uint32_t first, uint32_t count,
+                       uint32_t limit, float *out, uint32_t width, hipStream_t stream);
+/* out[0 .. count) = value */
+void launch_fill_f32(float *out, uint64_t count, float value, hipStream_t stream);
+
 /* q38_abi.hip: record an argument error for q38hip_last_error(); returns 0 */
 int abi_fail(const char *message);
 

@@ -48,6 +48,8 @@ def make_tensor(data_ptr, qtype, width, rows, nbytes=0):
 
 # Every symbol the C header declares (tests check the library exports them).
 EXPORTS = ("q38_f16_to_f32", "q38_quantize_q8_k", "q38_tensor_gemv_q8_k", "q38_tensor_gemm_q8_k",
+           "q38_tensor_row_f32", "q38_tensor_dot_row_f32", "q38_tensor_gemv_f32", "q38_tensor_gemm_f32",
+           "q38_prepare_iq1_s_repacks", "q38_release_iq1_s_repacks", "q38hip_gemm_f32", "q38hip_row_f32",
            "q38hip_quantize_q8_k", "q38hip_gemm_q8_k", "q38hip_argmax", "q38hip_argmax_noalloc", "q38hip_accept",
            "q38hip_tiled_q4k_bytes", "q38hip_repack_q4k_tiles", "q38hip_gemm_q8_k_tiled", "q38hip_attention_rows",
            "q38hip_sample", "q38hip_last_error", "q38hip_synchronize",
@@ -70,6 +72,15 @@ def load_library(path=LIB_PATH):
     lib.q38_tensor_gemv_q8_k.argtypes = [vp, vp, u64, ctypes.POINTER(GGUFTensor)]
     lib.q38_tensor_gemm_q8_k.argtypes = [vp, vp, u32, u64, ctypes.POINTER(GGUFTensor)]
     lib.q38hip_quantize_q8_k.argtypes = [vp, vp, u64, u32, vp]
+    lib.q38_tensor_row_f32.argtypes = [vp, ctypes.POINTER(GGUFTensor), u64]
+    lib.q38_tensor_dot_row_f32.argtypes = [vp, vp, ctypes.POINTER(GGUFTensor), u64]
+    lib.q38_tensor_gemv_f32.argtypes = [vp, vp, ctypes.POINTER(GGUFTensor)]
+    lib.q38_tensor_gemm_f32.argtypes = [vp, vp, u32, u64, ctypes.POINTER(GGUFTensor)]
+    lib.q38_prepare_iq1_s_repacks.argtypes = [vp]
+    lib.q38_release_iq1_s_repacks.restype = None
+    lib.q38_release_iq1_s_repacks.argtypes = [vp]
+    lib.q38hip_gemm_f32.argtypes = [vp, vp, u32, u64, ctypes.POINTER(GGUFTensor), vp]
+    lib.q38hip_row_f32.argtypes = [vp, ctypes.POINTER(GGUFTensor), u64, u32, vp]
     lib.q38hip_gemm_q8_k.argtypes = [vp, vp, u32, u64, ctypes.POINTER(GGUFTensor), vp]
     lib.q38hip_tiled_q4k_bytes.restype = u64
     lib.q38hip_tiled_q4k_bytes.argtypes = [u32, u64]
@@ -166,6 +177,29 @@ def gemm_q8_k(weights, qtype, width, rows, xq, batch, out=None):
     tensor = make_tensor(weights.data_ptr(), qtype, width, rows, weights.numel())
     _check(lib().q38hip_gemm_q8_k(_dev_ptr(out), _dev_ptr(xq), batch, width, ctypes.byref(tensor),
                                   _stream()), "q38hip_gemm_q8_k")
+    return out
+
+
+def gemm_f32(weights, qtype, width, rows, x, out=None):
+    """weights: uint8 GGUF rows on the GPU; x: float32 [batch, width] on the
+    GPU.  Returns float32 [batch, rows] (q38_tensor_gemm_f32)."""
+    import torch
+    x2 = x if x.dim() == 2 else x.reshape(1, -1)
+    if out is None:
+        out = torch.empty((x2.shape[0], rows), dtype=torch.float32, device=weights.device)
+    tensor = make_tensor(weights.data_ptr(), qtype, width, rows, weights.numel())
+    _check(lib().q38hip_gemm_f32(_dev_ptr(out), _dev_ptr(x2), x2.shape[0], width, ctypes.byref(tensor), _stream()),
+           "q38hip_gemm_f32")
+    return out
+
+
+def row_f32(weights, qtype, width, rows, first, count=1):
+    """Rows first .. first + count - 1 of a GGUF matrix on the GPU as
+    float32 [count, width] (q38_tensor_row_f32)."""
+    import torch
+    out = torch.empty((count, width), dtype=torch.float32, device=weights.device)
+    tensor = make_tensor(weights.data_ptr(), qtype, width, rows, weights.numel())
+    _check(lib().q38hip_row_f32(_dev_ptr(out), ctypes.byref(tensor), first, count, _stream()), "q38hip_row_f32")
     return out
 
 
