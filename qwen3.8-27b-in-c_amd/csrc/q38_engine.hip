@@ -331,7 +331,13 @@ void make_group(Group *g, std::initializer_list<const DevTensor *> parts)
     }
 }
 
-bool matrix_type_ok(uint32_t t) { return t == Q4_K || t == Q6_K || t == IQ1_M; }
+/* q38_matrix_type_supported (qwen38_model.c:172-189): the Q8_K-path formats
+ * and F32, F16, BF16, Q8_0 */
+bool matrix_type_ok(uint32_t t) { return q38::format_takes_q8k((int)t) || t == 0 || t == 1 || t == 8 || t == 30; }
+
+/* projections of these types take the fp32 input (q38_project,
+ * qwen38_model.c:598-605) */
+bool float_input(const DevTensor &t) { return !q38::format_takes_q8k((int)t.type); }
 
 }  // namespace
 
@@ -366,6 +372,11 @@ struct Q38Model {
     float *qbuf = nullptr, *attn = nullptr;
     float *scores = nullptr, *logits = nullptr, *target_norm = nullptr;
     float *prep = nullptr;   /* prepared DeltaNet inputs of a prefill batch */
+    /* fp32 inputs of the projections whose matrices take them (F32, F16,
+     * BF16, Q8_0): scratch_rows rows of up to kFFN floats, allocated only
+     * when the checkpoint has such a matrix */
+    float *fin = nullptr;
+    bool float_inputs = false;
     /* output-norm rows of a verify longer than kBatch rows (grown on demand) */
     float *long_norm = nullptr;
     uint32_t long_norm_rows = 0;
@@ -414,8 +425,7 @@ bool bind_tensor(const GGUFFile &f, const uint8_t *base, const std::string &name
     return true;
 }
 
-/* q38_expect_tensor (qwen38_model.c:190-207), restricted to the matrix types
- * this library has kernels for */
+/* q38_expect_tensor (qwen38_model.c:190-207) */
 bool expect(const DevTensor &t, const std::string &name, uint64_t width, uint64_t rows, bool f32_only)
 {
     const uint32_t dims = rows ? 2u : 1u;
@@ -425,7 +435,7 @@ bool expect(const DevTensor &t, const std::string &name, uint64_t width, uint64_
     fprintf(stderr, "qwen38: incompatible tensor %s; expected %s[%llu", name.c_str(), f32_only ? "F32 " : "",
             (unsigned long long)width);
     if (rows) fprintf(stderr, ",%llu", (unsigned long long)rows);
-    fprintf(stderr, "] of type %s\n", f32_only ? "F32" : "Q4_K, Q6_K or IQ1_M");
+    fprintf(stderr, "]%s\n", f32_only ? "" : " of a supported matrix type");
     return false;
 }
 
@@ -633,7 +643,6 @@ bool bind_mtp(Q38Model *m, const GGUFFile &f, const uint8_t *base)
               expect(m->enorm, "blk.64.nextn.enorm.weight", kHidden, 0, true) &&
               expect(m->hnorm, "blk.64.nextn.hnorm.weight", kHidden, 0, true) &&
               expect(m->shared_head_norm, "blk.64.nextn.shared_head_norm.weight", kHidden, 0, true);
-    if (ok && m->mtp_embedding.type != Q4_K) ok = report("MTP token_embd.weight must be Q4_K");
     if (ok) m->mtp_weights_loaded = true;
     return ok;
 }
@@ -645,7 +654,7 @@ void release(Q38Model *m)
     float **fbufs[] = {&m->conv_state, &m->delta_state, &m->key_cache, &m->value_cache, &m->mtp_hidden,
                        &m->ck_mtp_hidden, &m->rope, &m->hidden, &m->norm,
                        &m->branch, &m->wide0, &m->qbuf, &m->attn, &m->scores, &m->logits, &m->target_norm,
-                       &m->argmax_pv, &m->long_norm, &m->prep};
+                       &m->argmax_pv, &m->long_norm, &m->prep, &m->fin};
     for (float **p : fbufs) dfree(*p);
     uint32_t **ubufs[] = {&m->tokens, &m->params, &m->words, &m->argmax_pi};
     for (uint32_t **p : ubufs) dfree(*p);
@@ -709,6 +718,34 @@ bool allocate_state(Q38Model *m)
     m->query_scale = 1.0f / sqrtf(128.0f);
     return hip_ok(hipMemcpy(m->rope, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice),
                   "rope table upload");
+}
+
+/* whether a projection of the loaded blocks takes fp32 input (an F32, F16,
+ * BF16 or Q8_0 matrix); if so, allocate their input rows m->fin.  Captured
+ * step graphs are dropped when this changes what the steps compute. */
+bool setup_float_inputs(Q38Model *m)
+{
+    bool any = float_input(m->output);
+    const uint32_t last = m->mtp_weights_loaded ? kLayers + 1 : kLayers;
+    for (uint32_t l = 0; l < last; ++l) {
+        const Layer &L = m->layers[l];
+        const DevTensor *mats[] = {&L.ffn_gate, &L.ffn_up, &L.ffn_down};
+        for (const DevTensor *t : mats) any = any || float_input(*t);
+        if (L.full) {
+            any = any || float_input(L.q) || float_input(L.k) || float_input(L.v) || float_input(L.out);
+        } else {
+            any = any || float_input(L.qkv) || float_input(L.z) || float_input(L.alpha) || float_input(L.beta) ||
+                  float_input(L.ssm_out);
+        }
+    }
+    if (m->mtp_weights_loaded) any = any || float_input(m->eh_proj) || float_input(m->mtp_output);
+    if (!any || m->float_inputs) return true;
+    if (!dalloc(&m->fin, (size_t)m->scratch_rows * kFFN)) return false;
+    m->float_inputs = true;
+    for (auto &g : m->graphs) (void)hipGraphExecDestroy(g.second);
+    m->graphs.clear();
+    m->seen.clear();
+    return true;
 }
 
 /* zero the recurrent state (slot 0 of every layer becomes current), KV
@@ -786,17 +823,42 @@ bool gemm_rows(Q38Model *m, const DevTensor &w, uint32_t count, const uint8_t *x
     if (w.type == IQ1_M && count >= (uint32_t)q38::kWideMinTokens &&
         q38::launch_gemm_iq1m_wide(count, wdata, x, out, ldy, rows, nb, m->grid, m->stream))
         return true;
+    /* Q4_K, Q6_K and IQ1_M have their own kernel families; the other Q8_K
+     * formats run the generic lane-chain kernel */
+    const bool tuned = w.type == Q4_K || w.type == Q6_K || w.type == IQ1_M;
     for (uint32_t t0 = 0; t0 < count; t0 += kBatch) {
         const uint32_t n = std::min(kBatch, count - t0);
-        if (!q38::launch_gemm_ld((int)w.type, (int)n, wdata, x + (size_t)t0 * nb * kQ8KBytes, out + (size_t)t0 * ldy,
-                                 ldy, rows, nb, m->grid, m->stream))
-            return report("unsupported GEMM configuration");
+        const uint8_t *xt = x + (size_t)t0 * nb * kQ8KBytes;
+        const bool ok = tuned ? q38::launch_gemm_ld((int)w.type, (int)n, wdata, xt, out + (size_t)t0 * ldy, ldy, rows,
+                                                   nb, m->grid, m->stream)
+                              : q38::launch_gemm_format((int)w.type, (int)n, wdata, xt, out + (size_t)t0 * ldy, ldy,
+                                                        rows, nb, m->grid, m->stream);
+        if (!ok) return report("unsupported GEMM configuration");
     }
     return true;
 }
 
-bool gemm_q(Q38Model *m, const DevTensor &w, uint32_t count, float *out, size_t first_block = 0)
+/* a float-input matrix (F32, F16, BF16, Q8_0) over `count` fp32 rows at xf,
+ * rows w.width floats apart (q38_tensor_gemv_f32 per row) */
+bool gemm_float(Q38Model *m, const DevTensor &w, uint32_t count, const float *xf, float *out, uint32_t ldy,
+                uint32_t rows, const uint8_t *wdata)
 {
+    if (!xf) return report("float-input projection without its fp32 input");
+    for (uint32_t t0 = 0; t0 < count; t0 += 4) {
+        const uint32_t n = std::min<uint32_t>(4, count - t0);
+        if (!q38::launch_gemm_float((int)w.type, (int)n, wdata, xf + (size_t)t0 * w.width, out + (size_t)t0 * ldy, ldy,
+                                    rows, (uint32_t)w.width, m->stream))
+            return report("unsupported float GEMM configuration");
+    }
+    return true;
+}
+
+/* one projection: Q8_K rows from m->q8k (starting at block first_block), or
+ * for a float-input matrix the fp32 rows at xf */
+bool gemm_q(Q38Model *m, const DevTensor &w, uint32_t count, float *out, size_t first_block = 0,
+            const float *xf = nullptr)
+{
+    if (float_input(w)) return gemm_float(m, w, count, xf, out, (uint32_t)w.rows, (uint32_t)w.rows, w.data);
     if (count >= 2 && w.tiled &&
         q38::launch_gemm_q4k_tiled((int)count, w.tiled, m->q8k + first_block * kQ8KBytes, out, (uint32_t)w.rows,
                                    (uint32_t)w.rows, (uint32_t)(w.width / 256), m->stream))
@@ -892,12 +954,17 @@ bool build_tiled(Q38Model *m, uint32_t first, uint32_t last, bool with_eh, void 
 /* members [lo, hi) of group g over `count` Q8_K rows in m->q8k; row t of
  * member i lands at out + t * ldy + first[i] - first[lo].  Two or more rows
  * use the tiled copy where there is one. */
-bool gemm_group(Q38Model *m, const Group &g, int lo, int hi, uint32_t count, float *out, uint32_t ldy)
+bool gemm_group(Q38Model *m, const Group &g, int lo, int hi, uint32_t count, float *out, uint32_t ldy,
+                const float *xf = nullptr)
 {
     bool ok = true;
     for_runs(g, lo, hi, [&](int i, int, uint64_t rows) {
         const DevTensor &a = g.part[i];
         float *y = out + (g.first[i] - g.first[lo]);
+        if (float_input(a)) {
+            if (!gemm_float(m, a, count, xf, y, ldy, (uint32_t)rows, a.data)) ok = false;
+            return;
+        }
         const uint32_t nb = (uint32_t)(a.width / 256);
         if (count >= 2 && a.tiled &&
             q38::launch_gemm_q4k_tiled((int)count, a.tiled, m->q8k, y, ldy, (uint32_t)rows, nb, m->stream))
@@ -934,6 +1001,19 @@ void advance_slots(Q38Model *m, uint32_t rows, uint32_t layers = kLayers)
     }
 }
 
+/* token embedding rows of `count` token ids into m->hidden
+ * (q38_tensor_row_f32 of token_embd): the Q4_K kernel, the generic row
+ * decode, or NaN rows for a type the reference's row decode has no case for */
+void embed(Q38Model *m, const DevTensor &table, const uint32_t *tokens, uint32_t count)
+{
+    if (table.type == Q4_K) {
+        q38::launch_embed_q4k(m->hidden, table.data, tokens, (int)count, kHidden, kVocab, m->stream);
+    } else if (!q38::launch_row_decode((int)table.type, table.data, tokens, 0, count, kVocab, m->hidden, kHidden,
+                                       m->stream)) {
+        q38::launch_fill_f32(m->hidden, (uint64_t)count * kHidden, __builtin_nanf(""), m->stream);
+    }
+}
+
 /* apply a pending FFN residual add to m->hidden */
 void flush_branch(Q38Model *m, uint32_t count)
 {
@@ -942,9 +1022,11 @@ void flush_branch(Q38Model *m, uint32_t count)
 }
 
 /* RMSNorm of the rows of m->hidden (after adding the pending FFN branch of
- * the previous block, if any) into Q8_K rows of m->q8k */
+ * the previous block, if any) into Q8_K rows of m->q8k, and the fp32 rows
+ * into norm_out (m->fin by default when float-input matrices need them) */
 void norm_hidden(Q38Model *m, const DevTensor &weight, uint32_t count, float *norm_out = nullptr)
 {
+    if (!norm_out && m->float_inputs) norm_out = m->fin;
     q38::launch_norm_quant(norm_out, kHidden, m->q8k, kHidden / 256, m->hidden, kHidden,
                            m->pending_branch ? m->branch : nullptr, weight.f32(), (int)count, m->stream);
     m->pending_branch = false;
@@ -960,7 +1042,7 @@ bool full_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count)
     const size_t kv_off = (size_t)full_index * m->context_length * kKVDim;
     /* per row: q+gate [12288] | k [1024] | v [1024] */
     const Group &g = L.mix_in;
-    if (!gemm_group(m, g, 0, 3, count, m->wide0, g.width)) return false;
+    if (!gemm_group(m, g, 0, 3, count, m->wide0, g.width, m->fin)) return false;
     q38::launch_attention(m->attn, m->q8k, m->qbuf, m->wide0, m->wide0 + g.first[1], m->wide0 + g.first[2], g.width,
                           L.q_norm.f32(), L.k_norm.f32(), m->rope, m->key_cache + kv_off, m->value_cache + kv_off,
                           m->scores, (int)m->context_length, s.params, (int)count, m->stream);
@@ -972,7 +1054,7 @@ bool full_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count)
         trace(m, "Vcur-", layer, m->wide0 + g.first[2], kKVDim);
         trace(m, "attn_gated-", layer, m->attn, kQDim);
     }
-    if (!gemm_q(m, L.out, count, m->branch)) return false;
+    if (!gemm_q(m, L.out, count, m->branch, 0, m->attn)) return false;
     if (count == 1) trace(m, "attn_output-", layer, m->branch, kHidden);
     return true;
 }
@@ -985,7 +1067,7 @@ bool linear_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count
     /* per row: qkv [10240] | z [6144] | beta [48] | alpha [48] */
     const Group &g = L.mix_in;
     const uint32_t ld = g.width;
-    if (!gemm_group(m, g, 0, 4, count, m->wide0, ld)) return false;
+    if (!gemm_group(m, g, 0, 4, count, m->wide0, ld, m->fin)) return false;
     const bool tr = count == 1 && trace_enabled();
     if (tr) {
         trace(m, "dn_qkv_proj-", layer, m->wide0, kQKV);
@@ -1024,7 +1106,7 @@ bool linear_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count
     q38::launch_deltanet_out_quant(m->attn, m->q8k, m->wide0 + g.first[1], ld, L.ssm_norm.f32(), (int)count,
                                    m->stream);
     if (tr) trace(m, "dn_gated-", layer, m->attn, kLinV);
-    return gemm_q(m, L.ssm_out, count, m->branch);
+    return gemm_q(m, L.ssm_out, count, m->branch, 0, m->attn);
 }
 
 /* one transformer block over `count` rows of m->hidden
@@ -1041,9 +1123,10 @@ bool layer_rows(Q38Model *m, const Step &s, int layer, uint32_t count)
     norm_hidden(m, L.post_norm, count);
     if (count == 1) trace(m, "attn_residual-", layer, m->hidden, kHidden);
     const Group &g = L.ffn_in;   /* per row: gate [17408] | up [17408] */
-    if (!gemm_group(m, g, 0, 2, count, m->wide0, g.width)) return false;
-    q38::launch_swiglu_quant(m->q8k, m->wide0, m->wide0 + g.first[1], g.width, (int)count, m->stream);
-    if (!gemm_q(m, L.ffn_down, count, m->branch)) return false;
+    if (!gemm_group(m, g, 0, 2, count, m->wide0, g.width, m->fin)) return false;
+    q38::launch_swiglu_quant(m->q8k, m->wide0, m->wide0 + g.first[1], g.width, (int)count, m->stream,
+                             m->float_inputs ? m->fin : nullptr);
+    if (!gemm_q(m, L.ffn_down, count, m->branch, 0, m->fin)) return false;
     m->pending_branch = true;
     if (count == 1 && trace_enabled()) {
         trace(m, "ffn_out-", layer, m->branch, kHidden);
@@ -1060,13 +1143,14 @@ bool layer_rows(Q38Model *m, const Step &s, int layer, uint32_t count)
  * caller advances the host-side state (slots, position). */
 bool target_rows(Q38Model *m, const Step &s, uint32_t count, uint32_t logit_rows)
 {
-    q38::launch_embed_q4k(m->hidden, m->embedding.data, s.tokens, (int)count, kHidden, kVocab, m->stream);
+    embed(m, m->embedding, s.tokens, count);
     m->pending_branch = false;
     if (count == 1) trace(m, "model.input_embed", -1, m->hidden, kHidden);
     for (uint32_t layer = 0; layer < kLayers; ++layer)
         if (!layer_rows(m, s, (int)layer, count)) return false;
     norm_hidden(m, m->output_norm, count, m->target_norm);
-    if (logit_rows && !gemm_q(m, m->output, logit_rows, m->logits, (size_t)(count - logit_rows) * (kHidden / 256)))
+    if (logit_rows && !gemm_q(m, m->output, logit_rows, m->logits, (size_t)(count - logit_rows) * (kHidden / 256),
+                              m->target_norm + (size_t)(count - logit_rows) * kHidden))
         return false;
     return launches_ok();
 }
@@ -1082,23 +1166,25 @@ bool mtp_catchup(Q38Model *m, const Step &s, uint32_t count)
 {
     const Layer &L = m->layers[kLayers];
     constexpr int kHB = kHidden / 256;   /* Q8_K blocks per hidden row */
-    q38::launch_embed_q4k(m->hidden, m->mtp_embedding.data, s.tokens, (int)count, kHidden, kVocab, m->stream);
+    embed(m, m->mtp_embedding, s.tokens, count);
     /* Q8_K rows of 2*kHidden: [enorm(e_t) | hnorm(prev_t)], prev_0 = MTP hidden,
-     * prev_t = target_norm[t-1] */
-    q38::launch_norm_quant(nullptr, 0, m->q8k, 2 * kHB, m->hidden, kHidden, nullptr, m->enorm.f32(), (int)count,
+     * prev_t = target_norm[t-1] (and the same fp32 rows in m->fin when the
+     * projection takes them) */
+    float *f = m->float_inputs ? m->fin : nullptr;
+    q38::launch_norm_quant(f, 2 * kHidden, m->q8k, 2 * kHB, m->hidden, kHidden, nullptr, m->enorm.f32(), (int)count,
                            m->stream);
-    q38::launch_norm_quant(nullptr, 0, m->q8k + kHB * kQ8KBytes, 2 * kHB, m->mtp_hidden, kHidden, nullptr,
-                           m->hnorm.f32(), 1, m->stream);
+    q38::launch_norm_quant(f ? f + kHidden : nullptr, 2 * kHidden, m->q8k + kHB * kQ8KBytes, 2 * kHB, m->mtp_hidden,
+                           kHidden, nullptr, m->hnorm.f32(), 1, m->stream);
     if (count > 1)
-        q38::launch_norm_quant(nullptr, 0, m->q8k + 3 * kHB * kQ8KBytes, 2 * kHB, m->target_norm, kHidden, nullptr,
-                               m->hnorm.f32(), (int)count - 1, m->stream);
-    if (!gemm_q(m, m->eh_proj, count, m->hidden)) return false;
+        q38::launch_norm_quant(f ? f + 3 * kHidden : nullptr, 2 * kHidden, m->q8k + 3 * kHB * kQ8KBytes, 2 * kHB,
+                               m->target_norm, kHidden, nullptr, m->hnorm.f32(), (int)count - 1, m->stream);
+    if (!gemm_q(m, m->eh_proj, count, m->hidden, 0, m->fin)) return false;
     m->pending_branch = false;
     norm_hidden(m, L.attn_norm, count);
     /* k | v members of the block's q+gate | k | v group, rows 2048 apart */
     const Group &g = L.mix_in;
     const uint32_t ld = g.first[2] + (uint32_t)g.part[2].rows - g.first[1];
-    if (!gemm_group(m, g, 1, 3, count, m->wide0, ld)) return false;
+    if (!gemm_group(m, g, 1, 3, count, m->wide0, ld, m->fin)) return false;
     const size_t kv_off = (size_t)(kLayers / 4) * m->context_length * kKVDim;
     q38::launch_kv_write(m->wide0, m->wide0 + (g.first[2] - g.first[1]), ld, L.k_norm.f32(), m->rope,
                          m->key_cache + kv_off, m->value_cache + kv_off, s.params, (int)count, m->stream);
@@ -1115,18 +1201,19 @@ bool mtp_catchup(Q38Model *m, const Step &s, uint32_t count)
 bool mtp_step(Q38Model *m, const Step &s)
 {
     constexpr int kHB = kHidden / 256;
-    q38::launch_embed_q4k(m->hidden, m->mtp_embedding.data, s.tokens, 1, kHidden, kVocab, m->stream);
-    q38::launch_norm_quant(nullptr, 0, m->q8k, 2 * kHB, m->hidden, kHidden, nullptr, m->enorm.f32(), 1, m->stream);
-    q38::launch_norm_quant(nullptr, 0, m->q8k + kHB * kQ8KBytes, 2 * kHB, m->mtp_hidden, kHidden, nullptr,
-                           m->hnorm.f32(), 1, m->stream);
-    if (!gemm_q(m, m->eh_proj, 1, m->hidden)) return false;
+    embed(m, m->mtp_embedding, s.tokens, 1);
+    float *f = m->float_inputs ? m->fin : nullptr;
+    q38::launch_norm_quant(f, 2 * kHidden, m->q8k, 2 * kHB, m->hidden, kHidden, nullptr, m->enorm.f32(), 1, m->stream);
+    q38::launch_norm_quant(f ? f + kHidden : nullptr, 2 * kHidden, m->q8k + kHB * kQ8KBytes, 2 * kHB, m->mtp_hidden,
+                           kHidden, nullptr, m->hnorm.f32(), 1, m->stream);
+    if (!gemm_q(m, m->eh_proj, 1, m->hidden, 0, m->fin)) return false;
     m->pending_branch = false;
     if (!layer_rows(m, s, (int)kLayers, 1)) return false;
     /* mtp hidden = shared_head_norm(hidden + branch), and its Q8_K rows */
     q38::launch_norm_quant(m->mtp_hidden, kHidden, m->q8k, kHB, m->hidden, kHidden,
                            m->pending_branch ? m->branch : nullptr, m->shared_head_norm.f32(), 1, m->stream);
     m->pending_branch = false;
-    return gemm_q(m, m->mtp_output, 1, m->logits) && launches_ok();
+    return gemm_q(m, m->mtp_output, 1, m->logits, 0, m->mtp_hidden) && launches_ok();
 }
 
 /* ---- graphs ------------------------------------------------------------------ */
@@ -1418,13 +1505,12 @@ Q38Model *q38_model_open_gguf(const char *path, uint32_t context_length)
     ok = ok && expect(m->embedding, "token_embd.weight", kHidden, kVocab, false) &&
          expect(m->output_norm, "output_norm.weight", kHidden, 0, true) &&
          expect(m->output, "output.weight", kHidden, kVocab, false);
-    if (ok && m->embedding.type != Q4_K) ok = report("token_embd.weight must be Q4_K");
     uint32_t blocks = 0;
     if (ok && m->gguf.get_u32("qwen35.block_count", &blocks) && blocks == kTotalLayers)
         ok = bind_mtp(m, m->gguf, base);
     ok = ok && build_tiled(m, 0, kLayers, false, &m->tiled_weights) &&
          (!m->mtp_weights_loaded || build_tiled(m, kLayers, kLayers + 1, true, &m->tiled_mtp));
-    ok = ok && allocate_state(m) && clear_state(m);
+    ok = ok && allocate_state(m) && clear_state(m) && setup_float_inputs(m);
     if (ok && !q38::configure_attention((int)context_length)) ok = report("attention kernel configuration failed");
     if (const char *v = getenv("QWEN38_NO_GRAPHS")) m->graphs_enabled = !(v[0] && strcmp(v, "0") != 0);
     if (!ok) {
@@ -1441,7 +1527,7 @@ int q38_model_attach_mtp_gguf(Q38Model *m, const char *path)
         return 0;
     const bool ok = m->mtp_gguf.open(path) && upload(m->mtp_gguf, &m->mtp_weights) &&
                     bind_mtp(m, m->mtp_gguf, static_cast<const uint8_t *>(m->mtp_weights)) &&
-                    build_tiled(m, kLayers, kLayers + 1, true, &m->tiled_mtp);
+                    build_tiled(m, kLayers, kLayers + 1, true, &m->tiled_mtp) && setup_float_inputs(m);
     if (!ok) {
         m->layers[kLayers] = Layer();
         m->mtp_embedding = m->mtp_output = m->eh_proj = m->enorm = m->hnorm = m->shared_head_norm = DevTensor();
@@ -1504,7 +1590,7 @@ int q38_model_forward_token_layers(Q38Model *m, uint32_t token, uint32_t layer_c
     write_params(m, kParamTarget, m->position);
     if (!upload_tokens(m, &token, 1, m->tokens) || !flush_params(m)) return 0;
     const Step s = step_of(m, kParamTarget, m->tokens);
-    q38::launch_embed_q4k(m->hidden, m->embedding.data, s.tokens, 1, kHidden, kVocab, m->stream);
+    embed(m, m->embedding, s.tokens, 1);
     trace(m, "model.input_embed", -1, m->hidden, kHidden);
     m->pending_branch = false;
     for (uint32_t layer = 0; layer < layer_count; ++layer)

@@ -106,9 +106,10 @@ bool launch_sample(uint32_t *token_out, uint64_t *state, const float *logits, ui
 void launch_norm_quant(float *norm_out, long long norm_stride, uint8_t *q_out, int q_stride_blocks, float *hidden,
                        long long in_stride, const float *branch, const float *weight, int rows, hipStream_t stream);
 void launch_add(float *hidden, const float *branch, long long n, hipStream_t stream);
-/* row t of gate and up starts at t * stride floats */
+/* row t of gate and up starts at t * stride floats; f_out (optional) gets
+ * the fp32 rows before quantisation, row t at t * 17408 */
 void launch_swiglu_quant(uint8_t *q_out, const float *gate, const float *up, long long stride, int rows,
-                         hipStream_t stream);
+                         hipStream_t stream, float *f_out = nullptr);
 void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int count, int width, uint32_t vocab,
                       hipStream_t stream);
 /* gated DeltaNet core of one row: conv + SiLU + q/k L2 norm + beta/alpha,

@@ -54,7 +54,8 @@ constexpr int kFFNWidth = 17408;
  * qwen38_model.c:532-549), one wavefront per 256-element block; row t of
  * gate and up starts at t * stride (a multiple of 4). */
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(uint8_t *__restrict__ q_out, const float *__restrict__ gate,
-                                                           const float *__restrict__ up, long long stride, int nblocks)
+                                                           const float *__restrict__ up, long long stride, int nblocks,
+                                                           float *__restrict__ f_out)
 {
     const int lane = threadIdx.x & 63;
     const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -65,6 +66,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(uint8_t *__restrict__
     const float4 u = *reinterpret_cast<const float4 *>(up + at);
     const float v[4] = {__fmul_rn(siluf_exact(g.x), u.x), __fmul_rn(siluf_exact(g.y), u.y),
                         __fmul_rn(siluf_exact(g.z), u.z), __fmul_rn(siluf_exact(g.w), u.w)};
+    if (f_out) *reinterpret_cast<float4 *>(f_out + (size_t)b * 256 + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
     wave_quantize_q8k(v, q_out + (size_t)b * kQ8KBytes, lane);
 }
 
@@ -716,10 +718,10 @@ void launch_add(float *hidden, const float *branch, long long n, hipStream_t str
 }
 
 void launch_swiglu_quant(uint8_t *q_out, const float *gate, const float *up, long long stride, int rows,
-                         hipStream_t stream)
+                         hipStream_t stream, float *f_out)
 {
     const int nblocks = rows * (kFFNWidth / 256);
-    swiglu_quant_kernel<<<(nblocks + 3) / 4, 256, 0, stream>>>(q_out, gate, up, stride, nblocks);
+    swiglu_quant_kernel<<<(nblocks + 3) / 4, 256, 0, stream>>>(q_out, gate, up, stride, nblocks, f_out);
 }
 
 void launch_embed_q4k(float *out, const uint8_t *w, const uint32_t *tokens, int count, int width, uint32_t vocab,

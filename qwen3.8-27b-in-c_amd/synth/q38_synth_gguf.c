@@ -30,7 +30,19 @@
  * A tensor's bytes depend on its place in the full 65-block Q4_K_M list, so
  * tensors shared between variants are byte-identical.
  *
- * Usage: q38_synth_gguf OUT.gguf SEED q4km|iq1m|accept|accept_mtp
+ * The mixed variant exercises every other matrix format the reference model
+ * accepts: the layer matrices cycle through Q2_K, Q3_K, Q5_K, IQ2_XXS,
+ * IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ4_XS, IQ4_NL, IQ1_S, Q4_K, Q6_K and
+ * IQ1_M; the small DeltaNet alpha / beta and attention K / V matrices cycle
+ * through Q8_0, F16, BF16 and F32, as do the FFN down, attention output and
+ * DeltaNet output matrices of a few layers (so every producer of a float
+ * projection input is used); the token embedding is Q8_0 and the LM head
+ * Q5_K.  Random bytes with each format's fp16 scales set to a size that
+ * gives weights of standard deviation ~1/sqrt(fan_in) (the constants below
+ * are the standard deviation of a block's weights at scale 1); Q2_K and Q5_K
+ * mins are set to centre their sub-blocks as for Q4_K.
+ *
+ * Usage: q38_synth_gguf OUT.gguf SEED q4km|iq1m|accept|accept_mtp|mixed
  */
 #define _GNU_SOURCE
 #include <fcntl.h>
@@ -41,7 +53,10 @@
 #include <string.h>
 #include <unistd.h>
 
-enum { F32 = 0, Q4_K = 12, Q6_K = 14, IQ1_M = 29 };
+enum {
+    F32 = 0, F16 = 1, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14, IQ2_XXS = 16, IQ2_XS = 17,
+    IQ3_XXS = 18, IQ1_S = 19, IQ4_NL = 20, IQ3_S = 21, IQ2_S = 22, IQ4_XS = 23, IQ1_M = 29, BF16 = 30
+};
 enum { HIDDEN = 5120, FFN = 17408, VOCAB = 248320, LAYERS = 64 };
 
 static uint64_t mix64(uint64_t z)
@@ -99,14 +114,58 @@ typedef struct {
 static Tensor tensors[1024];
 static int tensor_count;
 
+/* bytes and elements of one block */
 static uint64_t block_bytes(uint32_t type)
 {
     switch (type) {
     case Q4_K: return 144;
     case Q6_K: return 210;
     case IQ1_M: return 56;
+    case Q2_K: return 84;
+    case Q3_K: return 110;
+    case Q5_K: return 176;
+    case IQ2_XXS: return 66;
+    case IQ2_XS: return 74;
+    case IQ2_S: return 82;
+    case IQ3_XXS: return 98;
+    case IQ3_S: return 110;
+    case IQ4_XS: return 136;
+    case IQ4_NL: return 18;
+    case IQ1_S: return 50;
+    case Q8_0: return 34;
+    case F16: case BF16: return 2;
     default: return 4;
     }
+}
+
+static uint64_t block_elements(uint32_t type)
+{
+    switch (type) {
+    case F32: case F16: case BF16: return 1;
+    case Q8_0: case IQ4_NL: return 32;
+    default: return 256;
+    }
+}
+
+/* matrix formats of the mixed variant */
+static const uint32_t q8k_cycle[14] = {Q2_K, Q3_K, Q5_K, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS,
+                                       IQ3_S, IQ4_XS, IQ4_NL, IQ1_S, Q4_K, Q6_K, IQ1_M};
+static const uint32_t float_cycle[4] = {Q8_0, F16, BF16, F32};
+static int mixed_variant;
+static int mixed_counter;
+
+/* the type of the next layer matrix of `rows` rows in the mixed variant */
+static uint32_t mixed_type(const char *suffix, int layer)
+{
+    const int small = strstr(suffix, "ssm_alpha") || strstr(suffix, "ssm_beta") || strstr(suffix, "attn_k.") ||
+                      strstr(suffix, "attn_v.");
+    /* float-input projections fed by every producer: SwiGLU (ffn_down),
+     * attention (attn_output), DeltaNet (ssm_out), the MTP input (eh_proj) */
+    const int float_big = (strstr(suffix, "ffn_down") && (layer == 5 || layer == 40)) ||
+                          (strstr(suffix, "attn_output") && layer == 7) || (strstr(suffix, "ssm_out") && layer == 9) ||
+                          strstr(suffix, "eh_proj");
+    if (small || float_big) return float_cycle[(mixed_counter++ + layer) % 4];
+    return q8k_cycle[mixed_counter++ % 14];
 }
 
 static void add(const char *name, uint64_t width, uint64_t rows, uint32_t type, int kind)
@@ -122,14 +181,17 @@ static void add(const char *name, uint64_t width, uint64_t rows, uint32_t type, 
     t->type = type;
     t->kind = kind;
     const uint64_t elements = width * (rows ? rows : 1);
-    t->nbytes = type == F32 ? elements * 4 : elements / 256 * block_bytes(type);
+    t->nbytes = elements / block_elements(type) * block_bytes(type);
 }
 
 static void add_layer(int layer, uint32_t m)
 {
     char name[64];
 #define T(suffix, w, r, type, kind) \
-    do { snprintf(name, sizeof(name), "blk.%d.%s", layer, suffix); add(name, w, r, type, kind); } while (0)
+    do { \
+        snprintf(name, sizeof(name), "blk.%d.%s", layer, suffix); \
+        add(name, w, r, mixed_variant && !(kind) ? mixed_type(suffix, layer) : (uint32_t)(type), kind); \
+    } while (0)
     T("attn_norm.weight", HIDDEN, 0, F32, 1);
     T("post_attention_norm.weight", HIDDEN, 0, F32, 1);
     T("ffn_gate.weight", HIDDEN, FFN, m, 0);
@@ -215,6 +277,60 @@ static void iq1m_block(uint8_t *b, uint64_t seed, uint64_t tid, uint64_t index, 
     }
 }
 
+/* store half h at b + offset */
+static void put_half(uint8_t *b, int offset, float value)
+{
+    const uint16_t h = f32_to_f16(value);
+    memcpy(b + offset, &h, 2);
+}
+
+/* a block of one of the other formats: random bytes, fp16 scale fields set
+ * to base * (0.5 + u) / unit_std */
+static void other_block(uint32_t type, uint8_t *b, uint64_t seed, uint64_t tid, uint64_t index, double base)
+{
+    const uint64_t bytes = block_bytes(type);
+    fill_words(b, bytes, seed, tid, index * 32);
+    const float d = (float)(base * (0.5 + unit(hash3(seed, tid, index * 32 + 30))));
+    switch (type) {
+    case Q2_K: {
+        /* w = d sc q - dmin m, q in 0..3: m = round(3 sc / 4), dmin = 2d centres it */
+        for (int i = 0; i < 16; ++i) {
+            const int sc = b[i] & 15;
+            b[i] = (uint8_t)(sc | ((3 * sc + 2) / 4) << 4);
+        }
+        put_half(b, 80, d / 9.8f);
+        put_half(b, 82, 2.0f * d / 9.8f);
+        break;
+    }
+    case Q3_K: put_half(b, 108, d / 43.0f); break;
+    case Q5_K: {
+        /* q in 0..31: m = round(31 sc / 32), dmin = 16 d */
+        uint8_t sc[8], mn[8];
+        for (int j = 0; j < 8; ++j) {
+            sc[j] = b[4 + j] & 63;
+            mn[j] = (uint8_t)((31 * sc[j] + 16) / 32);
+        }
+        uint8_t *s = b + 4;
+        for (int j = 0; j < 4; ++j) {
+            s[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+            s[j + 4] = (uint8_t)((mn[j] & 63) | ((mn[j + 4] >> 4) << 6));
+            s[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4));
+        }
+        put_half(b, 0, d / 336.0f);
+        put_half(b, 2, 16.0f * d / 336.0f);
+        break;
+    }
+    case IQ2_XXS: case IQ2_XS: case IQ2_S: put_half(b, 0, d / 67.0f); break;
+    case IQ3_XXS: put_half(b, 0, d / 172.0f); break;
+    case IQ3_S: put_half(b, 0, d / 170.0f); break;
+    case IQ4_XS: put_half(b, 0, d / 1245.0f); break;
+    case IQ4_NL: put_half(b, 0, d / 67.0f); break;
+    case IQ1_S: put_half(b, 0, d / 7.5f); break;
+    case Q8_0: put_half(b, 0, d / 74.0f); break;
+    default: break;
+    }
+}
+
 static float f32_value(const Tensor *t, uint64_t seed, uint64_t tid, uint64_t i)
 {
     const double u = unit(hash3(seed, tid, i));
@@ -230,6 +346,27 @@ static float f32_value(const Tensor *t, uint64_t seed, uint64_t tid, uint64_t i)
 /* Fill bytes [begin, end) of tensor t (block aligned for quantised types). */
 static void generate(const Tensor *t, uint64_t seed, uint64_t tid, uint64_t begin, uint64_t end, uint8_t *out)
 {
+    if (t->kind == 0 && (t->type == F32 || t->type == F16 || t->type == BF16)) {
+        /* dense matrix: uniform weights of standard deviation 1/sqrt(fan_in) */
+        const uint64_t size = t->type == F32 ? 4 : 2;
+        const double a = sqrt(3.0 / (double)t->shape[0]);
+        for (uint64_t i = begin / size; i < end / size; ++i) {
+            const float v = (float)(a * (2.0 * unit(hash3(seed, tid, i)) - 1.0));
+            uint8_t *dst = out + (i * size - begin);
+            if (t->type == F32) {
+                memcpy(dst, &v, 4);
+            } else if (t->type == F16) {
+                const uint16_t h = f32_to_f16(v);
+                memcpy(dst, &h, 2);
+            } else {
+                uint32_t x;
+                memcpy(&x, &v, 4);
+                const uint16_t h = (uint16_t)(x >> 16);
+                memcpy(dst, &h, 2);
+            }
+        }
+        return;
+    }
     if (t->type == F32) {
         for (uint64_t i = begin / 4; i < end / 4; ++i) {
             const float v = f32_value(t, seed, tid, i);
@@ -249,7 +386,8 @@ static void generate(const Tensor *t, uint64_t seed, uint64_t tid, uint64_t begi
         }
         if (t->type == Q4_K) q4k_block(b, seed, tid, index, 1.0 / (168.0 * sqrt(fan_in)));
         else if (t->type == Q6_K) q6k_block(b, seed, tid, index, 1.0 / (1367.0 * sqrt(fan_in)));
-        else iq1m_block(b, seed, tid, index, 1.0 / (7.5 * sqrt(fan_in)));
+        else if (t->type == IQ1_M) iq1m_block(b, seed, tid, index, 1.0 / (7.5 * sqrt(fan_in)));
+        else other_block(t->type, b, seed, tid, index, 1.0 / sqrt(fan_in));
     }
 }
 
@@ -275,16 +413,17 @@ int main(int argc, char **argv)
 {
     const char *variant = argc == 4 ? argv[3] : "";
     const int accept = strcmp(variant, "accept") == 0, accept_mtp = strcmp(variant, "accept_mtp") == 0;
-    if (argc != 4 || (strcmp(variant, "q4km") && strcmp(variant, "iq1m") && !accept && !accept_mtp)) {
-        fprintf(stderr, "usage: %s OUT.gguf SEED q4km|iq1m|accept|accept_mtp\n", argv[0]);
+    mixed_variant = strcmp(variant, "mixed") == 0;
+    if (argc != 4 || (strcmp(variant, "q4km") && strcmp(variant, "iq1m") && !accept && !accept_mtp && !mixed_variant)) {
+        fprintf(stderr, "usage: %s OUT.gguf SEED q4km|iq1m|accept|accept_mtp|mixed\n", argv[0]);
         return 2;
     }
     const uint64_t seed = strtoull(argv[2], NULL, 0);
     const uint32_t m = strcmp(variant, "iq1m") == 0 ? IQ1_M : Q4_K;
 
-    add("token_embd.weight", HIDDEN, VOCAB, Q4_K, 0);
+    add("token_embd.weight", HIDDEN, VOCAB, mixed_variant ? Q8_0 : Q4_K, 0);
     add("output_norm.weight", HIDDEN, 0, F32, 1);
-    add("output.weight", HIDDEN, VOCAB, Q6_K, 0);
+    add("output.weight", HIDDEN, VOCAB, mixed_variant ? Q5_K : Q6_K, 0);
     const int first_mtp_tensor = tensor_count;
     for (int layer = 0; layer <= LAYERS; ++layer) add_layer(layer, m);
     int mtp_begin = first_mtp_tensor;
@@ -351,7 +490,7 @@ int main(int argc, char **argv)
     uint64_t written = 0, next_report = data_bytes / 10;
     for (int i = 0; i < tensor_count; ++i) {
         const Tensor *t = &tensors[i];
-        const uint64_t unit_bytes = t->type == F32 ? 4 : block_bytes(t->type);
+        const uint64_t unit_bytes = block_bytes(t->type);
         const uint64_t step = slice / unit_bytes * unit_bytes;
         const int64_t slices = (int64_t)((t->nbytes + step - 1) / step);
 #pragma omp parallel for schedule(dynamic, 1) reduction(| : failed)

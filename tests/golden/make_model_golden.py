@@ -2,8 +2,10 @@
 """Golden token sequences and logits digests of the COMPILED REFERENCE engine
 (oracle/_ref/libq38ref.so, the reference's own C sources) on the synthetic
 27B-shaped models written by qwen3.8-27b-in-c_amd/synth/q38_synth_gguf: the
-Q4_K_M layout (variant q4km) and the IQ1_M layout (variant iq1m: IQ1_M layer
-matrices, Q4_K embedding, Q6_K LM head).
+Q4_K_M layout (variant q4km), the IQ1_M layout (variant iq1m: IQ1_M layer
+matrices, Q4_K embedding, Q6_K LM head) and the mixed layout (variant mixed:
+every other matrix format the reference accepts, a Q8_0 embedding and a Q5_K
+LM head).
 
 The GGUF is a pure function of its seed (about 15.7 GB, not committed); this
 script writes it when missing, runs the reference's model API
@@ -19,7 +21,7 @@ Scenarios (context 256, MTP enabled, prompt of 12 seeded ids):
   spec     prefill(prompt) then speculative_greedy(k=3) until 12 tokens
 
 Run from the repository root:
-  python tests/golden/make_model_golden.py [q4km|iq1m [GGUF_PATH]]
+  python tests/golden/make_model_golden.py [q4km|iq1m|mixed [GGUF_PATH]]
 """
 import hashlib
 import os
@@ -120,8 +122,8 @@ def main():
     from oracle import reference_model
     from q38hip import synth
     variant = sys.argv[1] if len(sys.argv) > 1 else "q4km"
-    if variant not in ("q4km", "iq1m"):
-        raise SystemExit("variant must be q4km or iq1m")
+    if variant not in ("q4km", "iq1m", "mixed"):
+        raise SystemExit("variant must be q4km, iq1m or mixed")
     path = sys.argv[2] if len(sys.argv) > 2 else synth.model_path(SEED, variant)
     synth.write_model_gguf(path, SEED, variant)
     t0 = time.time()

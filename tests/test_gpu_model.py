@@ -1,8 +1,11 @@
 """Full-model parity on the GPU: the engine ABI of libq38hip (include/q38model.h)
 against the compiled reference engine's outputs on the same synthetic
-27B-shaped checkpoints, Q4_K_M layout and IQ1_M layout
-(tests/golden/model_<variant>_s1.npz, written by
-tests/golden/make_model_golden.py from oracle/_ref).
+27B-shaped checkpoints: the Q4_K_M layout, the IQ1_M layout and the mixed
+layout, whose matrices cycle through every other format the reference
+accepts (Q2_K, Q3_K, Q5_K, IQ1_S, IQ2_*, IQ3_*, IQ4_*, and F32, F16, BF16,
+Q8_0 on projections fed by every producer of an fp32 input), with a Q8_0
+embedding and a Q5_K LM head (tests/golden/model_<variant>_s1.npz, written
+by tests/golden/make_model_golden.py from oracle/_ref).
 
 Bar: bit-identical.  Hidden states after 1 and 4 blocks compare as uint32;
 every logits row compares by SHA-256 of its float32 bytes; token ids and
@@ -18,7 +21,7 @@ import pytest
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
 
 GOLDEN_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-VARIANTS = [v for v in ("q4km", "iq1m") if os.path.exists(os.path.join(GOLDEN_DIR, "model_%s_s1.npz" % v))]
+VARIANTS = [v for v in ("q4km", "iq1m", "mixed") if os.path.exists(os.path.join(GOLDEN_DIR, "model_%s_s1.npz" % v))]
 NO_STOP = 0xFFFFFFFF
 
 
