@@ -54,3 +54,14 @@ def test_reference_spec_probe_on_gpu(device):
     probe = program("qwen38-spec-probe-hip")
     out = run([probe, synthetic_model("accept"), synthetic_model("accept_mtp")])
     assert out.returncode == 0, out.stderr
+
+
+def test_reference_kernel_unit_test_on_gpu(device):
+    """tests/unit/test_qwen38_quant.c of the reference, linked against
+    libq38hip.so: its known answers for every format, its portable
+    restatements of the IQ kernels on random blocks, GEMM-equals-GEMV over
+    batch sizes 1..7, the IQ1_S repack identity and the F32 path, all through
+    this library's GPU kernels."""
+    out = run([program("test-qwen38-quant-hip")])
+    assert out.returncode == 0, out.stderr
+    assert "qwen38 quant: ok" in out.stdout

@@ -1,10 +1,11 @@
-"""Drop-in link test of the model ABI, CPU only: the reference's own CLI and
-model probes (src/cli/qwen38_main.c, qwen38_spec_bench.c, qwen38_spec_probe.c,
-qwen38_mtp_probe.c, qwen38_batch_probe.c, qwen38_forward_probe.c,
-qwen38_logits_probe.c), compiled from its sources by oracle/Makefile and
-linked against libq38hip.so in place of its model and kernel objects, link
-with no unresolved symbol, and the reference's model header and
-include/q38model.h declare the same functions.  Needs the reference sources
+"""Drop-in link test of the model and kernel ABIs, CPU only: the reference's
+own CLI and model probes (src/cli/qwen38_main.c, qwen38_spec_bench.c,
+qwen38_spec_probe.c, qwen38_mtp_probe.c, qwen38_batch_probe.c,
+qwen38_forward_probe.c, qwen38_logits_probe.c) and its kernel unit test
+(tests/unit/test_qwen38_quant.c), compiled from its sources by
+oracle/Makefile and linked against libq38hip.so in place of its model and
+kernel objects, link with no unresolved symbol, and the reference's model
+header and include/q38model.h declare the same functions.  Needs the reference sources
 (this container); the GPU run of the linked probes is in
 tests/test_gpu_reference_probes.py."""
 import os
@@ -16,7 +17,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 REF = "/root/reference"
 REF_DIR = os.path.join(ROOT, "oracle", "_ref")
 LINKED = ["qwen38-hip"] + ["qwen38-%s-hip" % p for p in
-                           ("spec-bench", "spec-probe", "mtp-probe", "batch-probe", "forward-probe", "logits-probe")]
+                           ("spec-bench", "spec-probe", "mtp-probe", "batch-probe", "forward-probe", "logits-probe")] + \
+    ["test-qwen38-quant-hip"]
 
 pytestmark = pytest.mark.skipif(not os.path.isdir(os.path.join(REF, "src", "cli")),
                                 reason="reference sources not present")
