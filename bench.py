@@ -272,12 +272,10 @@ def trace_summary(directory, transactions=0):
         names = [r["short"] for r in rows]
         prefill = ("gemm_q4k_wide", "gemm_iq1m_wide", "gemm_q4k_tiled<8", "gemm_q4k_t32<8", "gemm_iq1m_mfma<8")
         first = max(i for i, n in enumerate(names) if n.startswith(prefill)) + 1
-        last = min(i for i, n in enumerate(names)
-                   if i >= first and (n.startswith("repack_q4k_tiles") or n.startswith("quantize_q8k_kernel")))
+        # the decode ends with the last transaction's acceptance kernel (the
+        # roofline runs that follow launch none); the wall clock stops there
+        last = max(i for i, n in enumerate(names) if n.startswith("accept_kernel")) + 1
         rows = rows[first:last]
-        # the wall clock stops at the last transaction's acceptance kernel:
-        # host work (the CPU baseline) may separate it from the roofline run
-        rows = rows[:max(i for i, r in enumerate(rows) if r["short"].startswith("accept_kernel")) + 1]
         wall =int(rows[-1]["End_Timestamp"]) - int(rows[0]["Start_Timestamp"])
         busy = sum(r["ns"] for r in rows)
         print("%d dispatches over %d transactions: %.3f ms wall and %.3f ms kernel time per transaction"

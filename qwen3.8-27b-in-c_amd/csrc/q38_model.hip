@@ -520,7 +520,7 @@ constexpr int kAttnHeads = 24, kKVHeads = 4, kAttnDim = 256, kKVDim = 1024, kQDi
 constexpr int kScoreChunk = 64;
 /* q heads per lane in the score kernel (more heads: fewer wavefronts, more
  * independent chains per lane) */
-constexpr int kScoreHeadsPerLane = 2;
+constexpr int kScoreHeadsPerLane = 6;
 constexpr int kMaxLdsPositions = 32768;   /* softmax weights kept in LDS up to this many positions */
 constexpr int kAttnLoadBatch = 32;        /* value-cache loads in flight per thread */
 constexpr int kScoreLoads = 32;           /* float4 key loads in flight per lane */
@@ -575,18 +575,24 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float *__restrict__ q_ou
     else kc[h * kAttnDim + i] = y;
 }
 
-/* Attention scores of row t (blockIdx.z) for HPL of the six q heads sharing
- * a KV head (head group blockIdx.x), positions blockIdx.y*64 .. +63 (one per
- * lane): score = fmaf-chain over the 256 dims in order, times 1/16
- * (qwen38_model.c:854-862).  Each lane reads its K row once for HPL
- * independent chains.  scores is [rows][24][context]. */
+/* Attention scores of one row for HPL of the six q heads sharing a KV head,
+ * 64 positions per workgroup (one per lane): score = fmaf-chain over the 256
+ * dims in order, times 1/16 (qwen38_model.c:854-862).  Each lane reads its K
+ * row once for HPL independent chains.  scores is [rows][24][context].
+ * Workgroups go to the eight XCDs round-robin; XCD x = blockIdx.x % 8 takes
+ * KV head x / 2 and every other position chunk of it (chunk parity x % 2),
+ * so the key rows of a KV head are read into two L2s only. */
 template <int HPL>
 __global__ __launch_bounds__(64) void attn_scores_kernel(float *__restrict__ scores, const float *__restrict__ q,
                                                          const float *__restrict__ key_cache, int context,
                                                          const uint32_t *__restrict__ position_ptr)
 {
     constexpr int kGroups = 6 / HPL;   /* head groups per KV head */
-    const int hg = blockIdx.x, chunk = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, lane = threadIdx.x;
+    const int half_chunks = ((context + kScoreChunk - 1) / kScoreChunk + 1) / 2;
+    const int hg = (xcd >> 1) * kGroups + slot % kGroups;
+    const int chunk = 2 * ((slot / kGroups) % half_chunks) + (xcd & 1);
+    const int t = slot / (kGroups * half_chunks);
     const int kvh = hg / kGroups, h0 = kvh * 6 + (hg % kGroups) * HPL;
     const int n = (int)*position_ptr + t + 1;
     if (chunk * kScoreChunk >= n) return;
@@ -818,9 +824,12 @@ void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_
 {
     attn_prep_kernel<<<dim3(kAttnHeads + kKVHeads + 1, rows), 256, 0, stream>>>(
         q_buf, q_and_gate, key, value, in_stride, q_norm, k_norm, rope, key_cache, value_cache, position, 0);
-    attn_scores_kernel<kScoreHeadsPerLane>
-        <<<dim3(kKVHeads * 6 / kScoreHeadsPerLane, (context + kScoreChunk - 1) / kScoreChunk, rows), 64, 0, stream>>>(
-            scores, q_buf, key_cache, context, position);
+    {
+        const int half_chunks = ((context + kScoreChunk - 1) / kScoreChunk + 1) / 2;
+        attn_scores_kernel<kScoreHeadsPerLane>
+            <<<dim3(8 * (6 / kScoreHeadsPerLane) * half_chunks * rows), 64, 0, stream>>>(scores, q_buf, key_cache,
+                                                                                        context, position);
+    }
     if (context <= kMaxLdsPositions)
         attn_output_kernel<true><<<dim3(kAttnHeads, rows), 256, (size_t)context * 4, stream>>>(
             attn, q_out, scores, q_and_gate, in_stride, value_cache, context, position);

@@ -7,8 +7,9 @@ Bar: bit-identical outputs, K/V cache rows and Q8_K blocks of the output.
 Cases: the 2048-token cache of a verify block with M = 1..5 rows (the last
 row at position 2047), a 5124-token cache with 5 rows at positions
 4096-4100 and 5119-5123, short contexts across the 32-position batches of
-the output kernel, and a context above 32768 positions, where the softmax
-weights stay in the scores buffer instead of LDS."""
+the output kernel, a 12-row prefill batch, and a context above 32768
+positions, where the softmax weights stay in the scores buffer instead of
+LDS."""
 import numpy as np
 import pytest
 
@@ -27,6 +28,7 @@ CASES = [
     (2048, 2043, 5),
     (5124, 4096, 5),
     (5124, 5119, 5),
+    (700, 600, 12),
     (40000, 60, 3),
 ]
 
