@@ -209,7 +209,7 @@ int q38hip_gemm_q8_k_tiled(float *output, const Q38Q8KBlock *input,
  *     are written;
  *   attention: [rows][6144] gated output; attention_q8k (optional, may be
  *     NULL): its Q8_K blocks [rows][24], the input of the output projection.
- * All pointers are device pointers.  position + rows <= context_length.
+ * All pointers are device pointers.  position + rows <= context_length <= 524287.
  * Allocates and frees its working buffers (the RoPE table of the context,
  * the scores) and synchronises `stream` before returning. */
 int q38hip_attention_rows(float *attention, Q38Q8KBlock *attention_q8k, const float *q_and_gate,

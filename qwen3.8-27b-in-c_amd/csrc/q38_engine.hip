@@ -1490,6 +1490,10 @@ extern "C" {
 Q38Model *q38_model_open_gguf(const char *path, uint32_t context_length)
 {
     if (!path || context_length == 0) return nullptr;
+    if (context_length > q38::kMaxAttentionContext) {
+        report("context length above 524287 positions");
+        return nullptr;
+    }
     Q38Model *m = new Q38Model();
     m->context_length = context_length;
     bool ok = m->gguf.open(path) && validate_base(m) &&

@@ -141,7 +141,11 @@ bool launch_deltanet_fused(float *attn, float *delta_state, long long slot_strid
 void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, long long z_stride, const float *ssm_norm,
                                int rows, hipStream_t stream);
 /* full attention over `rows` rows at positions *position + t: prep (norms,
- * RoPE, K/V write), scores, softmax + V + gate + Q8_K of the output */
+ * RoPE, K/V write), scores, softmax, V + gate, Q8_K of the output.
+ * configure_attention(context) sets the kernels up for a context length on
+ * the current device; false for a context above kMaxAttentionContext (the
+ * value stream addresses a layer's cache with 32-bit byte offsets). */
+constexpr uint32_t kMaxAttentionContext = 524287;
 bool configure_attention(int context);
 /* host: the RoPE cos/sin table of positions [0, context), 64 floats each */
 void rope_table_host(float *table, uint32_t context);

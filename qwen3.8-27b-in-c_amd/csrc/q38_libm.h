@@ -87,13 +87,10 @@ __device__ static const double q38_logf_table_dev[16][2] = Q38_LOGF_TABLE;
 static const uint64_t q38_exp2_table_host[32] = Q38_EXP2_TABLE;
 static const double q38_logf_table_host[16][2] = Q38_LOGF_TABLE;
 
-Q38_LIBM_FN float q38_expf(float x)
+/* q38_expf with the 2^(i/32) table at `tab` (a copy of Q38_EXP2_TABLE, for
+ * instance in LDS) */
+Q38_LIBM_FN float q38_expf_table(float x, const uint64_t *tab)
 {
-#if defined(__HIP_DEVICE_COMPILE__)
-    const uint64_t *tab = q38_exp2_table_dev;
-#else
-    const uint64_t *tab = q38_exp2_table_host;
-#endif
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32;
     const double shift = 0x1.8p+52;
     /* 2^(r/32) ~ 1 + c2 r + c1 r^2 + c0 r^3 (coefficients pre-scaled by 1/32) */
@@ -125,6 +122,15 @@ Q38_LIBM_FN float q38_expf(float x)
     y = __builtin_fma(z, r2, y);
     y = y * s;
     return (float)y;
+}
+
+Q38_LIBM_FN float q38_expf(float x)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    return q38_expf_table(x, q38_exp2_table_dev);
+#else
+    return q38_expf_table(x, q38_exp2_table_host);
+#endif
 }
 
 Q38_LIBM_FN float q38_logf(float x)

@@ -522,8 +522,8 @@ constexpr int kScoreChunk = 64;
  * independent chains per lane) */
 constexpr int kScoreHeadsPerLane = 6;
 constexpr int kMaxLdsPositions = 32768;   /* softmax weights kept in LDS up to this many positions */
-constexpr int kAttnLoadBatch = 32;        /* value-cache loads in flight per thread */
-constexpr int kScoreLoads = 32;           /* float4 key loads in flight per lane */
+constexpr int kAttnLoadBatch = 32;        /* softmax weights read ahead of the denominator's adds */
+constexpr int kSoftmaxPad = 64;           /* LDS floats past the context in the softmax kernel */
 
 /* q / gate split, per-head RMSNorm of q and k (q_norm / k_norm weights),
  * RoPE on dims 0..63 (pairs i, i+32) and the K/V cache write
@@ -596,113 +596,322 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(float *__restrict__ sco
     const int kvh = hg / kGroups, h0 = kvh * 6 + (hg % kGroups) * HPL;
     const int n = (int)*position_ptr + t + 1;
     if (chunk * kScoreChunk >= n) return;
-    __shared__ float qs[HPL][kAttnDim];
-    const float *qsrc = q + (size_t)t * kQDim + h0 * kAttnDim;
-    for (int e = lane; e < HPL * kAttnDim; e += 64) qs[e >> 8][e & 255] = qsrc[e];
-    __syncthreads();
+    __shared__ float4 qs4[HPL * kAttnDim / 4];
+    /* the lane's key row (position p; lanes past n read row n - 1 and store
+     * nothing) in two halves of 32 quads, each requested at once; the first
+     * half before the q heads are staged */
     const int p = chunk * kScoreChunk + lane;
-    if (p >= n) return;
-    const float4 *k4 = reinterpret_cast<const float4 *>(key_cache + (size_t)p * kKVDim + kvh * kAttnDim);
+    const float4 *k4 =
+        reinterpret_cast<const float4 *>(key_cache + (size_t)(p < n ? p : n - 1) * kKVDim + kvh * kAttnDim);
+    constexpr int kHalfRow = kAttnDim / 8;
+    float4 kk[kHalfRow];
+#pragma unroll
+    for (int m = 0; m < kHalfRow; ++m) kk[m] = k4[m];
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        const float4 *q4 = reinterpret_cast<const float4 *>(q + (size_t)t * kQDim + h0 * kAttnDim);
+        float4 qv[HPL];
+#pragma unroll
+        for (int j = 0; j < HPL; ++j) qv[j] = q4[lane + 64 * j];
+#pragma unroll
+        for (int j = 0; j < HPL; ++j) qs4[lane + 64 * j] = qv[j];
+    }
+    __syncthreads();
     float acc[HPL];
     for (int j = 0; j < HPL; ++j) acc[j] = 0.0f;
-    /* the chain runs over d in order; kScoreLoads float4 of the key row are
-     * loaded together */
-    for (int c = 0; c < 64 / kScoreLoads; ++c) {
-        float4 kk[kScoreLoads];
+    /* the chain runs over d in order */
+    for (int c = 0; c < 2; ++c) {
+        if (c == 1) {
 #pragma unroll
-        for (int m = 0; m < kScoreLoads; ++m) kk[m] = k4[c * kScoreLoads + m];
+            for (int m = 0; m < kHalfRow; ++m) kk[m] = k4[kHalfRow + m];
+            __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
-        for (int m = 0; m < kScoreLoads; ++m) {
+        for (int m = 0; m < kHalfRow; ++m) {
             const float kv[4] = {kk[m].x, kk[m].y, kk[m].z, kk[m].w};
             for (int e = 0; e < 4; ++e) {
-                const int d = (c * kScoreLoads + m) * 4 + e;
-                for (int j = 0; j < HPL; ++j) acc[j] = __builtin_fmaf(qs[j][d], kv[e], acc[j]);
+                const int d = (c * kHalfRow + m) * 4 + e;
+                for (int j = 0; j < HPL; ++j)
+                    acc[j] = __builtin_fmaf(reinterpret_cast<const float *>(qs4)[j * kAttnDim + d], kv[e], acc[j]);
             }
         }
     }
+    if (p >= n) return;
     for (int j = 0; j < HPL; ++j)
         scores[((size_t)t * kAttnHeads + h0 + j) * context + p] = __fmul_rn(acc[j], 0.0625f);
 }
 
-/* Softmax and weighted sum of V for q head blockIdx.x of row blockIdx.y
- * (qwen38_model.c:863-882): maximum; e_p = expf(score_p - max); denominator
- * summed in position order; out_i = fmaf-chain over positions of
- * (e_p / denominator) * v_p[i]; out_i *= sigmoid(gate_i); then Q8_K of the
- * head's 256 outputs (one block of the out-projection input).  IN_LDS: the
- * softmax weights live in dynamic LDS (context <= 32768), else in place in
- * the scores row. */
+/* Softmax of q head blockIdx.x of row blockIdx.y (qwen38_model.c:863-876):
+ * maximum over the scores (the reference's running max from -inf, which
+ * NaN never wins); e_p = expf(score_p - max); the denominator summed in
+ * position order; then the probability e_p / denominator of every position
+ * written over its score, the input of attn_mix_kernel.  IN_LDS: the e_p
+ * are staged in dynamic LDS for the sequential sum (context <= 32768),
+ * otherwise they live in the scores row itself. */
 template <bool IN_LDS>
-__global__ __launch_bounds__(256) void attn_output_kernel(float *__restrict__ out, uint8_t *__restrict__ q_out,
-                                                          float *__restrict__ scores,
-                                                          const float *__restrict__ q_and_gate, long long qg_stride,
-                                                          const float *__restrict__ value_cache, int context,
-                                                          const uint32_t *__restrict__ position_ptr)
+__global__ __launch_bounds__(256) void attn_softmax_kernel(float *__restrict__ scores, int context,
+                                                           const uint32_t *__restrict__ position_ptr)
 {
-    extern __shared__ float lds_e[];
+    extern __shared__ __attribute__((aligned(16))) float lds_e[];
     __shared__ float red[4];
     __shared__ float den_s;
-    __shared__ float ybuf[kAttnDim];
+    __shared__ uint64_t exp_tab[32];
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    const int kvh = h / (kAttnHeads / kKVHeads);
     const int n = (int)*position_ptr + t + 1;
     float *sc = scores + ((size_t)t * kAttnHeads + h) * context;
     float *e = IN_LDS ? lds_e : sc;
+    /* maximum: eight score loads in flight per thread; with IN_LDS the
+     * scores are kept in LDS for the exponentials */
     float local_max = -__builtin_inff();
-    for (int p = tid; p < n; p += 256) {
-        const float v = sc[p];
-        if (IN_LDS) e[p] = v;
+    int p0 = tid;
+    for (; p0 + 256 * 7 < n; p0 += 256 * 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = sc[p0 + 256 * k];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (IN_LDS) e[p0 + 256 * k] = v[k];
+            local_max = fmaxf(local_max, v[k]);
+        }
+    }
+    for (; p0 < n; p0 += 256) {
+        const float v = sc[p0];
+        if (IN_LDS) e[p0] = v;
         local_max = fmaxf(local_max, v);
     }
-    /* the reference's running max (score > maximum from -inf) equals the
-     * max over non-NaN scores; NaN scores never win */
     for (int off = 32; off > 0; off >>= 1) local_max = fmaxf(local_max, __shfl_xor(local_max, off, 64));
     if ((tid & 63) == 0) red[tid >> 6] = local_max;
+    if (tid < 32) exp_tab[tid] = q38_exp2_table_dev[tid];
     __syncthreads();
     const float maximum = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int p = tid; p < n; p += 256) e[p] = q38_expf(__fsub_rn(e[p], maximum));
+    for (int p = tid; p < n; p += 256) e[p] = q38_expf_table(__fsub_rn(IN_LDS ? e[p] : sc[p], maximum), exp_tab);
     __syncthreads();
     if (tid == 0) {
         float d = 0.0f;
         int p = 0;
-        /* position order; the weights of kAttnLoadBatch positions are read
-         * ahead of their adds */
-        for (; p + kAttnLoadBatch <= n; p += kAttnLoadBatch) {
-            float a[kAttnLoadBatch];
+        if (IN_LDS) {
+            /* position order, 32 weights per batch as 8 quads, three
+             * batches in registers: batch c + 2 is read while batch c is
+             * added, one LDS read between every four adds (the LDS row has
+             * kSoftmaxPad floats past the context, so the read-ahead past
+             * the last batch stays inside it) */
+            const float4 *e4 = reinterpret_cast<const float4 *>(e);
+            const int full = n / 32;
+            float4 q0[8], q1[8], q2[8];
+            auto step = [&d, e4](const float4 *cur, float4 *ahead, int batch) {
 #pragma unroll
-            for (int k = 0; k < kAttnLoadBatch; ++k) a[k] = e[p + k];
+                for (int k = 0; k < 8; ++k) {
+                    ahead[k] = e4[8 * batch + k];
+                    d = __fadd_rn(d, cur[k].x);
+                    d = __fadd_rn(d, cur[k].y);
+                    d = __fadd_rn(d, cur[k].z);
+                    d = __fadd_rn(d, cur[k].w);
+                }
 #pragma unroll
-            for (int k = 0; k < kAttnLoadBatch; ++k) d = __fadd_rn(d, a[k]);
+                for (int k = 0; k < 8; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                }
+            };
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                q0[k] = e4[k];
+                q1[k] = e4[8 + k];
+            }
+            for (int c = 0; c < full; c += 3) {
+                step(q0, q2, c + 2);
+                if (c + 1 >= full) break;
+                step(q1, q0, c + 3);
+                if (c + 2 >= full) break;
+                step(q2, q1, c + 4);
+            }
+            p = 32 * full;
+        } else {
+            /* position order; the weights of kAttnLoadBatch positions are
+             * read ahead of their adds */
+            for (; p + kAttnLoadBatch <= n; p += kAttnLoadBatch) {
+                float a[kAttnLoadBatch];
+#pragma unroll
+                for (int k = 0; k < kAttnLoadBatch; ++k) a[k] = e[p + k];
+#pragma unroll
+                for (int k = 0; k < kAttnLoadBatch; ++k) d = __fadd_rn(d, a[k]);
+            }
         }
         for (; p < n; ++p) d = __fadd_rn(d, e[p]);
         den_s = d;
     }
     __syncthreads();
     const float denominator = den_s;
-    for (int p = tid; p < n; p += 256) e[p] = div_rn(e[p], denominator);
-    __syncthreads();
-    /* the chain runs in position order; the V loads of kAttnLoadBatch
-     * positions are issued together, so a round trip to memory covers that
-     * many links */
-    const float *vcol = value_cache + kvh * kAttnDim + tid;
+    for (int p = tid; p < n; p += 256) sc[p] = div_rn(e[p], denominator);
+}
+
+/* Weighted sum of V (qwen38_model.c:877-884): out_i = fmaf-chain over the
+ * positions in order of probability_p * v_p[i], then out_i *= sigmoid(gate_i).
+ *
+ * One workgroup per (row, q head, 64-dimension slice), so the chains of a
+ * head are spread over four compute units.  Wavefront 0 runs the chains,
+ * lane i that of dimension 64 * slice + i; wavefront 1 only streams: the
+ * value rows of the slice (256 contiguous bytes per position) and the
+ * probabilities go through an LDS ring of kMixSlots chunks of kMixChunk
+ * positions, written by the load unit itself (buffer loads with the LDS
+ * flag), up to kMixSlots - 1 chunks ahead.  One barrier per chunk: at
+ * barrier c, chunk c + 1 has landed and the chain wavefront has consumed
+ * chunk c - 1, whose slot the streaming wavefront then refills; the chain
+ * wavefront reads chunk c + 1 into registers while it runs the links of
+ * chunk c.  Both buffer resources end at position n, so the positions of
+ * the last chunk past n read as zero and their links fmaf(0, 0, o) leave
+ * the chain unchanged (o is never -0: it starts at +0 and an exact zero sum
+ * rounds to +0).
+ *
+ * Workgroups go to the eight XCDs round-robin: XCD x = blockIdx.x % 8 takes
+ * KV head x / 2 and the slice pair x % 2, so the value rows a KV head's
+ * heads read stay in two L2s. */
+constexpr int kMixChunk = 32;                              /* positions per ring slot */
+constexpr int kMixSlots = 8;                               /* ring slots */
+constexpr int kMixVOps = kMixChunk / 4;                    /* 1 KiB value loads per chunk */
+constexpr int kMixOps = kMixVOps + 1;                      /* + one load of 64 probabilities */
+constexpr int kMixSlotBytes = kMixChunk * 256 + 256;
+constexpr int kMixLdsBytes = kMixSlots * kMixSlotBytes;
+static_assert(kMixOps * (kMixSlots - 1) <= 63, "loads in flight within the vmcnt range");
+constexpr uint32_t kMixRawBuffer = 0x00020000u;   /* raw 32-bit buffer resource (gfx9) */
+
+__device__ __forceinline__ uint32_t lds_address(const void *p)
+{
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+}
+
+/* chunk c into the ring slot at LDS address `slot`: kMixVOps value loads
+ * (lane i: position 32c + 4j + i / 16, dimensions 4 (i % 16) .. + 3 of the
+ * slice, landing at slot + 1024 j + 16 i, i.e. [position][64 dimensions])
+ * and one probability load (lane i: position 32c + i, at slot + 8192 + 4 i).
+ * Inline assembly, so the compiler's wait-count pass does not treat the
+ * loads as LDS stores. */
+__device__ __forceinline__ void mix_load_chunk(__amdgpu_buffer_rsrc_t vr, __amdgpu_buffer_rsrc_t pr, uint32_t v_lane,
+                                               int c, uint32_t slot, int lane)
+{
+#pragma unroll
+    for (int j = 0; j < kMixVOps; ++j) {
+        const uint32_t voff = v_lane + (uint32_t)(kMixChunk * c + 4 * j) * (kKVDim * 4);
+        asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
+                     :: "v"(voff), "s"(slot + 1024 * j), "s"(vr) : "memory", "m0");
+    }
+    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, 0 offen lds"
+                 :: "v"((uint32_t)(kMixChunk * c + lane) * 4u), "s"(slot + kMixChunk * 256), "s"(pr)
+                 : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void mix_wait_vmcnt()
+{
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+__device__ __forceinline__ void mix_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+/* half a chunk of the ring (16 positions) in registers: v[k] = value of
+ * position k in this lane's dimension, pr = the probabilities */
+constexpr int kMixHalf = kMixChunk / 2;
+struct MixHalf {
+    float v[kMixHalf];
+    float4 pr[kMixHalf / 4];
+};
+
+/* 12 LDS reads (8 two-position value reads, 4 probability quads) */
+__device__ __forceinline__ void mix_read(MixHalf &r, const uint8_t *slot, int half, int lane)
+{
+    const float *vs = reinterpret_cast<const float *>(slot) + half * kMixHalf * 64;
+    const float4 *ps = reinterpret_cast<const float4 *>(slot + kMixChunk * 256) + half * (kMixHalf / 4);
+#pragma unroll
+    for (int k = 0; k < kMixHalf / 4; ++k) r.pr[k] = ps[k];
+#pragma unroll
+    for (int k = 0; k < kMixHalf; ++k) r.v[k] = vs[k * 64 + lane];
+}
+
+__device__ __forceinline__ float mix_links(const MixHalf &r, float o)
+{
+#pragma unroll
+    for (int k = 0; k < kMixHalf / 4; ++k) {
+        o = __builtin_fmaf(r.pr[k].x, r.v[4 * k], o);
+        o = __builtin_fmaf(r.pr[k].y, r.v[4 * k + 1], o);
+        o = __builtin_fmaf(r.pr[k].z, r.v[4 * k + 2], o);
+        o = __builtin_fmaf(r.pr[k].w, r.v[4 * k + 3], o);
+    }
+    return o;
+}
+
+/* the chain over chunk c (halves a0, a1, read earlier) while chunk c + 1
+ * (landed at this chunk's barrier) is read into b0, b1: each half's links
+ * wait only for that half's 12 reads, the other half's stay in flight.
+ * After the last chunk the reads take a stale slot and are never used. */
+__device__ __forceinline__ float mix_step(float o, const MixHalf &a0, const MixHalf &a1, MixHalf &b0, MixHalf &b1,
+                                          const uint8_t *next_slot, int lane)
+{
+    mix_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    o = mix_links(a0, o);
+    __builtin_amdgcn_sched_barrier(0);
+    mix_read(b0, next_slot, 0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    o = mix_links(a1, o);
+    __builtin_amdgcn_sched_barrier(0);
+    mix_read(b1, next_slot, 1, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    return o;
+}
+
+__global__ __launch_bounds__(128) void attn_mix_kernel(float *__restrict__ out, const float *__restrict__ prob,
+                                                       const float *__restrict__ q_and_gate, long long qg_stride,
+                                                       const float *__restrict__ value_cache, int context,
+                                                       const uint32_t *__restrict__ position_ptr)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kMixLdsBytes];
+    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3, lane = threadIdx.x & 63;
+    const int kvh = xcd >> 1, slice = 2 * (xcd & 1) + ((j / 6) & 1);
+    const int h = kvh * 6 + j % 6, t = j / 12;
+    const int n = (int)*position_ptr + t + 1;
+    const int chunks = (n + kMixChunk - 1) / kMixChunk;
+    if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) == 1) {
+        /* streaming wavefront */
+        const __amdgpu_buffer_rsrc_t vr =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(value_cache), 0, n * kKVDim * 4, kMixRawBuffer);
+        const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(prob + ((size_t)t * kAttnHeads + h) * context), 0, n * 4, kMixRawBuffer);
+        const uint32_t v_lane = (uint32_t)(lane >> 4) * (kKVDim * 4) +
+                                (uint32_t)(kvh * kAttnDim + 64 * slice) * 4 + (uint32_t)(lane & 15) * 16;
+        const uint32_t ring_base = __builtin_amdgcn_readfirstlane(lds_address(ring));
+#pragma unroll
+        for (int c = 0; c < kMixSlots - 1; ++c)
+            mix_load_chunk(vr, pr, v_lane, c, ring_base + c * kMixSlotBytes, lane);
+        /* loads retire in order */
+        mix_wait_vmcnt<kMixOps * (kMixSlots - 2)>();   /* chunk 0 */
+        mix_barrier();
+#pragma unroll 1
+        for (int c = 0; c < chunks; ++c) {
+            mix_wait_vmcnt<kMixOps * (kMixSlots - 3)>();   /* chunk c + 1 */
+            mix_barrier();
+            /* chunk c - 1 is consumed: its slot takes chunk c + kMixSlots - 1
+             * (past the end: every lane out of range, nothing read) */
+            mix_load_chunk(vr, pr, v_lane, c + kMixSlots - 1,
+                           ring_base + ((c + kMixSlots - 1) % kMixSlots) * kMixSlotBytes, lane);
+        }
+        mix_wait_vmcnt<0>();
+        return;
+    }
+    /* chain wavefront: one barrier per chunk, as the streaming wavefront */
+    MixHalf a0, a1, b0, b1;
+    mix_barrier();
+    mix_read(a0, ring, 0, lane);
+    mix_read(a1, ring, 1, lane);
     float o = 0.0f;
-    int p = 0;
-    for (; p + kAttnLoadBatch <= n; p += kAttnLoadBatch) {
-        float vv[kAttnLoadBatch];
-#pragma unroll
-        for (int k = 0; k < kAttnLoadBatch; ++k) vv[k] = vcol[(size_t)(p + k) * kKVDim];
-#pragma unroll
-        for (int k = 0; k < kAttnLoadBatch; ++k) o = __builtin_fmaf(e[p + k], vv[k], o);
+#pragma unroll 1
+    for (int c = 0; c < chunks; c += 2) {
+        o = mix_step(o, a0, a1, b0, b1, ring + ((c + 1) % kMixSlots) * kMixSlotBytes, lane);
+        if (c + 1 >= chunks) break;
+        o = mix_step(o, b0, b1, a0, a1, ring + ((c + 2) % kMixSlots) * kMixSlotBytes, lane);
     }
-    for (; p < n; ++p) o = __builtin_fmaf(e[p], vcol[(size_t)p * kKVDim], o);
-    const float g = q_and_gate[(size_t)t * qg_stride + h * 2 * kAttnDim + kAttnDim + tid];
-    const float y = __fmul_rn(o, sigmoidf_exact(g));
-    out[(size_t)t * kQDim + h * kAttnDim + tid] = y;
-    ybuf[tid] = y;
-    __syncthreads();
-    if (tid < 64) {
-        const float q4[4] = {ybuf[4 * tid], ybuf[4 * tid + 1], ybuf[4 * tid + 2], ybuf[4 * tid + 3]};
-        wave_quantize_q8k(q4, q_out + ((size_t)t * kAttnHeads + h) * kQ8KBytes, tid);
-    }
+    const int dim = h * kAttnDim + 64 * slice + lane;
+    const float g = q_and_gate[(size_t)t * qg_stride + h * 2 * kAttnDim + kAttnDim + 64 * slice + lane];
+    out[(size_t)t * kQDim + dim] = __fmul_rn(o, sigmoidf_exact(g));
 }
 
 /* ---- launchers ----------------------------------------------------------- */
@@ -779,7 +988,7 @@ void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, long
     deltanet_out_quant_kernel<<<dim3(kVHeads / 2, rows), 256, 0, stream>>>(attn, q_out, z, z_stride, ssm_norm);
 }
 
-/* The dynamic-LDS limit of the in-LDS output kernel is a per-device
+/* The dynamic-LDS limit of the in-LDS softmax kernel is a per-device
  * attribute of the function: it only ever grows, to the largest context
  * configured so far on the device, so a later model or call with a smaller
  * context never lowers it under an earlier one. */
@@ -787,14 +996,15 @@ bool configure_attention(int context)
 {
     static std::mutex mutex;
     static std::vector<int> configured;
+    if (context < 1 || (uint32_t)context > kMaxAttentionContext) return false;
     if (context > kMaxLdsPositions) return true;
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) return false;
     std::lock_guard<std::mutex> lock(mutex);
     if ((int)configured.size() <= device) configured.resize(device + 1, 0);
     if (context <= configured[device]) return true;
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_output_kernel<true>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, context * 4) != hipSuccess)
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_softmax_kernel<true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (context + kSoftmaxPad) * 4) != hipSuccess)
         return false;
     configured[device] = context;
     return true;
@@ -831,11 +1041,13 @@ void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_
                                                                                         context, position);
     }
     if (context <= kMaxLdsPositions)
-        attn_output_kernel<true><<<dim3(kAttnHeads, rows), 256, (size_t)context * 4, stream>>>(
-            attn, q_out, scores, q_and_gate, in_stride, value_cache, context, position);
+        attn_softmax_kernel<true><<<dim3(kAttnHeads, rows), 256, (size_t)(context + kSoftmaxPad) * 4, stream>>>(scores, context,
+                                                                                              position);
     else
-        attn_output_kernel<false><<<dim3(kAttnHeads, rows), 256, 0, stream>>>(
-            attn, q_out, scores, q_and_gate, in_stride, value_cache, context, position);
+        attn_softmax_kernel<false><<<dim3(kAttnHeads, rows), 256, 0, stream>>>(scores, context, position);
+    attn_mix_kernel<<<dim3(8 * 12 * rows), 128, 0, stream>>>(attn, scores, q_and_gate, in_stride, value_cache, context,
+                                                            position);
+    launch_quantize(attn, q_out, (uint32_t)(rows * kAttnHeads), stream);
 }
 
 void launch_kv_write(const float *key, const float *value, long long in_stride, const float *k_norm,

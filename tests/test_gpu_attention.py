@@ -1,15 +1,16 @@
 """Full-attention decode core on the GPU (q38hip_attention_rows: the engine's
-attention prep, score and output kernels) against the oracle's
-orc_attention_decode, which is pinned to the reference's own q38_full_core
-(src/qwen38/qwen38_model.c:816-885; tests/test_oracle_pins.py).
+attention prep, score, softmax, value-mix and Q8_K kernels) against the
+oracle's orc_attention_decode, which is pinned to the reference's own
+q38_full_core (src/qwen38/qwen38_model.c:816-885; tests/test_oracle_pins.py).
 
 Bar: bit-identical outputs, K/V cache rows and Q8_K blocks of the output.
 Cases: the 2048-token cache of a verify block with M = 1..5 rows (the last
 row at position 2047), a 5124-token cache with 5 rows at positions
-4096-4100 and 5119-5123, short contexts across the 32-position batches of
-the output kernel, a 12-row prefill batch, and a context above 32768
-positions, where the softmax weights stay in the scores buffer instead of
-LDS."""
+4096-4100 and 5119-5123, contexts of 1..66 positions around the 32-position
+chunks of the value stream, a 12-row prefill batch, a 16384-token cache,
+and a context above 32768 positions, where the softmax weights stay in the
+scores buffer instead of LDS.  Cache rows past the last row's position hold
+NaN, so a kernel that read them would fail the comparison."""
 import numpy as np
 import pytest
 
@@ -29,6 +30,10 @@ CASES = [
     (5124, 4096, 5),
     (5124, 5119, 5),
     (700, 600, 12),
+    (40, 0, 2),
+    (80, 30, 4),
+    (80, 62, 4),
+    (16384, 16000, 2),
     (40000, 60, 3),
 ]
 
@@ -45,6 +50,8 @@ def test_attention_rows_bit_exact(device, oracle, context, position, rows):
     import q38hip
     print("attention context=%d position=%d rows=%d" % (context, position, rows), flush=True)
     rows_in, qn, kn, kc, vc = ac.inputs(context, position, rows)
+    kc[position + rows:] = np.nan
+    vc[position + rows:] = np.nan
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
     dk, dv = d(kc), d(vc)
     got, got_q = q38hip.attention_rows(d(rows_in), d(qn), d(kn), dk, dv, position)
