@@ -204,12 +204,14 @@ int q38hip_gemm_q8_k_tiled(float *output, const Q38Q8KBlock *input,
  * of each row, scores, softmax and the sigmoid-gated output.
  *   q_and_gate: row t at t * in_stride floats, 24 heads x (256 q | 256 gate);
  *   key, value: row t at t * in_stride floats, 1024 each;
- *   key_cache, value_cache: [context_length][1024] fp32 (one layer), rows
- *     before `position` already filled; rows position .. position + rows - 1
- *     are written;
+ *   key_cache: [context_length][1024] fp32 (one layer); value_cache:
+ *     channel-major [1024][pitch] fp32 with pitch = context_length rounded
+ *     up to a multiple of 32 (position p of channel e at e * pitch + p);
+ *     positions before `position` already filled, positions position ..
+ *     position + rows - 1 are written;
  *   attention: [rows][6144] gated output; attention_q8k (optional, may be
  *     NULL): its Q8_K blocks [rows][24], the input of the output projection.
- * All pointers are device pointers.  position + rows <= context_length <= 524287.
+ * All pointers are device pointers.  position + rows <= context_length <= 524256.
  * Allocates and frees its working buffers (the RoPE table of the context,
  * the scores) and synchronises `stream` before returning. */
 int q38hip_attention_rows(float *attention, Q38Q8KBlock *attention_q8k, const float *q_and_gate,

@@ -26,7 +26,7 @@ extern "C" {
 typedef struct Q38Model Q38Model;
 
 /* qwen38_model.h:12 (open + upload to HBM; NULL on failure, and for a
- * context_length above 524287 positions) */
+ * context_length above 524256 positions) */
 Q38Model *q38_model_open_gguf(const char *path, uint32_t context_length);
 /* qwen38_model.h:13 */
 int q38_model_attach_mtp_gguf(Q38Model *model, const char *path);

@@ -40,7 +40,7 @@ extern "C" int q38hip_attention_rows(float *attention, Q38Q8KBlock *attention_q8
         return q38::abi_fail("bad attention arguments");
     if (in_stride < kKVDim || (rows > 1 && in_stride < kQGDim)) return q38::abi_fail("row stride too small");
     if ((uint64_t)position + rows > context_length) return q38::abi_fail("position + rows beyond the context");
-    if (context_length > q38::kMaxAttentionContext) return q38::abi_fail("context length above 524287 positions");
+    if (context_length > q38::kMaxAttentionContext) return q38::abi_fail("context length above 524256 positions");
     hipStream_t s = static_cast<hipStream_t>(stream);
     /* drain the caller's earlier work on the stream: the buffers below are
      * released before return */

@@ -607,6 +607,8 @@ void dfree(T *&p)
 size_t conv_count() { return (size_t)kRecurrent * kQKV * 3; }
 size_t delta_count() { return (size_t)kRecurrent * kVHeads * kHeadDim * kHeadDim; }
 size_t kv_count(uint32_t ctx) { return (size_t)kFullLayers * ctx * kKVDim; }
+/* the value cache is channel-major per layer: [1024][value_pitch(ctx)] */
+size_t value_layer_floats(uint32_t ctx) { return (size_t)kKVDim * q38::value_pitch(ctx); }
 
 bool validate_base(Q38Model *m)
 {
@@ -686,7 +688,7 @@ bool allocate_state(Q38Model *m)
     const uint32_t B = m->scratch_rows;
     const size_t slots = q38::kRecurrentStateSlots;
     bool ok = dalloc(&m->conv_state, slots * conv_count()) && dalloc(&m->delta_state, slots * delta_count()) &&
-              dalloc(&m->key_cache, kv_count(ctx)) && dalloc(&m->value_cache, kv_count(ctx)) &&
+              dalloc(&m->key_cache, kv_count(ctx)) && dalloc(&m->value_cache, kFullLayers * value_layer_floats(ctx)) &&
               dalloc(&m->mtp_hidden, kHidden) && dalloc(&m->rope, (size_t)ctx * 64) &&
               dalloc(&m->hidden, (size_t)B * kHidden) && dalloc(&m->norm, (size_t)kBatch * 2 * kHidden) &&
               dalloc(&m->branch, (size_t)B * kHidden) && dalloc(&m->wide0, (size_t)B * 2 * kFFN) &&
@@ -757,7 +759,8 @@ bool clear_state(Q38Model *m)
     return hip_ok(hipMemsetAsync(m->conv_state, 0, conv_count() * sizeof(float), s), "reset") &&
            hip_ok(hipMemsetAsync(m->delta_state, 0, delta_count() * sizeof(float), s), "reset") &&
            hip_ok(hipMemsetAsync(m->key_cache, 0, kv_count(m->context_length) * sizeof(float), s), "reset") &&
-           hip_ok(hipMemsetAsync(m->value_cache, 0, kv_count(m->context_length) * sizeof(float), s), "reset") &&
+           hip_ok(hipMemsetAsync(m->value_cache, 0, kFullLayers * value_layer_floats(m->context_length) * sizeof(float), s),
+                  "reset") &&
            hip_ok(hipMemsetAsync(m->mtp_hidden, 0, kHidden * sizeof(float), s), "reset") &&
            hip_ok(hipStreamSynchronize(s), "reset");
 }
@@ -1040,11 +1043,12 @@ bool full_attention_rows(Q38Model *m, const Step &s, int layer, uint32_t count)
     const Layer &L = m->layers[layer];
     const int full_index = layer / 4;
     const size_t kv_off = (size_t)full_index * m->context_length * kKVDim;
+    const size_t v_off = (size_t)full_index * value_layer_floats(m->context_length);
     /* per row: q+gate [12288] | k [1024] | v [1024] */
     const Group &g = L.mix_in;
     if (!gemm_group(m, g, 0, 3, count, m->wide0, g.width, m->fin)) return false;
     q38::launch_attention(m->attn, m->q8k, m->qbuf, m->wide0, m->wide0 + g.first[1], m->wide0 + g.first[2], g.width,
-                          L.q_norm.f32(), L.k_norm.f32(), m->rope, m->key_cache + kv_off, m->value_cache + kv_off,
+                          L.q_norm.f32(), L.k_norm.f32(), m->rope, m->key_cache + kv_off, m->value_cache + v_off,
                           m->scores, (int)m->context_length, s.params, (int)count, m->stream);
     if (count == 1 && trace_enabled()) {
         uint32_t pos = 0;
@@ -1186,8 +1190,10 @@ bool mtp_catchup(Q38Model *m, const Step &s, uint32_t count)
     const uint32_t ld = g.first[2] + (uint32_t)g.part[2].rows - g.first[1];
     if (!gemm_group(m, g, 1, 3, count, m->wide0, ld, m->fin)) return false;
     const size_t kv_off = (size_t)(kLayers / 4) * m->context_length * kKVDim;
+    const size_t v_off = (size_t)(kLayers / 4) * value_layer_floats(m->context_length);
     q38::launch_kv_write(m->wide0, m->wide0 + (g.first[2] - g.first[1]), ld, L.k_norm.f32(), m->rope,
-                         m->key_cache + kv_off, m->value_cache + kv_off, s.params, (int)count, m->stream);
+                         m->key_cache + kv_off, m->value_cache + v_off, (int)m->context_length, s.params,
+                         (int)count, m->stream);
     return launches_ok() &&
            hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm + (size_t)(count - 1) * kHidden,
                                  kHidden * sizeof(float), hipMemcpyDeviceToDevice, m->stream),
@@ -1491,7 +1497,7 @@ Q38Model *q38_model_open_gguf(const char *path, uint32_t context_length)
 {
     if (!path || context_length == 0) return nullptr;
     if (context_length > q38::kMaxAttentionContext) {
-        report("context length above 524287 positions");
+        report("context length above 524256 positions");
         return nullptr;
     }
     Q38Model *m = new Q38Model();

@@ -142,10 +142,15 @@ void launch_deltanet_out_quant(float *attn, uint8_t *q_out, const float *z, long
                                int rows, hipStream_t stream);
 /* full attention over `rows` rows at positions *position + t: prep (norms,
  * RoPE, K/V write), scores, softmax, V + gate, Q8_K of the output.
- * configure_attention(context) sets the kernels up for a context length on
- * the current device; false for a context above kMaxAttentionContext (the
- * value stream addresses a layer's cache with 32-bit byte offsets). */
-constexpr uint32_t kMaxAttentionContext = 524287;
+ * key_cache of one layer: [context][1024] fp32; value_cache: channel-major
+ * [1024][value_pitch(context)] fp32 (position p of channel e at
+ * e * value_pitch + p), so each chain of the weighted sum reads consecutive
+ * positions.  configure_attention(context) sets the kernels up for a
+ * context length on the current device; false for a context above
+ * kMaxAttentionContext (a layer's value block is addressed with 31-bit byte
+ * offsets). */
+constexpr uint32_t kMaxAttentionContext = 524256;
+__host__ __device__ inline uint32_t value_pitch(uint32_t context) { return (context + 31) & ~31u; }
 bool configure_attention(int context);
 /* host: the RoPE cos/sin table of positions [0, context), 64 floats each */
 void rope_table_host(float *table, uint32_t context);
@@ -155,7 +160,7 @@ void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_
                       const uint32_t *position, int rows, hipStream_t stream);
 /* K-norm, RoPE and K/V cache write of `rows` rows without the query side */
 void launch_kv_write(const float *key, const float *value, long long in_stride, const float *k_norm,
-                     const float *rope, float *key_cache, float *value_cache, const uint32_t *position, int rows,
-                     hipStream_t stream);
+                     const float *rope, float *key_cache, float *value_cache, int context, const uint32_t *position,
+                     int rows, hipStream_t stream);
 
 }  // namespace q38

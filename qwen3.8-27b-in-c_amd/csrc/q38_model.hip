@@ -528,7 +528,8 @@ constexpr int kSoftmaxPad = 64;           /* LDS floats past the context in the 
 /* q / gate split, per-head RMSNorm of q and k (q_norm / k_norm weights),
  * RoPE on dims 0..63 (pairs i, i+32) and the K/V cache write
  * (q38_full_core, qwen38_model.c:816-846; q38_rope :697-713) for row t
- * (blockIdx.y) at position *position_ptr + t.  Blocks 0..23 are q heads,
+ * (blockIdx.y) at position *position_ptr + t; the value row goes into the
+ * channel-major value cache (pitch v_pitch).  Blocks 0..23 are q heads,
  * 24..27 k heads, 28 copies v.  `rope` holds cos (32) then sin (32) per
  * position, computed once on the host with the C library.  `block_base` =
  * 24 runs only the K/V part.  Row t of q_and_gate, key and value starts at
@@ -539,7 +540,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float *__restrict__ q_ou
                                                         const float *__restrict__ q_norm,
                                                         const float *__restrict__ k_norm,
                                                         const float *__restrict__ rope, float *__restrict__ key_cache,
-                                                        float *__restrict__ value_cache,
+                                                        float *__restrict__ value_cache, int v_pitch,
                                                         const uint32_t *__restrict__ position_ptr, int block_base)
 {
     const int t = blockIdx.y;
@@ -548,7 +549,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float *__restrict__ q_ou
     const int block = blockIdx.x + block_base;
     float *kc = key_cache + (size_t)pos * kKVDim;
     if (block == kAttnHeads + kKVHeads) {
-        for (int e = i; e < kKVDim; e += 256) value_cache[(size_t)pos * kKVDim + e] = value[(size_t)t * in_stride + e];
+        for (int e = i; e < kKVDim; e += 256) value_cache[(size_t)e * v_pitch + pos] = value[(size_t)t * in_stride + e];
         return;
     }
     const bool is_q = block < kAttnHeads;
@@ -751,17 +752,17 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(float *__restrict__ s
  * One workgroup per (row, q head, 64-dimension slice), so the chains of a
  * head are spread over four compute units.  Wavefront 0 runs the chains,
  * lane i that of dimension 64 * slice + i; wavefront 1 only streams: the
- * value rows of the slice (256 contiguous bytes per position) and the
- * probabilities go through an LDS ring of kMixSlots chunks of kMixChunk
- * positions, written by the load unit itself (buffer loads with the LDS
- * flag), up to kMixSlots - 1 chunks ahead.  One barrier per chunk: at
- * barrier c, chunk c + 1 has landed and the chain wavefront has consumed
- * chunk c - 1, whose slot the streaming wavefront then refills; the chain
- * wavefront reads chunk c + 1 into registers while it runs the links of
- * chunk c.  Both buffer resources end at position n, so the positions of
- * the last chunk past n read as zero and their links fmaf(0, 0, o) leave
- * the chain unchanged (o is never -0: it starts at +0 and an exact zero sum
- * rounds to +0).
+ * slice's channel rows of the channel-major value cache (128 contiguous
+ * bytes per channel and chunk) and the probabilities go through an LDS ring
+ * of kMixSlots chunks of kMixChunk positions, written by the load unit
+ * itself (buffer loads with the LDS flag), up to kMixSlots - 1 chunks
+ * ahead.  One barrier per chunk: at barrier c, chunk c + 1 has landed and
+ * the chain wavefront has consumed chunk c - 1, whose slot the streaming
+ * wavefront then refills; the chain wavefront reads chunk c + 1 into
+ * registers (four positions of its channel per LDS read) while it runs the
+ * links of chunk c.  The full chunks run through the pipeline; the n % 32
+ * positions of a last, partial chunk are linked one by one, so no position
+ * past n enters a chain.
  *
  * Workgroups go to the eight XCDs round-robin: XCD x = blockIdx.x % 8 takes
  * KV head x / 2 and the slice pair x % 2, so the value rows a KV head's
@@ -769,35 +770,13 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(float *__restrict__ s
 constexpr int kMixChunk = 32;                              /* positions per ring slot */
 constexpr int kMixSlots = 8;                               /* ring slots */
 constexpr int kMixVOps = kMixChunk / 4;                    /* 1 KiB value loads per chunk */
-constexpr int kMixOps = kMixVOps + 1;                      /* + one load of 64 probabilities */
 constexpr int kMixSlotBytes = kMixChunk * 256 + 256;
 constexpr int kMixLdsBytes = kMixSlots * kMixSlotBytes;
-static_assert(kMixOps * (kMixSlots - 1) <= 63, "loads in flight within the vmcnt range");
 constexpr uint32_t kMixRawBuffer = 0x00020000u;   /* raw 32-bit buffer resource (gfx9) */
 
 __device__ __forceinline__ uint32_t lds_address(const void *p)
 {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
-}
-
-/* chunk c into the ring slot at LDS address `slot`: kMixVOps value loads
- * (lane i: position 32c + 4j + i / 16, dimensions 4 (i % 16) .. + 3 of the
- * slice, landing at slot + 1024 j + 16 i, i.e. [position][64 dimensions])
- * and one probability load (lane i: position 32c + i, at slot + 8192 + 4 i).
- * Inline assembly, so the compiler's wait-count pass does not treat the
- * loads as LDS stores. */
-__device__ __forceinline__ void mix_load_chunk(__amdgpu_buffer_rsrc_t vr, __amdgpu_buffer_rsrc_t pr, uint32_t v_lane,
-                                               int c, uint32_t slot, int lane)
-{
-#pragma unroll
-    for (int j = 0; j < kMixVOps; ++j) {
-        const uint32_t voff = v_lane + (uint32_t)(kMixChunk * c + 4 * j) * (kKVDim * 4);
-        asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
-                     :: "v"(voff), "s"(slot + 1024 * j), "s"(vr) : "memory", "m0");
-    }
-    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, 0 offen lds"
-                 :: "v"((uint32_t)(kMixChunk * c + lane) * 4u), "s"(slot + kMixChunk * 256), "s"(pr)
-                 : "memory", "m0");
 }
 
 template <int N>
@@ -808,34 +787,96 @@ __device__ __forceinline__ void mix_wait_vmcnt()
 
 __device__ __forceinline__ void mix_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+/* chunk c into the ring slot at LDS address `slot`: eight value loads and
+ * one probability load.  Value load j: lane i takes channel 8j + i / 8 of
+ * the slice and its positions 32c + 4u .. 32c + 4u + 3 with
+ * u = (i % 8) ^ (i / 8 % 8) ^ (j % 2), landing at slot + 1024 j + 16 i:
+ * channel d's quad u sits at unit 64 (d / 8) + 8 (d % 8) + (u ^ s(d)),
+ * s(d) = (d % 8) ^ (d / 8 % 2), so the chain's reads of one quad of 16
+ * consecutive channels hit 16 different 16-byte bank groups.  v_lane[j] is the
+ * lane's byte offset of its channel and quad in load j; the chunk goes into
+ * the scalar offset, with c clamped to the last chunk holding positions
+ * below n (`last`), so every address stays inside the layer's value block
+ * whatever the range check does with the scalar offset (slots loaded past
+ * the end are never read).  Probability load: lane i takes position
+ * 32c + i, at slot + 8192 + 4 i; that resource ends at position n.  Inline
+ * assembly, so the compiler's wait-count pass does not treat the loads as
+ * LDS stores. */
+__device__ __forceinline__ void mix_load_chunk(__amdgpu_buffer_rsrc_t vr, __amdgpu_buffer_rsrc_t pr,
+                                               const uint32_t (&v_lane)[kMixVOps], uint32_t p_lane, int c, int last,
+                                               uint32_t slot)
+{
+    const uint32_t chunk_off = (uint32_t)(c < last ? c : last) * (kMixChunk * 4);
+#pragma unroll
+    for (int j = 0; j < kMixVOps; ++j)
+        asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, %3 offen lds"
+                     :: "v"(v_lane[j]), "s"(slot + 1024 * j), "s"(vr), "s"(chunk_off) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, 0 offen lds"
+                 :: "v"(p_lane + (uint32_t)c * (kMixChunk * 4)), "s"(slot + kMixChunk * 256), "s"(pr)
+                 : "memory", "m0");
+}
+constexpr int kMixOps = kMixVOps + 1;   /* loads per chunk */
+static_assert(kMixOps * (kMixSlots - 1) <= 63, "loads in flight within the vmcnt range");
+
 /* half a chunk of the ring (16 positions) in registers: v[k] = value of
  * position k in this lane's dimension, pr = the probabilities */
 constexpr int kMixHalf = kMixChunk / 2;
 struct MixHalf {
     float v[kMixHalf];
-    float4 pr[kMixHalf / 4];
+    float pr;   /* probability of position 16 half + lane % 16 of the chunk */
 };
 
-/* 12 LDS reads (8 two-position value reads, 4 probability quads) */
-__device__ __forceinline__ void mix_read(MixHalf &r, const uint8_t *slot, int half, int lane)
+/* LDS address of channel d's quad u (positions 4u .. 4u + 3) in a slot */
+__device__ __forceinline__ int mix_quad(int d, int u)
 {
-    const float *vs = reinterpret_cast<const float *>(slot) + half * kMixHalf * 64;
-    const float4 *ps = reinterpret_cast<const float4 *>(slot + kMixChunk * 256) + half * (kMixHalf / 4);
-#pragma unroll
-    for (int k = 0; k < kMixHalf / 4; ++k) r.pr[k] = ps[k];
-#pragma unroll
-    for (int k = 0; k < kMixHalf; ++k) r.v[k] = vs[k * 64 + lane];
+    return 1024 * (d >> 3) + 16 * (8 * (d & 7) + (u ^ (d & 7) ^ ((d >> 3) & 1)));
 }
 
-__device__ __forceinline__ float mix_links(const MixHalf &r, float o)
+/* 5 LDS reads: four quads of the lane's channel and one probability per
+ * lane (each 16-lane row holds the half's 16 probabilities) */
+__device__ __forceinline__ void mix_read(MixHalf &r, const uint8_t *slot, int half, int lane)
 {
+    const float *ps = reinterpret_cast<const float *>(slot + kMixChunk * 256) + half * kMixHalf;
+    r.pr = ps[lane & 15];
 #pragma unroll
     for (int k = 0; k < kMixHalf / 4; ++k) {
-        o = __builtin_fmaf(r.pr[k].x, r.v[4 * k], o);
-        o = __builtin_fmaf(r.pr[k].y, r.v[4 * k + 1], o);
-        o = __builtin_fmaf(r.pr[k].z, r.v[4 * k + 2], o);
-        o = __builtin_fmaf(r.pr[k].w, r.v[4 * k + 3], o);
+        const float4 q = *reinterpret_cast<const float4 *>(slot + mix_quad(lane, 4 * half + k));
+        r.v[4 * k] = q.x;
+        r.v[4 * k + 1] = q.y;
+        r.v[4 * k + 2] = q.z;
+        r.v[4 * k + 3] = q.w;
     }
+}
+
+/* the 16 links of a half in position order: o = fmaf(probability k, v[k],
+ * o), probability k broadcast from lane k of each 16-lane row into the
+ * fma's first operand (v_fmac_f32 with row_newbcast DPP: the same fused
+ * multiply-add as fmaf).  One statement, so nothing is scheduled between
+ * the links; it opens with the two wait states a DPP read of a VGPR written
+ * by a VALU instruction just before needs. */
+__device__ __forceinline__ float mix_links(const MixHalf &r, float o)
+{
+    asm volatile("s_nop 1\n\t"
+                 "v_fmac_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf"
+                 : "+v"(o)
+                 : "v"(r.pr), "v"(r.v[0]), "v"(r.v[1]), "v"(r.v[2]), "v"(r.v[3]), "v"(r.v[4]), "v"(r.v[5]),
+                   "v"(r.v[6]), "v"(r.v[7]), "v"(r.v[8]), "v"(r.v[9]), "v"(r.v[10]), "v"(r.v[11]), "v"(r.v[12]),
+                   "v"(r.v[13]), "v"(r.v[14]), "v"(r.v[15]));
     return o;
 }
 
@@ -870,18 +911,24 @@ __global__ __launch_bounds__(128) void attn_mix_kernel(float *__restrict__ out, 
     const int h = kvh * 6 + j % 6, t = j / 12;
     const int n = (int)*position_ptr + t + 1;
     const int chunks = (n + kMixChunk - 1) / kMixChunk;
+    const uint32_t pitch4 = value_pitch((uint32_t)context) * 4u;
     if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) == 1) {
         /* streaming wavefront */
-        const __amdgpu_buffer_rsrc_t vr =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(value_cache), 0, n * kKVDim * 4, kMixRawBuffer);
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(value_cache), 0, (int)(kKVDim * pitch4), kMixRawBuffer);
         const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float *>(prob + ((size_t)t * kAttnHeads + h) * context), 0, n * 4, kMixRawBuffer);
-        const uint32_t v_lane = (uint32_t)(lane >> 4) * (kKVDim * 4) +
-                                (uint32_t)(kvh * kAttnDim + 64 * slice) * 4 + (uint32_t)(lane & 15) * 16;
+        uint32_t v_lane[kMixVOps];
+#pragma unroll
+        for (int jj = 0; jj < kMixVOps; ++jj)
+            v_lane[jj] = (uint32_t)(kvh * kAttnDim + 64 * slice + 8 * jj + (lane >> 3)) * pitch4 +
+                         16u * (uint32_t)((lane & 7) ^ ((lane >> 3) & 7) ^ (jj & 1));
+        const uint32_t p_lane = (uint32_t)lane * 4u;
         const uint32_t ring_base = __builtin_amdgcn_readfirstlane(lds_address(ring));
+        const int last = chunks - 1;
 #pragma unroll
         for (int c = 0; c < kMixSlots - 1; ++c)
-            mix_load_chunk(vr, pr, v_lane, c, ring_base + c * kMixSlotBytes, lane);
+            mix_load_chunk(vr, pr, v_lane, p_lane, c, last, ring_base + c * kMixSlotBytes);
         /* loads retire in order */
         mix_wait_vmcnt<kMixOps * (kMixSlots - 2)>();   /* chunk 0 */
         mix_barrier();
@@ -889,25 +936,48 @@ __global__ __launch_bounds__(128) void attn_mix_kernel(float *__restrict__ out, 
         for (int c = 0; c < chunks; ++c) {
             mix_wait_vmcnt<kMixOps * (kMixSlots - 3)>();   /* chunk c + 1 */
             mix_barrier();
-            /* chunk c - 1 is consumed: its slot takes chunk c + kMixSlots - 1
-             * (past the end: every lane out of range, nothing read) */
-            mix_load_chunk(vr, pr, v_lane, c + kMixSlots - 1,
-                           ring_base + ((c + kMixSlots - 1) % kMixSlots) * kMixSlotBytes, lane);
+            /* chunk c - 1 is consumed: its slot takes chunk c + kMixSlots - 1 */
+            mix_load_chunk(vr, pr, v_lane, p_lane, c + kMixSlots - 1, last,
+                           ring_base + ((c + kMixSlots - 1) % kMixSlots) * kMixSlotBytes);
         }
         mix_wait_vmcnt<0>();
         return;
     }
     /* chain wavefront: one barrier per chunk, as the streaming wavefront */
+    const int full = n / kMixChunk, rest = n % kMixChunk;
     MixHalf a0, a1, b0, b1;
     mix_barrier();
     mix_read(a0, ring, 0, lane);
     mix_read(a1, ring, 1, lane);
     float o = 0.0f;
+    int c = 0;
+    static_assert(kMixSlots == 8, "the unrolled loop takes one ring turn per iteration");
+    /* whole ring turns: chunk c + k sits in slot k, a constant LDS offset */
 #pragma unroll 1
-    for (int c = 0; c < chunks; c += 2) {
+    for (; c + kMixSlots <= full; c += kMixSlots) {
+        o = mix_step(o, a0, a1, b0, b1, ring + 1 * kMixSlotBytes, lane);
+        o = mix_step(o, b0, b1, a0, a1, ring + 2 * kMixSlotBytes, lane);
+        o = mix_step(o, a0, a1, b0, b1, ring + 3 * kMixSlotBytes, lane);
+        o = mix_step(o, b0, b1, a0, a1, ring + 4 * kMixSlotBytes, lane);
+        o = mix_step(o, a0, a1, b0, b1, ring + 5 * kMixSlotBytes, lane);
+        o = mix_step(o, b0, b1, a0, a1, ring + 6 * kMixSlotBytes, lane);
+        o = mix_step(o, a0, a1, b0, b1, ring + 7 * kMixSlotBytes, lane);
+        o = mix_step(o, b0, b1, a0, a1, ring, lane);
+    }
+#pragma unroll 1
+    for (; c + 2 <= full; c += 2) {
         o = mix_step(o, a0, a1, b0, b1, ring + ((c + 1) % kMixSlots) * kMixSlotBytes, lane);
-        if (c + 1 >= chunks) break;
         o = mix_step(o, b0, b1, a0, a1, ring + ((c + 2) % kMixSlots) * kMixSlotBytes, lane);
+    }
+    if (c < full) o = mix_step(o, a0, a1, b0, b1, ring + ((c + 1) % kMixSlots) * kMixSlotBytes, lane);
+    if (rest) {
+        /* the partial last chunk (landed at the previous barrier), link by
+         * link up to position n - 1 */
+        mix_barrier();
+        const uint8_t *slot = ring + (full % kMixSlots) * kMixSlotBytes;
+        const float *ps = reinterpret_cast<const float *>(slot + kMixChunk * 256);
+        for (int k = 0; k < rest; ++k)
+            o = __builtin_fmaf(ps[k], *reinterpret_cast<const float *>(slot + mix_quad(lane, k >> 2) + 4 * (k & 3)), o);
     }
     const int dim = h * kAttnDim + 64 * slice + lane;
     const float g = q_and_gate[(size_t)t * qg_stride + h * 2 * kAttnDim + kAttnDim + 64 * slice + lane];
@@ -1033,7 +1103,8 @@ void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_
                       const uint32_t *position, int rows, hipStream_t stream)
 {
     attn_prep_kernel<<<dim3(kAttnHeads + kKVHeads + 1, rows), 256, 0, stream>>>(
-        q_buf, q_and_gate, key, value, in_stride, q_norm, k_norm, rope, key_cache, value_cache, position, 0);
+        q_buf, q_and_gate, key, value, in_stride, q_norm, k_norm, rope, key_cache, value_cache,
+        (int)value_pitch((uint32_t)context), position, 0);
     {
         const int half_chunks = ((context + kScoreChunk - 1) / kScoreChunk + 1) / 2;
         attn_scores_kernel<kScoreHeadsPerLane>
@@ -1051,11 +1122,12 @@ void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_
 }
 
 void launch_kv_write(const float *key, const float *value, long long in_stride, const float *k_norm,
-                     const float *rope, float *key_cache, float *value_cache, const uint32_t *position, int rows,
-                     hipStream_t stream)
+                     const float *rope, float *key_cache, float *value_cache, int context, const uint32_t *position,
+                     int rows, hipStream_t stream)
 {
     attn_prep_kernel<<<dim3(kKVHeads + 1, rows), 256, 0, stream>>>(nullptr, nullptr, key, value, in_stride, nullptr,
-                                                                  k_norm, rope, key_cache, value_cache, position,
+                                                                  k_norm, rope, key_cache, value_cache,
+                                                                  (int)value_pitch((uint32_t)context), position,
                                                                   kAttnHeads);
 }
 

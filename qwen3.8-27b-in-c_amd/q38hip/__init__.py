@@ -277,15 +277,23 @@ def accept(targets, drafts):
     return out
 
 
+def value_pitch(context):
+    """positions per channel row of the channel-major value cache"""
+    return (int(context) + 31) // 32 * 32
+
+
 def attention_rows(rows_in, q_norm, k_norm, key_cache, value_cache, position):
     """Full-attention core over the rows of rows_in (float32 [rows, 14336] on
     the GPU: 24 heads x (256 q | 256 gate), then key [1024], then value
-    [1024]) at positions position + t; key_cache / value_cache: float32
-    [context, 1024] on the GPU, updated in place.  Returns (attention
-    float32 [rows, 6144], its Q8_K blocks uint8 [rows * 24 * 292])."""
+    [1024]) at positions position + t; key_cache: float32 [context, 1024],
+    value_cache: channel-major float32 [1024, value_pitch(context)], both on
+    the GPU and updated in place.  Returns (attention float32 [rows, 6144],
+    its Q8_K blocks uint8 [rows * 24 * 292])."""
     import torch
     rows, stride = rows_in.shape
     context = key_cache.shape[0]
+    if tuple(value_cache.shape) != (1024, value_pitch(context)):
+        raise ValueError("value_cache must be [1024, value_pitch(context)]")
     out = torch.empty((rows, 6144), dtype=torch.float32, device=rows_in.device)
     q8k = torch.empty(rows * 24 * Q8K_BYTES, dtype=torch.uint8, device=rows_in.device)
     base = rows_in.data_ptr()

@@ -53,7 +53,11 @@ def test_attention_rows_bit_exact(device, oracle, context, position, rows):
     kc[position + rows:] = np.nan
     vc[position + rows:] = np.nan
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
-    dk, dv = d(kc), d(vc)
+    # the library keeps the value cache channel-major, padded to 32 positions
+    pitch = q38hip.value_pitch(context)
+    vc_t = np.full((1024, pitch), np.nan, dtype=np.float32)
+    vc_t[:, :context] = vc.T
+    dk, dv = d(kc), d(vc_t)
     got, got_q = q38hip.attention_rows(d(rows_in), d(qn), d(kn), dk, dv, position)
     torch.cuda.synchronize()
     want = ac.run_rows(_oracle_core(oracle), rows_in, qn, kn, kc, vc, position)
@@ -62,5 +66,5 @@ def test_attention_rows_bit_exact(device, oracle, context, position, rows):
         "max abs diff %g" % np.abs(got - want).max()
     span = slice(position, position + rows)
     assert np.array_equal(dk.cpu().numpy()[span].view(np.uint32), kc[span].view(np.uint32))
-    assert np.array_equal(dv.cpu().numpy()[span].view(np.uint32), vc[span].view(np.uint32))
+    assert np.array_equal(np.ascontiguousarray(dv.cpu().numpy()[:, span].T).view(np.uint32), vc[span].view(np.uint32))
     assert got_q.cpu().numpy().tobytes() == oracle.quantize(want.reshape(-1)).tobytes()
