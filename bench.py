@@ -73,6 +73,15 @@ WORKLOADS = {
     "iq1m_wide_m256": (29, 34816, 5120, 256, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 256 tokens (prefill)"),
     "q4k_wide_down_m256": (12, 5120, 17408, 256, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 256 tokens (prefill)"),
 }
+# device kernel each launch of a workload runs (q38hip dispatch for that shape; the
+# trace summaries and counter profiles under profiles/ name the same kernels)
+DEVICE_KERNEL = {
+    "q4k_gemv": "gemm_q8k_stream<12, 1>",
+    "iq1m_gemv": "gemm_iq1m_mfma<1, 20, 8, 2>",
+    "q4k_tiled_m3": "gemm_q4k_mm16<3, 20, 9, 4, 1>",
+    "q4k_tiled_down_m3": "gemm_q4k_t32<3, 68, 4, 2>",
+    "iq1m_gemm_m3": "gemm_iq1m_mfma<3, 20, 4, 2>",
+}
 # dense matrix-core peaks of MI355X, TOP/s: the Q4_K GEMM runs fp16 MFMA, IQ1_M int8
 MFMA_PEAK_TOPS = {12: ("f16", 2500.0), 29: ("i8", 5000.0)}
 BLOCK = {12: 144, 14: 210, 29: 56}
@@ -228,7 +237,7 @@ def kernel_roofline(torch, workload, steps, warmup):
     traffic = committed_traffic(workload)
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None if traffic is None else int(traffic),
-                "kernel": "%s (%s)" % ("gemm_q4k_tiled" if tiled else "gemm_q8k", label),
+                "kernel": "%s (%s)" % (DEVICE_KERNEL.get(workload, "gemm_q4k_tiled" if tiled else "gemm_q8k"), label),
                 "bytes_per_launch": nbytes, "launch_us": round(per_launch_ms * 1e3, 3)}
     if (tiled and tokens > 1) or qtype == 29:
         # matrix-core kernels: algorithmic multiply-adds (2 ops each) per second
