@@ -52,6 +52,8 @@ constexpr uint32_t kQ8KBytes = 292;
 /* device parameter blocks of kParamWords words: [0] position of row 0 of
  * the step, [1 + r] current state slot of recurrent layer r */
 constexpr uint32_t kParamWords = 64;
+/* word of the verify parameter block holding the stop token */
+constexpr uint32_t kParamStopWord = kParamWords - 1;
 enum : uint32_t { kParamTarget = 0, kParamCatchup = 1, kParamDraft0 = 2, kParamSets = 2 + kBatch };
 
 enum : uint32_t { F32 = 0, Q4_K = 12, Q6_K = 14, IQ1_M = 29 };
@@ -387,6 +389,8 @@ struct Q38Model {
      * sampled token [48] */
     uint32_t *words = nullptr, *sampled = nullptr;
     float *argmax_pv = nullptr;
+    /* the logits row a speculative call returns, gathered on the device */
+    float *logits_stage = nullptr;
     uint32_t *argmax_pi = nullptr;
     /* device sampling: the row of the logits the last call returned (valid
      * until the next call), a device copy of the sampler's presence bytes
@@ -656,7 +660,7 @@ void release(Q38Model *m)
     float **fbufs[] = {&m->conv_state, &m->delta_state, &m->key_cache, &m->value_cache, &m->mtp_hidden,
                        &m->ck_mtp_hidden, &m->rope, &m->hidden, &m->norm,
                        &m->branch, &m->wide0, &m->qbuf, &m->attn, &m->scores, &m->logits, &m->target_norm,
-                       &m->argmax_pv, &m->long_norm, &m->prep, &m->fin};
+                       &m->argmax_pv, &m->long_norm, &m->prep, &m->fin, &m->logits_stage};
     for (float **p : fbufs) dfree(*p);
     uint32_t **ubufs[] = {&m->tokens, &m->params, &m->words, &m->argmax_pi};
     for (uint32_t **p : ubufs) dfree(*p);
@@ -695,7 +699,8 @@ bool allocate_state(Q38Model *m)
               dalloc(&m->qbuf, (size_t)B * kQDim) && dalloc(&m->attn, (size_t)B * kLinV) &&
               dalloc(&m->prep, (size_t)B * 2 * kFFN) &&
               dalloc(&m->scores, (size_t)B * kAttnHeads * ctx) &&
-              dalloc(&m->logits, (size_t)kBatch * kVocab) && dalloc(&m->target_norm, (size_t)B * kHidden) &&
+              dalloc(&m->logits, (size_t)kBatch * kVocab) && dalloc(&m->logits_stage, kVocab) &&
+              dalloc(&m->target_norm, (size_t)B * kHidden) &&
               dalloc(&m->q8k, (size_t)B * (kFFN / 256) * kQ8KBytes) && dalloc(&m->tokens, B) &&
               dalloc(&m->params, (size_t)kParamSets * kParamWords) && dalloc(&m->words, 64) &&
               dalloc(&m->argmax_pv, (size_t)kBatch * q38::argmax_chunks(kVocab)) &&
@@ -1166,8 +1171,10 @@ bool target_rows(Q38Model *m, const Step &s, uint32_t count, uint32_t logit_rows
  * target_norm[count - 1].  The rest of the reference's catch-up block
  * (queries, attention output, FFN) is computed there and never read, so it
  * is not computed here.  Enqueue only. */
-bool mtp_catchup(Q38Model *m, const Step &s, uint32_t count)
+bool mtp_catchup(Q38Model *m, const Step &s, uint32_t count, const float *prev0 = nullptr,
+                 const uint32_t *last_row = nullptr)
 {
+    if (!prev0) prev0 = m->mtp_hidden;
     const Layer &L = m->layers[kLayers];
     constexpr int kHB = kHidden / 256;   /* Q8_K blocks per hidden row */
     embed(m, m->mtp_embedding, s.tokens, count);
@@ -1177,8 +1184,8 @@ bool mtp_catchup(Q38Model *m, const Step &s, uint32_t count)
     float *f = m->float_inputs ? m->fin : nullptr;
     q38::launch_norm_quant(f, 2 * kHidden, m->q8k, 2 * kHB, m->hidden, kHidden, nullptr, m->enorm.f32(), (int)count,
                            m->stream);
-    q38::launch_norm_quant(f ? f + kHidden : nullptr, 2 * kHidden, m->q8k + kHB * kQ8KBytes, 2 * kHB, m->mtp_hidden,
-                           kHidden, nullptr, m->hnorm.f32(), 1, m->stream);
+    q38::launch_norm_quant(f ? f + kHidden : nullptr, 2 * kHidden, m->q8k + kHB * kQ8KBytes, 2 * kHB,
+                           const_cast<float *>(prev0), kHidden, nullptr, m->hnorm.f32(), 1, m->stream);
     if (count > 1)
         q38::launch_norm_quant(f ? f + 3 * kHidden : nullptr, 2 * kHidden, m->q8k + 3 * kHB * kQ8KBytes, 2 * kHB,
                                m->target_norm, kHidden, nullptr, m->hnorm.f32(), (int)count - 1, m->stream);
@@ -1194,6 +1201,12 @@ bool mtp_catchup(Q38Model *m, const Step &s, uint32_t count)
     q38::launch_kv_write(m->wide0, m->wide0 + (g.first[2] - g.first[1]), ld, L.k_norm.f32(), m->rope,
                          m->key_cache + kv_off, m->value_cache + v_off, (int)m->context_length, s.params,
                          (int)count, m->stream);
+    /* the MTP hidden state continues from the last row (or from row
+     * *last_row - 1, read on the device) */
+    if (last_row) {
+        q38::launch_copy_row(m->mtp_hidden, m->target_norm, kHidden, kHidden, last_row, count, m->stream);
+        return launches_ok();
+    }
     return launches_ok() &&
            hip_ok(hipMemcpyAsync(m->mtp_hidden, m->target_norm + (size_t)(count - 1) * kHidden,
                                  kHidden * sizeof(float), hipMemcpyDeviceToDevice, m->stream),
@@ -1224,7 +1237,7 @@ bool mtp_step(Q38Model *m, const Step &s)
 
 /* ---- graphs ------------------------------------------------------------------ */
 
-enum : uint32_t { kGraphTarget = 1, kGraphVerify = 2, kGraphDraft = 3, kGraphCatchup = 4 };
+enum : uint32_t { kGraphTarget = 1, kGraphDraft = 3, kGraphCatchup = 4, kGraphTransaction = 5 };
 
 uint64_t graph_key(uint32_t kind, uint32_t a, uint32_t b = 0) { return ((uint64_t)kind << 32) | (a << 16) | b; }
 
@@ -1712,87 +1725,68 @@ int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_toke
     }
     for (uint32_t i = 0; i < k; ++i) write_params(m, kParamDraft0 + i, m->ck_mtp_position + i);
     write_params(m, kParamTarget, m->ck_position);
+    write_params(m, kParamCatchup, m->ck_mtp_position);
+    m->host_params[(size_t)kParamTarget * kParamWords + kParamStopWord] = stop_token;
     if (!upload_tokens(m, &token, 1, m->drafts) || !flush_params(m)) return 0;
 
-    bool ok = true;
-    for (uint32_t i = 0; ok && i < k; ++i) {
-        const Step s = step_of(m, kParamDraft0 + i, m->drafts + i);
-        ok = run_step(m, graph_key(kGraphDraft, i, 0), [&] {
-            if (!mtp_step(m, s)) return false;
-            q38::launch_argmax(m->logits, kVocab, 1, m->argmax_pv, m->argmax_pi, m->drafts + i + 1, m->stream);
-            return true;
-        });
-    }
-    /* verify rows m->drafts[0 .. k), per-row argmax into m->targets and the
-     * device acceptance over all k rows */
-    const Step sv = step_of(m, kParamTarget, m->drafts);
-    ok = ok && run_step(m, graph_key(kGraphVerify, k), [&] {
-        if (!target_rows(m, sv, k, k)) return false;
-        q38::launch_argmax(m->logits, kVocab, k, m->argmax_pv, m->argmax_pi, m->targets, m->stream);
-        q38::launch_accept(m->accept, m->targets, m->drafts + 1, k, m->stream);
-        return true;
-    });
-    /* drafts, targets and the acceptance in one download: host words
-     * [64..) mirror m->words (drafts at 64, targets at 80, acceptance at 96) */
-    uint32_t *hw = m->host_words;
-    ok = ok &&
-         hip_ok(hipMemcpyAsync(hw + 64, m->words, 48 * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream),
-                "acceptance") &&
-         hip_ok(hipStreamSynchronize(m->stream), "acceptance");
-    if (!ok) {
-        restore_target(m);
-        (void)restore_mtp(m);
-        (void)hipStreamSynchronize(m->stream);
-        return 0;
-    }
-    const uint32_t *drafts = hw + 65, *targets = hw + 80;
-    uint32_t n = k;
-    for (uint32_t i = 0; i < k; ++i)
-        if (drafts[i] == stop_token) { n = i + 1; break; }
-    uint32_t matched, consumed;
-    uint32_t accepted[kBatch];
-    if (n == k) {
-        consumed = hw[96];
-        matched = hw[97];
-        for (uint32_t i = 0; i < consumed; ++i) accepted[i] = hw[99 + i];
-    } else {
-        /* the reference's loop over its n rows (qwen38_model.c:1665-1682) */
-        matched = 0;
-        uint32_t next = 0;
-        while (matched < n && targets[matched] == drafts[matched]) ++matched;
-        if (matched < n) next = targets[matched];
-        consumed = matched < n ? matched + 1 : n;
-        for (uint32_t i = 0; i < matched; ++i) accepted[i] = drafts[i];
-        if (matched < n) accepted[matched] = next;
-    }
-    /* On a rejection the reference restores its checkpoint and replays the
+    /* one graph per draft count: the k MTP drafts (draft i + 1 is the argmax
+     * of draft i's logits), the verify rows m->drafts[0 .. k) with their
+     * per-row argmax into m->targets, the device acceptance (rows up to the
+     * first draft equal to the stop token, as the reference checks), the
+     * returned logits row (row consumed - 1) gathered into m->logits_stage,
+     * and the MTP catch-up.
+     *
+     * On a rejection the reference restores its checkpoint and replays the
      * consumed rows (qwen38_model.c:1684-1691).  Every row of the verify
      * batch computed exactly what the replay would (rows are independent in
      * the GEMMs and the recurrent state advanced row by row), so the state
      * after the consumed rows is already in slot checkpoint + consumed, their
      * K/V entries are in the caches, and the last consumed row's logits are
      * row consumed - 1 of the batch; entries of the rejected rows are never
-     * read before being overwritten. */
-    restore_target(m, consumed);
-    (void)restore_mtp(m);
-    write_params(m, kParamCatchup, m->ck_mtp_position);
+     * read before being overwritten.  The MTP catch-up runs over all k rows
+     * from the checkpointed MTP hidden state (rows past the consumed ones
+     * only write MTP cache entries past the positions the next drafts
+     * rewrite before reading them) and continues the MTP hidden state from
+     * row consumed - 1, read on the device: one host wait per call. */
+    const Step sv = step_of(m, kParamTarget, m->drafts);
     const Step sc = step_of(m, kParamCatchup, m->drafts);
-    /* the verify logits are final (the stream is synchronised) and the
-     * catch-up does not write them: download on the copy stream meanwhile */
-    ok = hip_ok(hipEventRecord(m->logits_ready, m->stream), "event") &&
-         hip_ok(hipStreamWaitEvent(m->copy_stream, m->logits_ready, 0), "event") &&
-         hip_ok(hipMemcpyAsync(m->host_logits, m->logits + (size_t)(consumed - 1) * kVocab, kVocab * sizeof(float),
-                               hipMemcpyDeviceToHost, m->copy_stream), "logits download") &&
-         flush_params(m) && run_step(m, graph_key(kGraphCatchup, consumed), [&] { return mtp_catchup(m, sc, consumed); }) &&
-         hip_ok(hipStreamSynchronize(m->stream), "catch-up") &&
-         hip_ok(hipStreamSynchronize(m->copy_stream), "logits download");
+    const uint32_t *stop = m->params + (size_t)kParamTarget * kParamWords + kParamStopWord;
+    uint32_t *hw = m->host_words;
+    bool ok = run_step(m, graph_key(kGraphTransaction, k), [&] {
+                  for (uint32_t i = 0; i < k; ++i) {
+                      if (!mtp_step(m, step_of(m, kParamDraft0 + i, m->drafts + i))) return false;
+                      q38::launch_argmax(m->logits, kVocab, 1, m->argmax_pv, m->argmax_pi, m->drafts + i + 1,
+                                         m->stream);
+                  }
+                  if (!target_rows(m, sv, k, k)) return false;
+                  q38::launch_argmax(m->logits, kVocab, k, m->argmax_pv, m->argmax_pi, m->targets, m->stream);
+                  q38::launch_accept(m->accept, m->targets, m->drafts + 1, k, m->stream, stop);
+                  q38::launch_copy_row(m->logits_stage, m->logits, kVocab, kVocab, m->accept, k, m->stream);
+                  return mtp_catchup(m, sc, k, m->ck_mtp_hidden, m->accept);
+              }) &&
+         /* then the acceptance words and the logits row: host words [64..)
+          * mirror m->words (drafts at 64, targets at 80, acceptance at 96) */
+         hip_ok(hipMemcpyAsync(hw + 64, m->words, 48 * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream),
+                "acceptance") &&
+         hip_ok(hipMemcpyAsync(m->host_logits, m->logits_stage, kVocab * sizeof(float), hipMemcpyDeviceToHost,
+                               m->stream), "logits download") &&
+         hip_ok(hipStreamSynchronize(m->stream), "catch-up");
     if (!ok) {
         restore_target(m);
         (void)restore_mtp(m);
         (void)hipStreamSynchronize(m->stream);
-        (void)hipStreamSynchronize(m->copy_stream);
         return 0;
     }
+    const uint32_t consumed = hw[96];
+    if (consumed == 0 || consumed > k) {
+        restore_target(m);
+        (void)restore_mtp(m);
+        (void)hipStreamSynchronize(m->stream);
+        return report("acceptance result out of range");
+    }
+    uint32_t accepted[kBatch];
+    for (uint32_t i = 0; i < consumed; ++i) accepted[i] = hw[99 + i];
+    restore_target(m, consumed);
     m->mtp_position = m->ck_mtp_position + consumed;
     m->last_logits = m->logits + (size_t)(consumed - 1) * kVocab;
     for (uint32_t i = 0; i < consumed; ++i) accepted_tokens[i] = accepted[i];

@@ -81,8 +81,15 @@ void launch_quantize(const float *x, uint8_t *out, uint32_t nblocks, hipStream_t
 uint32_t argmax_chunks(uint32_t count);
 void launch_argmax(const float *values, uint32_t count, uint32_t rows, float *pv, uint32_t *pi, uint32_t *out,
                    hipStream_t stream);
+/* result[0] = rows consumed, [1] = drafts matched, [2] = next token,
+ * [3 ..] = accepted tokens, over `rows` rows, or over the rows up to the
+ * first draft equal to *stop when stop is not null */
 void launch_accept(uint32_t *result, const uint32_t *targets, const uint32_t *drafts, uint32_t rows,
-                   hipStream_t stream);
+                   hipStream_t stream, const uint32_t *stop = nullptr);
+/* dst[0 .. count) = row (*index - 1) of the `rows` rows of src, `stride`
+ * floats apart (index clamped to 1 .. rows) */
+void launch_copy_row(float *dst, const float *src, size_t stride, uint32_t count, const uint32_t *index,
+                     uint32_t rows, hipStream_t stream);
 
 /* q38_sample.hip: q38_sample (qwen38_sampler.c:51-119) on a device logits
  * row; *token_out is a device word written on `stream`.  *state is the

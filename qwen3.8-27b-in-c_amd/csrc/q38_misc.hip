@@ -106,9 +106,19 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(
  * rows whose target argmax equals the draft are matched; the first
  * mismatching target becomes `next`; consumed = matched + 1, or all rows. */
 __global__ void accept_kernel(uint32_t *__restrict__ result, const uint32_t *__restrict__ targets,
-                              const uint32_t *__restrict__ drafts, uint32_t rows)
+                              const uint32_t *__restrict__ drafts, uint32_t rows, const uint32_t *__restrict__ stop)
 {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    /* a draft equal to the stop token ends the rows the reference checks
+     * (qwen38_model.c:1640-1649) */
+    if (stop) {
+        const uint32_t st = *stop;
+        for (uint32_t i = 0; i < rows; ++i)
+            if (drafts[i] == st) {
+                rows = i + 1;
+                break;
+            }
+    }
     uint32_t matched = 0, next = 0;
     while (matched < rows) {
         if (targets[matched] != drafts[matched]) { next = targets[matched]; break; }
@@ -144,9 +154,34 @@ void launch_argmax(const float *values, uint32_t count, uint32_t rows, float *pv
 }
 
 void launch_accept(uint32_t *result, const uint32_t *targets, const uint32_t *drafts, uint32_t rows,
-                   hipStream_t stream)
+                   hipStream_t stream, const uint32_t *stop)
 {
-    hipLaunchKernelGGL(accept_kernel, dim3(1), dim3(64), 0, stream, result, targets, drafts, rows);
+    hipLaunchKernelGGL(accept_kernel, dim3(1), dim3(64), 0, stream, result, targets, drafts, rows, stop);
+}
+
+/* dst[0 .. count) = row (*index - 1) of the `rows` rows of src (`stride`
+ * floats apart); the index is clamped to 1 .. rows */
+__global__ __launch_bounds__(256) void copy_row_kernel(float *__restrict__ dst, const float *__restrict__ src,
+                                                       size_t stride, uint32_t count, const uint32_t *__restrict__ index,
+                                                       uint32_t rows)
+{
+    const uint32_t r = min(max(*index, 1u), rows) - 1u;
+    const float *row = src + (size_t)r * stride;
+    for (uint32_t i = (blockIdx.x * 256u + threadIdx.x) * 4u; i < count; i += gridDim.x * 1024u) {
+        if (i + 4u <= count) {
+            *reinterpret_cast<float4 *>(dst + i) = *reinterpret_cast<const float4 *>(row + i);
+        } else {
+            for (uint32_t k = i; k < count; ++k) dst[k] = row[k];
+        }
+    }
+}
+
+void launch_copy_row(float *dst, const float *src, size_t stride, uint32_t count, const uint32_t *index,
+                     uint32_t rows, hipStream_t stream)
+{
+    const uint32_t blocks = (count + 1023u) / 1024u;
+    hipLaunchKernelGGL(copy_row_kernel, dim3(blocks < 64u ? blocks : 64u), dim3(256), 0, stream, dst, src, stride,
+                       count, index, rows);
 }
 
 }  // namespace q38
