@@ -1,6 +1,6 @@
 /* Device-math probe for the GPU tests (test infrastructure; not part of
  * libq38hip).  Evaluates the device functions the kernels use
- * (qwen3.8-27b-in-c_amd/csrc/q38_math.h, q38_libm.h) on given inputs, and
+ * (qwen3.8-27b-in-c_amd/csrc/q38_math.h, q38_libm.h, q38_norm.h) on given inputs, and
  * forms an order-independent 64-bit checksum of q38_expf / q38_logf over all
  * 2^32 float inputs that tests/native/libm_check.c also forms on the host
  * with the C library's expf / logf. */
@@ -8,6 +8,7 @@
 #include <stdint.h>
 
 #include "q38_math.h"
+#include "q38_norm.h"
 
 namespace {
 
@@ -65,9 +66,26 @@ __global__ __launch_bounds__(kThreads) void checksum_kernel(int op, uint64_t *pa
     if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
 }
 
+/* the mean of squares of the RMSNorm (q38_norm.h: parallel double sum,
+ * sequential redo near a rounding boundary) over one vector */
+__global__ __launch_bounds__(256) void mean_square_kernel(const float *x, int n, float *out)
+{
+    const float m = q38::block_sum_squares<256>(x, n, q38::MeanPost{(double)n});
+    if (threadIdx.x == 0) *out = m;
+}
+
 }  // namespace
 
 extern "C" {
+
+/* *out = (float)(sum of x[i]^2 / n) as the kernels' RMSNorm forms it;
+ * device pointers, synchronous. */
+int probe_mean_square(const float *x, int n, float *out)
+{
+    if (n <= 0) return 0;
+    mean_square_kernel<<<1, 256>>>(x, n, out);
+    return hipDeviceSynchronize() == hipSuccess;
+}
 
 /* out/x/y are device pointers (y may be null); synchronous. */
 int probe_eval(int op, float *out, const float *x, const float *y, uint64_t n)
