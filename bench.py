@@ -61,14 +61,14 @@ WORKLOADS = {
     # name: (type, rows, width, tokens, tiled, label)
     "q4k_gemv": (12, 17408, 5120, 1, False, "Q4_K GEMV 17408x5120"),
     "q4k_gemv_t": (12, 5120, 17408, 1, False, "Q4_K GEMV 5120x17408"),
-    "iq1m_gemv": (29, 17408, 5120, 1, False, "IQ1_M GEMV 17408x5120"),
-    "iq1m_gemv_t": (29, 5120, 17408, 1, False, "IQ1_M GEMV 5120x17408"),
+    "iq1m_gemv": (29, 17408, 5120, 1, True, "IQ1_M GEMV 17408x5120"),
+    "iq1m_gemv_t": (29, 5120, 17408, 1, True, "IQ1_M GEMV 5120x17408"),
     "q6k_gemv": (14, 17408, 5120, 1, False, "Q6_K GEMV 17408x5120"),
     "q4k_tiled_m3": (12, 34816, 5120, 3, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 3 tokens"),
     "q4k_tiled_down_m3": (12, 5120, 17408, 3, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 3 tokens"),
-    "iq1m_gemm_m3": (29, 34816, 5120, 3, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 3 tokens"),
+    "iq1m_gemm_m3": (29, 34816, 5120, 3, True, "IQ1_M GEMM 34816x5120 (FFN gate|up), 3 tokens"),
     "q4k_tiled_m8": (12, 34816, 5120, 8, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
-    "iq1m_gemm_m8": (29, 34816, 5120, 8, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
+    "iq1m_gemm_m8": (29, 34816, 5120, 8, True, "IQ1_M GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
     "q4k_wide_m256": (12, 34816, 5120, 256, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 256 tokens (prefill)"),
     "iq1m_wide_m256": (29, 34816, 5120, 256, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 256 tokens (prefill)"),
     "q4k_wide_down_m256": (12, 5120, 17408, 256, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 256 tokens (prefill)"),
@@ -77,10 +77,10 @@ WORKLOADS = {
 # trace summaries and counter profiles under profiles/ name the same kernels)
 DEVICE_KERNEL = {
     "q4k_gemv": "gemm_q8k_stream<12, 1>",
-    "iq1m_gemv": "gemm_iq1m_mfma<1, 20, 8, 2>",
+    "iq1m_gemv": "gemm_iq1m_mfma<1, 20, 8, 2, true>",
     "q4k_tiled_m3": "gemm_q4k_mm16<3, 20, 9, 4, 1>",
     "q4k_tiled_down_m3": "gemm_q4k_t32<3, 68, 4, 2>",
-    "iq1m_gemm_m3": "gemm_iq1m_mfma<3, 20, 4, 2>",
+    "iq1m_gemm_m3": "gemm_iq1m_mfma<3, 20, 4, 2, true>",
 }
 # dense matrix-core peaks of MI355X, TOP/s: the Q4_K GEMM runs fp16 MFMA, IQ1_M int8
 MFMA_PEAK_TOPS = {12: ("f16", 2500.0), 29: ("i8", 5000.0)}
@@ -212,7 +212,8 @@ def kernel_roofline(torch, workload, steps, warmup):
     nbytes = algorithmic_bytes(qtype, rows, width, tokens)
     base = torch.from_numpy(synth.matrix(qtype, rows, width, seed=1)).to(dev)
     if tiled:
-        base = q38hip.repack_q4k_tiles(base, width, rows)
+        # the engine's 16-row tiled copies (Q4_K, and IQ1_M for 1..8 tokens)
+        base = (q38hip.repack_iq1m_tiles if qtype == 29 else q38hip.repack_q4k_tiles)(base, width, rows)
     copies = max(2, -(-(1 << 30) // base.numel()) + 1)
     # one allocation holds every copy, as the engine holds all weights in one
     pool = torch.empty(copies * base.numel(), dtype=torch.uint8, device=dev)
@@ -225,7 +226,9 @@ def kernel_roofline(torch, workload, steps, warmup):
     stream = torch.cuda.current_stream()
 
     def launch(i):
-        if tiled:
+        if tiled and qtype == 29:
+            q38hip.gemm_q8_k_iq1m_tiled(weights[i % copies], width, rows, xq, tokens, out=out)
+        elif tiled:
             q38hip.gemm_q8_k_tiled(weights[i % copies], width, rows, xq, tokens, out=out)
         else:
             q38hip.gemm_q8_k(weights[i % copies], qtype, width, rows, xq, tokens, out=out)

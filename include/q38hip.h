@@ -195,6 +195,22 @@ int q38hip_gemm_q8_k_tiled(float *output, const Q38Q8KBlock *input,
                            uint32_t batch_size, uint64_t input_length,
                            const void *tiled, uint32_t rows, void *stream);
 
+/* Library extension: the same 16-row tiled copy for IQ1_M
+ * ([tile = row / 16][block][row % 16][56 bytes], rows past the last zero),
+ * which the engine keeps beside the row-major blocks.
+ * q38hip_tiled_iq1m_bytes: its size (0 for a bad shape);
+ * q38hip_repack_iq1m_tiles: write it from the row-major matrix (both in
+ * device memory, the copy 8-byte aligned); q38hip_gemm_q8_k_iq1m_tiled:
+ * q38hip_gemm_q8_k over it for batch_size 1..8 (output[t * rows + r]),
+ * input_length 5120, 6144, 10240 or 17408, bit for bit q38hip_gemm_q8_k's
+ * results. */
+uint64_t q38hip_tiled_iq1m_bytes(uint32_t rows, uint64_t input_length);
+int q38hip_repack_iq1m_tiles(void *tiled, const void *iq1m_rows, uint32_t rows,
+                             uint64_t input_length, void *stream);
+int q38hip_gemm_q8_k_iq1m_tiled(float *output, const Q38Q8KBlock *input,
+                                uint32_t batch_size, uint64_t input_length,
+                                const void *tiled, uint32_t rows, void *stream);
+
 /* Library extension: the full-attention decode core of one layer on the
  * device, for kernel-level use and tests.  It is the reference's static
  * q38_full_core (src/qwen38/qwen38_model.c:816-885) for `rows` consecutive

@@ -297,6 +297,39 @@ int q38hip_repack_q4k_tiles(void *tiled, const void *q4k_rows, uint32_t rows, ui
                : fail("repack launch failed (tiled copy must be 16-byte aligned)");
 }
 
+uint64_t q38hip_tiled_iq1m_bytes(uint32_t rows, uint64_t input_length)
+{
+    if (!rows || !input_length || input_length % Q38_Q8_K_BLOCK_SIZE || input_length / 256 > 0xffffffffull) return 0;
+    return q38::tiled_iq1m_bytes(rows, (uint32_t)(input_length / 256));
+}
+
+int q38hip_repack_iq1m_tiles(void *tiled, const void *iq1m_rows, uint32_t rows, uint64_t input_length, void *stream)
+{
+    if (!tiled || !iq1m_rows || !rows) return fail("null argument");
+    if (!input_length || input_length % Q38_Q8_K_BLOCK_SIZE || input_length / 256 > 0xffffffffull)
+        return fail("input length is not a positive multiple of 256");
+    if (!device_state()) return fail("device initialisation failed");
+    return q38::launch_repack_iq1m_tiles(static_cast<uint8_t *>(tiled), static_cast<const uint8_t *>(iq1m_rows),
+                                         rows, (uint32_t)(input_length / 256), static_cast<hipStream_t>(stream))
+               ? 1
+               : fail("repack launch failed (tiled copy must be 8-byte aligned)");
+}
+
+int q38hip_gemm_q8_k_iq1m_tiled(float *output, const Q38Q8KBlock *input, uint32_t batch_size, uint64_t input_length,
+                                const void *tiled, uint32_t rows, void *stream)
+{
+    if (!output || !input || !tiled || !rows) return fail("null argument");
+    if (batch_size < 1 || batch_size > 8) return fail("batch_size must be 1..8");
+    DeviceState *state = device_state();
+    if (!state) return fail("device initialisation failed");
+    if (input_length % Q38_Q8_K_BLOCK_SIZE) return fail("input length is not a multiple of 256");
+    return q38::launch_gemm_iq1m_tiled((int)batch_size, static_cast<const uint8_t *>(tiled),
+                                       reinterpret_cast<const uint8_t *>(input), output, rows, rows,
+                                       (uint32_t)(input_length / 256), state->grid, static_cast<hipStream_t>(stream))
+               ? 1
+               : fail("unsupported tiled GEMM shape (input_length 5120, 6144, 10240 or 17408)");
+}
+
 int q38hip_gemm_q8_k_tiled(float *output, const Q38Q8KBlock *input, uint32_t batch_size, uint64_t input_length,
                            const void *tiled, uint32_t rows, void *stream)
 {

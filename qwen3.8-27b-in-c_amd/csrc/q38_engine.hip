@@ -861,15 +861,29 @@ bool gemm_float(Q38Model *m, const DevTensor &w, uint32_t count, const float *xf
     return true;
 }
 
+/* the tiled copy's kernel where there is one: Q4_K for 2..8 rows and
+ * prefill batches, IQ1_M for 1..8 rows (prefill batches keep the row-major
+ * blocks); false when none ran */
+bool gemm_tiled(Q38Model *m, const DevTensor &w, uint32_t count, const uint8_t *x, float *out, uint32_t ldy,
+                uint32_t rows)
+{
+    if (!w.tiled) return false;
+    const uint32_t nb = (uint32_t)(w.width / 256);
+    if (w.type == Q4_K)
+        return count >= 2 && q38::launch_gemm_q4k_tiled((int)count, w.tiled, x, out, ldy, rows, nb, m->stream);
+    if (w.type == IQ1_M)
+        return count >= 1 && count <= kBatch &&
+               q38::launch_gemm_iq1m_tiled((int)count, w.tiled, x, out, ldy, rows, nb, m->grid, m->stream);
+    return false;
+}
+
 /* one projection: Q8_K rows from m->q8k (starting at block first_block), or
  * for a float-input matrix the fp32 rows at xf */
 bool gemm_q(Q38Model *m, const DevTensor &w, uint32_t count, float *out, size_t first_block = 0,
             const float *xf = nullptr)
 {
     if (float_input(w)) return gemm_float(m, w, count, xf, out, (uint32_t)w.rows, (uint32_t)w.rows, w.data);
-    if (count >= 2 && w.tiled &&
-        q38::launch_gemm_q4k_tiled((int)count, w.tiled, m->q8k + first_block * kQ8KBytes, out, (uint32_t)w.rows,
-                                   (uint32_t)w.rows, (uint32_t)(w.width / 256), m->stream))
+    if (gemm_tiled(m, w, count, m->q8k + first_block * kQ8KBytes, out, (uint32_t)w.rows, (uint32_t)w.rows))
         return true;
     return gemm_rows(m, w, count, m->q8k + first_block * kQ8KBytes, out, (uint32_t)w.rows, (uint32_t)w.rows,
                      w.data);
@@ -910,18 +924,23 @@ bool build_tiled(Q38Model *m, uint32_t first, uint32_t last, bool with_eh, void 
 {
     struct Job {
         const uint8_t *src;
-        uint32_t rows, nb;
+        uint32_t rows, nb, type;
         std::vector<std::pair<DevTensor *, uint64_t>> targets;   /* tensor, first tile */
     };
     std::vector<Job> jobs;
     auto supported = [](const DevTensor &t) {
         const uint64_t nb = t.width / 256;
-        return t.type == Q4_K && t.data && (nb == 20 || nb == 24 || nb == 40 || nb == 68);
+        return (t.type == Q4_K || t.type == IQ1_M) && t.data && (nb == 20 || nb == 24 || nb == 40 || nb == 68);
+    };
+    /* bytes of one block of a 16-row tile, and of the whole copy */
+    auto tile_block = [](uint32_t type) -> size_t { return type == IQ1_M ? 16 * 56 : 2304; };
+    auto tiled_bytes = [](const Job &j) {
+        return j.type == IQ1_M ? q38::tiled_iq1m_bytes(j.rows, j.nb) : q38::tiled_q4k_bytes(j.rows, j.nb);
     };
     auto add_group = [&](Group &g) {
         for_runs(g, 0, g.n, [&](int i, int j, uint64_t rows) {
             if (!supported(g.part[i])) return;
-            Job job{g.part[i].data, (uint32_t)rows, (uint32_t)(g.part[i].width / 256), {}};
+            Job job{g.part[i].data, (uint32_t)rows, (uint32_t)(g.part[i].width / 256), g.part[i].type, {}};
             uint64_t row = 0;
             for (int k = i; k < j; ++k) {
                 if (row % 16 == 0) job.targets.emplace_back(&g.part[k], row / 16);
@@ -931,7 +950,8 @@ bool build_tiled(Q38Model *m, uint32_t first, uint32_t last, bool with_eh, void 
         });
     };
     auto add_one = [&](DevTensor &t) {
-        if (supported(t)) jobs.push_back(Job{t.data, (uint32_t)t.rows, (uint32_t)(t.width / 256), {{&t, 0}}});
+        if (supported(t))
+            jobs.push_back(Job{t.data, (uint32_t)t.rows, (uint32_t)(t.width / 256), t.type, {{&t, 0}}});
     };
     for (uint32_t l = first; l < last; ++l) {
         Layer &L = m->layers[l];
@@ -945,7 +965,7 @@ bool build_tiled(Q38Model *m, uint32_t first, uint32_t last, bool with_eh, void 
     std::vector<size_t> offsets;
     for (const Job &j : jobs) {
         offsets.push_back(total);
-        total += align256(q38::tiled_q4k_bytes(j.rows, j.nb));
+        total += align256(tiled_bytes(j));
     }
     if (!total) return true;
     if (!hip_ok(hipMalloc(mem, total), "tiled weight allocation")) return false;
@@ -953,8 +973,10 @@ bool build_tiled(Q38Model *m, uint32_t first, uint32_t last, bool with_eh, void 
     for (size_t k = 0; k < jobs.size(); ++k) {
         const Job &j = jobs[k];
         uint8_t *dst = base + offsets[k];
-        if (!q38::launch_repack_q4k_tiles(dst, j.src, j.rows, j.nb, m->stream)) return report("tiled repack failed");
-        for (const auto &t : j.targets) t.first->tiled = dst + t.second * j.nb * 2304;
+        const bool ok = j.type == IQ1_M ? q38::launch_repack_iq1m_tiles(dst, j.src, j.rows, j.nb, m->stream)
+                                        : q38::launch_repack_q4k_tiles(dst, j.src, j.rows, j.nb, m->stream);
+        if (!ok) return report("tiled repack failed");
+        for (const auto &t : j.targets) t.first->tiled = dst + t.second * j.nb * tile_block(j.type);
     }
     return hip_ok(hipStreamSynchronize(m->stream), "tiled repack");
 }
@@ -973,10 +995,7 @@ bool gemm_group(Q38Model *m, const Group &g, int lo, int hi, uint32_t count, flo
             if (!gemm_float(m, a, count, xf, y, ldy, (uint32_t)rows, a.data)) ok = false;
             return;
         }
-        const uint32_t nb = (uint32_t)(a.width / 256);
-        if (count >= 2 && a.tiled &&
-            q38::launch_gemm_q4k_tiled((int)count, a.tiled, m->q8k, y, ldy, (uint32_t)rows, nb, m->stream))
-            return;
+        if (gemm_tiled(m, a, count, m->q8k, y, ldy, (uint32_t)rows)) return;
         if (!gemm_rows(m, a, count, m->q8k, y, ldy, (uint32_t)rows, a.data)) ok = false;
     });
     return ok;

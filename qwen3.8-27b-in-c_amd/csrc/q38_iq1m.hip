@@ -56,7 +56,7 @@ struct IQBlk {
 
 }  // namespace
 
-template <int MT, int NB, int S, int P>
+template <int MT, int NB, int S, int P, bool TILED>
 __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restrict__ w, const uint8_t *__restrict__ x,
                                                          float *__restrict__ y, uint32_t ldy, uint32_t rows,
                                                          const uint2 *__restrict__ grid)
@@ -86,7 +86,8 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
     for (int i = threadIdx.x; i < MT * NB; i += 64 * S)
         xs_s[i] = *reinterpret_cast<const float *>(x + (size_t)i * kQ8KBytes);
     const __amdgpu_buffer_rsrc_t wr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w), 0, rows * NB * kIQ1MBytes, kRawBuf);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w), 0,
+                                          (TILED ? ntiles * 16 : rows) * NB * kIQ1MBytes, kRawBuf);
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(x), 0, MT * NB * kQ8KBytes, kRawBuf);
     if (STAGE)
@@ -122,15 +123,16 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_mfma(const uint8_t *__restri
         const uint32_t row = tile * 16 + (uint32_t)r < rows ? tile * 16 + (uint32_t)r : rows - 1;
         int b = sw + S * (n % KB);
         b = b < NB ? b : NB - 1;   /* past the end: re-read the last block, unused */
-        const uint32_t woff = row * NB * kIQ1MBytes;
+        /* row-major: row `row`, block b; tiled: the 16 rows of block b of
+         * the tile are one contiguous 896 bytes */
+        const uint32_t woff = TILED ? (uint32_t)r * kIQ1MBytes : row * NB * kIQ1MBytes;
+        const int soff = TILED ? (int)((tile * NB + (uint32_t)b) * 16u * kIQ1MBytes) : b * kIQ1MBytes;
         IQBlk<TS> c;
-        const int2v qs = __builtin_bit_cast(
-            int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff + 8 * q, b * kIQ1MBytes, 0));
+        const int2v qs = __builtin_bit_cast(int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff + 8 * q, soff, 0));
         c.qs[0] = (uint32_t)qs[0];
         c.qs[1] = (uint32_t)qs[1];
-        c.qh = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, woff + 32 + 4 * q, b * kIQ1MBytes, 0);
-        const int2v sc = __builtin_bit_cast(
-            int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff + 48, b * kIQ1MBytes, 0));
+        c.qh = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, woff + 32 + 4 * q, soff, 0);
+        const int2v sc = __builtin_bit_cast(int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff + 48, soff, 0));
         c.sc[0] = (uint32_t)sc[0];
         c.sc[1] = (uint32_t)sc[1];
 #pragma unroll
@@ -236,37 +238,37 @@ constexpr int kIQ1MWaves = 4, kIQ1MWavesOneToken = 8;
 constexpr uint32_t kIQ1MGroups = 512;
 constexpr int kIQ1MPrefetch = 2;
 
-template <int MT, int NB, int S>
+template <int MT, int NB, int S, bool TILED>
 void launch_iq1m_s(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, const uint2 *grid,
                    hipStream_t stream)
 {
     const uint32_t tiles = (rows + 15) / 16;
     const uint32_t groups = tiles < kIQ1MGroups ? tiles : kIQ1MGroups;
-    hipLaunchKernelGGL((gemm_iq1m_mfma<MT, NB, S, kIQ1MPrefetch>), dim3(groups), dim3(64 * S), 0, stream, w, x, y,
+    hipLaunchKernelGGL((gemm_iq1m_mfma<MT, NB, S, kIQ1MPrefetch, TILED>), dim3(groups), dim3(64 * S), 0, stream, w, x, y,
                        ldy, rows, grid);
 }
 
-template <int MT, int NB>
+template <int MT, int NB, bool TILED>
 bool launch_iq1m_typed(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, const uint2 *grid,
                        hipStream_t stream)
 {
-    launch_iq1m_s<MT, NB, MT == 1 ? kIQ1MWavesOneToken : kIQ1MWaves>(w, x, y, ldy, rows, grid, stream);
+    launch_iq1m_s<MT, NB, MT == 1 ? kIQ1MWavesOneToken : kIQ1MWaves, TILED>(w, x, y, ldy, rows, grid, stream);
     return hipGetLastError() == hipSuccess;
 }
 
-template <int NB>
+template <int NB, bool TILED>
 bool launch_iq1m_nb(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                     const uint2 *grid, hipStream_t stream)
 {
     switch (m) {
-    case 1: return launch_iq1m_typed<1, NB>(w, x, y, ldy, rows, grid, stream);
-    case 2: return launch_iq1m_typed<2, NB>(w, x, y, ldy, rows, grid, stream);
-    case 3: return launch_iq1m_typed<3, NB>(w, x, y, ldy, rows, grid, stream);
-    case 4: return launch_iq1m_typed<4, NB>(w, x, y, ldy, rows, grid, stream);
-    case 5: return launch_iq1m_typed<5, NB>(w, x, y, ldy, rows, grid, stream);
-    case 6: return launch_iq1m_typed<6, NB>(w, x, y, ldy, rows, grid, stream);
-    case 7: return launch_iq1m_typed<7, NB>(w, x, y, ldy, rows, grid, stream);
-    case 8: return launch_iq1m_typed<8, NB>(w, x, y, ldy, rows, grid, stream);
+    case 1: return launch_iq1m_typed<1, NB, TILED>(w, x, y, ldy, rows, grid, stream);
+    case 2: return launch_iq1m_typed<2, NB, TILED>(w, x, y, ldy, rows, grid, stream);
+    case 3: return launch_iq1m_typed<3, NB, TILED>(w, x, y, ldy, rows, grid, stream);
+    case 4: return launch_iq1m_typed<4, NB, TILED>(w, x, y, ldy, rows, grid, stream);
+    case 5: return launch_iq1m_typed<5, NB, TILED>(w, x, y, ldy, rows, grid, stream);
+    case 6: return launch_iq1m_typed<6, NB, TILED>(w, x, y, ldy, rows, grid, stream);
+    case 7: return launch_iq1m_typed<7, NB, TILED>(w, x, y, ldy, rows, grid, stream);
+    case 8: return launch_iq1m_typed<8, NB, TILED>(w, x, y, ldy, rows, grid, stream);
     default: return false;
     }
 }
@@ -477,12 +479,62 @@ bool launch_gemm_iq1m_mfma(int m, const uint8_t *w, const uint8_t *x, float *y, 
     if (!rows || ldy < rows || !grid) return false;
     const uint2 *g = static_cast<const uint2 *>(grid);
     switch (nb) {
-    case 20: return launch_iq1m_nb<20>(m, w, x, y, ldy, rows, g, stream);
-    case 24: return launch_iq1m_nb<24>(m, w, x, y, ldy, rows, g, stream);
-    case 40: return launch_iq1m_nb<40>(m, w, x, y, ldy, rows, g, stream);
-    case 68: return launch_iq1m_nb<68>(m, w, x, y, ldy, rows, g, stream);
+    case 20: return launch_iq1m_nb<20, false>(m, w, x, y, ldy, rows, g, stream);
+    case 24: return launch_iq1m_nb<24, false>(m, w, x, y, ldy, rows, g, stream);
+    case 40: return launch_iq1m_nb<40, false>(m, w, x, y, ldy, rows, g, stream);
+    case 68: return launch_iq1m_nb<68, false>(m, w, x, y, ldy, rows, g, stream);
     default: return false;
     }
+}
+
+bool launch_gemm_iq1m_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                            uint32_t nb, const void *grid, hipStream_t stream)
+{
+    if (!rows || ldy < rows || !grid) return false;
+    const uint2 *g = static_cast<const uint2 *>(grid);
+    switch (nb) {
+    case 20: return launch_iq1m_nb<20, true>(m, w_tiled, x, y, ldy, rows, g, stream);
+    case 24: return launch_iq1m_nb<24, true>(m, w_tiled, x, y, ldy, rows, g, stream);
+    case 40: return launch_iq1m_nb<40, true>(m, w_tiled, x, y, ldy, rows, g, stream);
+    case 68: return launch_iq1m_nb<68, true>(m, w_tiled, x, y, ldy, rows, g, stream);
+    default: return false;
+    }
+}
+
+namespace {
+
+/* dst [tile][block][row % 16][56 bytes] from the row-major blocks, in 8-byte
+ * pieces (7 per block); rows past the last are zero */
+__global__ __launch_bounds__(256) void repack_iq1m_tiles_kernel(uint2 *__restrict__ dst, const uint8_t *__restrict__ src,
+                                                                uint32_t rows, uint32_t nb, size_t pieces)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= pieces) return;
+    const uint32_t k = (uint32_t)(i % 7);
+    const size_t blk = i / 7;                       /* (tile, block, row % 16) */
+    const uint32_t r = (uint32_t)(blk % 16);
+    const size_t tb = blk / 16;                     /* tile * nb + block */
+    const uint32_t b = (uint32_t)(tb % nb);
+    const uint32_t row = (uint32_t)(tb / nb) * 16 + r;
+    uint2 v = make_uint2(0, 0);
+    if (row < rows) __builtin_memcpy(&v, src + ((size_t)row * nb + b) * kIQ1MBytes + 8 * k, 8);
+    dst[i] = v;
+}
+
+}  // namespace
+
+size_t tiled_iq1m_bytes(uint32_t rows, uint32_t nb)
+{
+    return (size_t)((rows + 15) / 16) * nb * 16 * kIQ1MBytes;
+}
+
+bool launch_repack_iq1m_tiles(uint8_t *dst, const uint8_t *src, uint32_t rows, uint32_t nb, hipStream_t stream)
+{
+    if (!rows || !nb || (reinterpret_cast<uintptr_t>(dst) & 7)) return false;
+    const size_t pieces = tiled_iq1m_bytes(rows, nb) / 8;
+    hipLaunchKernelGGL(repack_iq1m_tiles_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream,
+                       reinterpret_cast<uint2 *>(dst), src, rows, nb, pieces);
+    return hipGetLastError() == hipSuccess;
 }
 
 }  // namespace q38

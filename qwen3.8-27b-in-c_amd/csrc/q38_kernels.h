@@ -28,6 +28,13 @@ bool launch_gemm_iq1m_wide(uint32_t tokens, const uint8_t *w, const uint8_t *x, 
 /* IQ1_M x Q8_K for 1..8 tokens on the matrix cores (row-major blocks) */
 bool launch_gemm_iq1m_mfma(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                            uint32_t nb, const void *grid, hipStream_t stream);
+/* the same over a 16-row tiled copy ([tile = row / 16][block][row % 16][56
+ * bytes], rows past the last zero), made by launch_repack_iq1m_tiles into
+ * tiled_iq1m_bytes(rows, nb) bytes (8-byte aligned) */
+bool launch_gemm_iq1m_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                            uint32_t nb, const void *grid, hipStream_t stream);
+size_t tiled_iq1m_bytes(uint32_t rows, uint32_t nb);
+bool launch_repack_iq1m_tiles(uint8_t *dst, const uint8_t *src, uint32_t rows, uint32_t nb, hipStream_t stream);
 bool launch_gemm_q4k_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                            uint32_t nb, hipStream_t stream);
 /* same product, 32 weight rows per wavefront (v_mfma_f32_32x32x16_f16) */

@@ -52,6 +52,7 @@ EXPORTS = ("q38_f16_to_f32", "q38_quantize_q8_k", "q38_tensor_gemv_q8_k", "q38_t
            "q38_prepare_iq1_s_repacks", "q38_release_iq1_s_repacks", "q38hip_gemm_f32", "q38hip_row_f32",
            "q38hip_quantize_q8_k", "q38hip_gemm_q8_k", "q38hip_argmax", "q38hip_argmax_noalloc", "q38hip_accept",
            "q38hip_tiled_q4k_bytes", "q38hip_repack_q4k_tiles", "q38hip_gemm_q8_k_tiled", "q38hip_attention_rows",
+           "q38hip_tiled_iq1m_bytes", "q38hip_repack_iq1m_tiles", "q38hip_gemm_q8_k_iq1m_tiled",
            "q38hip_sample", "q38hip_last_error", "q38hip_synchronize",
            "q38_model_open_gguf", "q38_model_attach_mtp_gguf", "q38_model_close", "q38_model_reset",
            "q38_model_forward_token", "q38_model_prefill", "q38_model_enable_mtp", "q38_model_mtp_forward",
@@ -86,6 +87,10 @@ def load_library(path=LIB_PATH):
     lib.q38hip_tiled_q4k_bytes.argtypes = [u32, u64]
     lib.q38hip_repack_q4k_tiles.argtypes = [vp, vp, u32, u64, vp]
     lib.q38hip_gemm_q8_k_tiled.argtypes = [vp, vp, u32, u64, vp, u32, vp]
+    lib.q38hip_tiled_iq1m_bytes.restype = u64
+    lib.q38hip_tiled_iq1m_bytes.argtypes = [u32, u64]
+    lib.q38hip_repack_iq1m_tiles.argtypes = [vp, vp, u32, u64, vp]
+    lib.q38hip_gemm_q8_k_iq1m_tiled.argtypes = [vp, vp, u32, u64, vp, u32, vp]
     lib.q38hip_argmax.argtypes = [vp, vp, u32, u32, vp]
     lib.q38hip_argmax_noalloc.argtypes = [vp, vp, u32, u32, vp]
     lib.q38hip_accept.argtypes = [vp, vp, vp, u32, vp]
@@ -222,6 +227,28 @@ def gemm_q8_k_tiled(tiled, width, rows, xq, batch, out=None):
         out = torch.empty((batch, rows), dtype=torch.float32, device=tiled.device)
     _check(lib().q38hip_gemm_q8_k_tiled(_dev_ptr(out), _dev_ptr(xq), batch, width, _dev_ptr(tiled), rows,
                                         _stream()), "q38hip_gemm_q8_k_tiled")
+    return out
+
+
+def repack_iq1m_tiles(weights, width, rows):
+    """weights: uint8 row-major IQ1_M rows on the GPU -> uint8 tiled copy."""
+    import torch
+    nbytes = int(lib().q38hip_tiled_iq1m_bytes(rows, width))
+    if nbytes == 0:
+        raise ValueError("bad tiled shape")
+    out = torch.empty(nbytes, dtype=torch.uint8, device=weights.device)
+    _check(lib().q38hip_repack_iq1m_tiles(_dev_ptr(out), _dev_ptr(weights), rows, width, _stream()),
+           "q38hip_repack_iq1m_tiles")
+    return out
+
+
+def gemm_q8_k_iq1m_tiled(tiled, width, rows, xq, batch, out=None):
+    """tiled: uint8 tiled IQ1_M copy on the GPU; returns float32 [batch, rows]."""
+    import torch
+    if out is None:
+        out = torch.empty((batch, rows), dtype=torch.float32, device=tiled.device)
+    _check(lib().q38hip_gemm_q8_k_iq1m_tiled(_dev_ptr(out), _dev_ptr(xq), batch, width, _dev_ptr(tiled), rows,
+                                             _stream()), "q38hip_gemm_q8_k_iq1m_tiled")
     return out
 
 

@@ -186,6 +186,44 @@ def test_tiled_repack_and_gemm_bit_exact(hip, oracle, device, rows, width):
         assert np.array_equal(bits(got), bits(want)), "M=%d" % m
 
 
+@pytest.mark.parametrize("rows,width", [(48, 5120), (1000, 5120), (520, 10240), (5136, 17408), (2064, 6144)])
+def test_tiled_iq1m_repack_and_gemm_bit_exact(hip, oracle, device, rows, width):
+    """16-row tiled IQ1_M copy ([tile][block][row % 16][56 bytes], zero rows
+    past the last): the repack equals the host restatement of the layout, and
+    the matrix-core kernel over it equals the oracle bit for bit for 1..8
+    tokens, with row counts that end inside a tile (1000, 520, 5136)."""
+    w = synth.matrix(IQ1_M, rows, width, seed=rows + 2 * width)
+    wd = to_dev(w, device)
+    tiled = hip.repack_iq1m_tiles(wd, width, rows)
+    nb = width // 256
+    tiles = (rows + 15) // 16
+    padded = np.zeros((tiles * 16, nb, 56), dtype=np.uint8)
+    padded[:rows] = w.reshape(rows, nb, 56)
+    want_layout = np.ascontiguousarray(padded.reshape(tiles, 16, nb, 56).transpose(0, 2, 1, 3)).reshape(-1)
+    assert tiled.cpu().numpy().tobytes() == want_layout.tobytes()
+    x = synth.activations(width, seed=rows * 5 + 3, count=8)
+    q = oracle.quantize(x.reshape(-1))
+    xq = hip.quantize_q8_k(to_dev(x, device))
+    for m in range(1, 9):
+        want = oracle.gemm(IQ1_M, w, rows, q[:m * nb], m)
+        got = hip.gemm_q8_k_iq1m_tiled(tiled, width, rows, xq[:m * nb * 292], m).cpu().numpy()
+        assert np.array_equal(bits(got), bits(want)), "M=%d" % m
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_tiled_iq1m_full_shape_matches_row_major(hip, device, m):
+    """34816x5120 (fused gate|up) and 5120x17408 (down) IQ1_M: the tiled copy's
+    kernel equals the row-major kernel bit for bit."""
+    for rows, width in ((34816, 5120), (5120, 17408)):
+        w = synth.matrix(IQ1_M, rows, width, seed=m + rows + 1)
+        wd = to_dev(w, device)
+        x = synth.activations(width, seed=m * 11 + width, count=m)
+        xq = hip.quantize_q8_k(to_dev(x, device))
+        want = hip.gemm_q8_k(wd, IQ1_M, width, rows, xq, m).cpu().numpy()
+        got = hip.gemm_q8_k_iq1m_tiled(hip.repack_iq1m_tiles(wd, width, rows), width, rows, xq, m).cpu().numpy()
+        assert np.array_equal(bits(got), bits(want)), (rows, width)
+
+
 @pytest.mark.parametrize("m", [2, 3, 4, 8])
 def test_tiled_gemm_full_shape_matches_row_major(hip, device, m):
     """34816x5120 (fused gate|up) and 5120x17408 (down): tiled = row-major kernels;
