@@ -271,9 +271,12 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
  * reading the untransformed projections in `qkv` and writing the prepared
  * values to `out` (same row stride and offsets).  The arithmetic per
  * element, including the L2 norm of each q/k head and row (the block's sum
- * over its 128 channels), is deltanet_prep_kernel's.  The block holding the
- * last row writes the conv state after the batch to slot *slot_ptr + rows;
- * block kQKV / 128 does beta / alpha. */
+ * over its 128 channels), is deltanet_prep_kernel's.  The blocks of row
+ * group 0 write the conv state after the batch to slot *slot_ptr + rows:
+ * they are the only readers of slot *slot_ptr, and each thread reads its
+ * channel's state before it writes, so the store stays ordered after the
+ * read also when rows is a multiple of kStateSlots (the same slot).  Block
+ * kQKV / 128 does beta / alpha. */
 constexpr int kPrepRows = 8;
 
 __global__ __launch_bounds__(128) void deltanet_prep_rows_kernel(float *__restrict__ out,
@@ -334,11 +337,18 @@ __global__ __launch_bounds__(128) void deltanet_prep_rows_kernel(float *__restri
         const float scale = div_rn(1.0f, fmaxf(sqrt_rn(sum), 1e-6f));
         *o = __fmul_rn(y, scale);
     }
-    if (t0 + tn == rows) {
+    if (t0 == 0) {
+        /* the inputs of rows rows-3 .. rows-1; row r < 0 is state entry 3 + r */
+        float last[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int r = rows - 3 + j;
+            last[j] = r >= 0 ? qkv[(long long)r * ld + ch] : st[3 + r];
+        }
         float *so = conv_state + (size_t)((slot0 + rows) % kStateSlots) * slot_stride + (size_t)ch * 3;
-        so[0] = s0;
-        so[1] = s1;
-        so[2] = s2;
+        so[0] = last[0];
+        so[1] = last[1];
+        so[2] = last[2];
     }
 }
 

@@ -86,7 +86,7 @@ def activations(width, seed, count=1):
 
 SYNTH_GGUF = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "synth", "q38_synth_gguf")
 MODEL_GGUF_BYTES = {"q4km": 15704910464, "iq1m": 7188425344, "accept": 15465926368, "accept_mtp": 1997090400,
-                    "mixed": 13753227904}
+                    "accept_all": 15704910464, "mixed": 13753227904}
 
 
 def write_model_gguf(path, seed, variant="q4km"):
@@ -94,7 +94,8 @@ def write_model_gguf(path, seed, variant="q4km"):
     to `path` unless a file of the expected size is already there.  Variants:
     q4km, iq1m, mixed (every other matrix format), and the checkpoint pair
     accept (64 blocks, an LM head with two live rows) + accept_mtp (its
-    separate MTP block)."""
+    separate MTP block), and accept_all (the q4km file with every LM head
+    row equal to row 0, so every draft is accepted)."""
     import subprocess
     expected = MODEL_GGUF_BYTES.get(variant)
     if expected and os.path.exists(path) and os.path.getsize(path) == expected:

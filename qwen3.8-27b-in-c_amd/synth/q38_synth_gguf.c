@@ -27,6 +27,11 @@
  *   accept_mtp  the matching separate MTP checkpoint (q38_model_attach_mtp_gguf):
  *               65-block metadata, token_embd, the same LM head and block 64
  *               with its nextn.* tensors.
+ * A third accepts every draft:
+ *   accept_all  the 65-block Q4_K_M file whose LM head rows all hold the
+ *               bytes of row 0: every logit of a row is the same value (a
+ *               function of the hidden state), so the target's and the MTP
+ *               head's greedy token is always 0 and every draft is accepted.
  * A tensor's bytes depend on its place in the full 65-block Q4_K_M list, so
  * tensors shared between variants are byte-identical.
  *
@@ -42,7 +47,7 @@
  * are the standard deviation of a block's weights at scale 1); Q2_K and Q5_K
  * mins are set to centre their sub-blocks as for Q4_K.
  *
- * Usage: q38_synth_gguf OUT.gguf SEED q4km|iq1m|accept|accept_mtp|mixed
+ * Usage: q38_synth_gguf OUT.gguf SEED q4km|iq1m|accept|accept_mtp|accept_all|mixed
  */
 #define _GNU_SOURCE
 #include <fcntl.h>
@@ -107,6 +112,7 @@ typedef struct {
     uint64_t nbytes;
     int kind;      /* 0 matrix, 1 norm weight, 2 conv, 3 dt bias, 4 ssm_a */
     int live_rows; /* > 0: only the first live_rows rows are non-zero */
+    int same_rows; /* every row holds the bytes of row 0 */
     int written;   /* part of the output file */
     uint64_t id;   /* seed index: place in the full tensor list */
 } Tensor;
@@ -378,7 +384,7 @@ static void generate(const Tensor *t, uint64_t seed, uint64_t tid, uint64_t begi
     const double fan_in = (double)t->shape[0];
     const uint64_t live_end = t->live_rows > 0 ? (uint64_t)t->live_rows * (t->shape[0] / 256) * bb : UINT64_MAX;
     for (uint64_t off = begin; off < end; off += bb) {
-        const uint64_t index = off / bb;
+        const uint64_t index = t->same_rows ? off / bb % (t->shape[0] / 256) : off / bb;
         uint8_t *b = out + (off - begin);
         if (off >= live_end) {
             memset(b, 0, bb);          /* zero block: d = 0, every weight 0 */
@@ -413,9 +419,11 @@ int main(int argc, char **argv)
 {
     const char *variant = argc == 4 ? argv[3] : "";
     const int accept = strcmp(variant, "accept") == 0, accept_mtp = strcmp(variant, "accept_mtp") == 0;
+    const int accept_all = strcmp(variant, "accept_all") == 0;
     mixed_variant = strcmp(variant, "mixed") == 0;
-    if (argc != 4 || (strcmp(variant, "q4km") && strcmp(variant, "iq1m") && !accept && !accept_mtp && !mixed_variant)) {
-        fprintf(stderr, "usage: %s OUT.gguf SEED q4km|iq1m|accept|accept_mtp|mixed\n", argv[0]);
+    if (argc != 4 || (strcmp(variant, "q4km") && strcmp(variant, "iq1m") && !accept && !accept_mtp && !accept_all &&
+                      !mixed_variant)) {
+        fprintf(stderr, "usage: %s OUT.gguf SEED q4km|iq1m|accept|accept_mtp|accept_all|mixed\n", argv[0]);
         return 2;
     }
     const uint64_t seed = strtoull(argv[2], NULL, 0);
@@ -428,6 +436,7 @@ int main(int argc, char **argv)
     for (int layer = 0; layer <= LAYERS; ++layer) add_layer(layer, m);
     int mtp_begin = first_mtp_tensor;
     while (mtp_begin < tensor_count && strncmp(tensors[mtp_begin].name, "blk.64.", 7) != 0) ++mtp_begin;
+    if (accept_all) tensors[2].same_rows = 1;
     if (accept || accept_mtp) {
         tensors[2].live_rows = 2;
         for (int i = 0; i < tensor_count; ++i) {
