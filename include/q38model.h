@@ -10,9 +10,14 @@
  * the reference.  Not reentrant: one caller thread per model.
  *
  * Supported checkpoints: the Qwen3.8-27B "qwen35" contract
- * (src/qwen38/qwen38_model.c:196-319) with Q4_K, Q6_K or IQ1_M matrices, a
- * Q4_K token embedding and F32 norm / conv / ssm vectors.  Other matrix types
- * are rejected at open with a message.
+ * (src/qwen38/qwen38_model.c:196-319) with every matrix type the reference
+ * accepts (q38_matrix_type_supported, qwen38_model.c:172-189): the Q8_K
+ * path types Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ1_S, IQ1_M, IQ2_XXS, IQ2_XS,
+ * IQ2_S, IQ3_XXS, IQ3_S, IQ4_XS and IQ4_NL, and the float-input types F32,
+ * F16, BF16 and Q8_0; F32 norm / conv / ssm vectors.  The token embedding
+ * may be any of these; for a type the reference's row decode has no case for
+ * (qwen38_quant.c:2768-2810: the IQ types but IQ4_NL) its rows are NaN, as
+ * in the reference.  Other types are rejected at open with a message.
  */
 #ifndef Q38MODEL_H
 #define Q38MODEL_H
@@ -77,6 +82,21 @@ int q38hip_model_sample(Q38Model *model, uint64_t *state, float temperature, flo
 int q38hip_model_forward_sample(Q38Model *model, uint32_t token_id, uint64_t *state, float temperature, float top_p,
                                 float presence_penalty, uint32_t top_k, const uint8_t *presence,
                                 uint32_t presence_size, uint32_t *next_token);
+
+/* Library extension for measurement (no counterpart in the reference): the
+ * device time of one block of the target model over `rows` (1..8) verify
+ * rows, as the speculative verify runs it, at positions position ..
+ * position + rows - 1 of the current cache.  `layer` is 0..63 (every fourth,
+ * 3, 7, .., a full-attention block).  The block is captured as a HIP graph
+ * and replayed `repeats` times between two events on the model's stream;
+ * *block_us is the mean time of one replay.  *tail_us is the same for the
+ * verify tail of a `rows`-row batch: the argmax of `rows` logits rows,
+ * the greedy acceptance and the gather of the returned logits row.  The
+ * call leaves the model's position, state slots and logits as they were
+ * (it writes only cache entries at and after `position`, which the next
+ * token overwrites before any read).  0 on bad arguments. */
+int q38hip_model_time_block(Q38Model *model, uint32_t layer, uint32_t rows, uint32_t repeats, float *block_us,
+                            float *tail_us);
 
 /* qwen38_model.h:48-50 */
 uint32_t q38_model_vocab_size(const Q38Model *model);

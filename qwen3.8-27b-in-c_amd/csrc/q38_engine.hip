@@ -1814,6 +1814,74 @@ int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_toke
     return 1;
 }
 
+/* Device time of one block over `rows` verify rows and of the verify tail
+ * (argmax, acceptance, row gather), each captured once as a graph and
+ * replayed `repeats` times between two events on the model's stream.  The
+ * block reads the hidden rows left in the scratch (their values do not
+ * change the work) and runs at positions position .. position + rows - 1;
+ * nothing the next call reads is changed: position and slots stay, the
+ * recurrent slots after the current one and the cache entries at and after
+ * `position` are rewritten by the next step before they are read. */
+int q38hip_model_time_block(Q38Model *m, uint32_t layer, uint32_t rows, uint32_t repeats, float *block_us,
+                            float *tail_us)
+{
+    begin_call();
+    if (!m || layer >= kLayers || rows == 0 || rows > kBatch || repeats == 0 || !block_us || !tail_us ||
+        rows > m->context_length - m->position)
+        return 0;
+    write_params(m, kParamTarget, m->position);
+    m->host_params[(size_t)kParamTarget * kParamWords + kParamStopWord] = 0xFFFFFFFFu;
+    const uint32_t zeros[kBatch] = {0};
+    if (!upload_tokens(m, zeros, rows, m->tokens) ||
+        !hip_ok(hipMemcpyAsync(m->drafts + 1, m->tokens, rows * sizeof(uint32_t), hipMemcpyDeviceToDevice,
+                               m->stream), "time block") ||
+        !flush_params(m) || !hip_ok(hipStreamSynchronize(m->stream), "time block"))
+        return 0;
+    const Step s = step_of(m, kParamTarget, m->tokens);
+    const uint32_t *stop = m->params + (size_t)kParamTarget * kParamWords + kParamStopWord;
+    auto block = [&] {
+        m->pending_branch = false;
+        const bool ok = layer_rows(m, s, (int)layer, rows);
+        m->pending_branch = false;
+        return ok;
+    };
+    auto tail = [&] {
+        q38::launch_argmax(m->logits, kVocab, rows, m->argmax_pv, m->argmax_pi, m->targets, m->stream);
+        q38::launch_accept(m->accept, m->targets, m->drafts + 1, rows, m->stream, stop);
+        q38::launch_copy_row(m->logits_stage, m->logits, kVocab, kVocab, m->accept, rows, m->stream);
+        return true;
+    };
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    bool ok = hip_ok(hipEventCreate(&e0), "event") && hip_ok(hipEventCreate(&e1), "event");
+    float *outs[2] = {block_us, tail_us};
+    for (int part = 0; ok && part < 2; ++part) {
+        /* one eager run (first-use allocations and module loads), then the graph */
+        ok = (part == 0 ? block() : tail()) && launches_ok();
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        ok = ok && hip_ok(hipStreamSynchronize(m->stream), "time block") &&
+             hip_ok(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal), "graph capture");
+        if (ok) {
+            const bool body = (part == 0 ? block() : tail()) && launches_ok();
+            ok = hip_ok(hipStreamEndCapture(m->stream, &graph), "graph capture") && body;
+        }
+        ok = ok && hip_ok(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "graph instantiate");
+        if (graph) (void)hipGraphDestroy(graph);
+        /* warm replays, then the timed ones */
+        for (uint32_t i = 0; ok && i < 3; ++i) ok = hip_ok(hipGraphLaunch(exec, m->stream), "graph launch");
+        ok = ok && hip_ok(hipEventRecord(e0, m->stream), "event");
+        for (uint32_t i = 0; ok && i < repeats; ++i) ok = hip_ok(hipGraphLaunch(exec, m->stream), "graph launch");
+        ok = ok && hip_ok(hipEventRecord(e1, m->stream), "event") && hip_ok(hipEventSynchronize(e1), "event");
+        float ms = 0.0f;
+        ok = ok && hip_ok(hipEventElapsedTime(&ms, e0, e1), "event");
+        if (ok) *outs[part] = ms * 1e3f / (float)repeats;
+        if (exec) (void)hipGraphExecDestroy(exec);
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    return ok ? 1 : 0;
+}
+
 uint32_t q38_model_vocab_size(const Q38Model *m) { return m ? kVocab : 0; }
 uint32_t q38_model_position(const Q38Model *m) { return m ? m->position : 0; }
 uint32_t q38_model_context_length(const Q38Model *m) { return m ? m->context_length : 0; }

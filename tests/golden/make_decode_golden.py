@@ -8,8 +8,9 @@
         prompt followed by speculative_greedy(k=3, no stop token) until 256
         tokens are produced.
   iq1m  IQ1_M layout: a 4096-token prompt (seed 11) prefilled as one batch,
-        then speculative_greedy(k=3) until 32 tokens are produced and, from
-        a reset, the same prompt followed by 16 greedy tokens.
+        then speculative_greedy(k=3) until 1024 tokens are produced and, from
+        a reset, the same prompt followed by 1024 greedy tokens (context
+        4097-5120, the benchmark's IQ1_M decode).
 
 Stored per scenario: the token ids, the accepted counts, and the SHA-256 of
 every returned logits row (prefill included), plus a strided sample of the
@@ -17,7 +18,7 @@ prefill logits.  The reference's own invariant is asserted as the fixture is
 written: its speculative tokens equal its greedy tokens
 (src/cli/qwen38_spec_bench.c:100-119).
 
-Run from the repository root (about 10 min for q4km and 25 min for iq1m on
+Run from the repository root (about 10 min for q4km and 2 h for iq1m on
 8 cores):
   python tests/golden/make_decode_golden.py q4km|iq1m [GGUF_PATH]
 """
@@ -38,7 +39,7 @@ NO_STOP = 0xFFFFFFFF
 DRAFT = 3
 SAMPLE_STRIDE = 1009
 # variant: (prompt tokens, speculative tokens, greedy tokens)
-SIZES = {"q4km": (512, 256, 256), "iq1m": (4096, 32, 16)}
+SIZES = {"q4km": (512, 256, 256), "iq1m": (4096, 1024, 1024)}
 
 
 def prompt_ids(count, seed=PROMPT_SEED):
@@ -85,6 +86,8 @@ def run(model, variant, log):
         logits = model.forward_token(tokens[-1])
         greedy_digests.append(digest(logits))
         tokens.append(argmax(logits))
+        if len(tokens) % 128 == 0:
+            log("greedy: %d tokens" % len(tokens))
     out["greedy_tokens"] = np.array(tokens, dtype=np.uint32)
     out["greedy_digests"] = np.array(greedy_digests)
     log("greedy done")
