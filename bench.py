@@ -66,20 +66,27 @@ WORKLOADS = {
     "q6k_gemv": (14, 17408, 5120, 1, False, "Q6_K GEMV 17408x5120"),
     "q4k_tiled_m3": (12, 34816, 5120, 3, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 3 tokens"),
     "q4k_tiled_down_m3": (12, 5120, 17408, 3, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 3 tokens"),
+    "q4k_tiled_out_m3": (12, 5120, 6144, 3, True,
+                         "Q4_K tiled GEMM 5120x6144 (attention output / DeltaNet output), 3 tokens"),
     "iq1m_gemm_m3": (29, 34816, 5120, 3, True, "IQ1_M GEMM 34816x5120 (FFN gate|up), 3 tokens"),
     "q4k_tiled_m8": (12, 34816, 5120, 8, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
     "iq1m_gemm_m8": (29, 34816, 5120, 8, True, "IQ1_M GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
     "q4k_wide_m256": (12, 34816, 5120, 256, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 256 tokens (prefill)"),
     "iq1m_wide_m256": (29, 34816, 5120, 256, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 256 tokens (prefill)"),
     "q4k_wide_down_m256": (12, 5120, 17408, 256, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 256 tokens (prefill)"),
+    "q4k_wide_m512": (12, 34816, 5120, 512, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 512 tokens (prefill)"),
+    "iq1m_wide_m512": (29, 34816, 5120, 512, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 512 tokens (prefill)"),
 }
 # device kernel each launch of a workload runs (q38hip dispatch for that shape; the
 # trace summaries and counter profiles under profiles/ name the same kernels)
 DEVICE_KERNEL = {
     "q4k_gemv": "gemm_q8k_stream<12, 1>",
+    "q4k_gemv_t": "gemm_q8k_ring<12, 1, 3, 16, 2>",
     "iq1m_gemv": "gemm_iq1m_mfma<1, 20, 8, 2, true>",
+    "iq1m_gemv_t": "gemm_iq1m_mfma<1, 68, 8, 2, true>",
     "q4k_tiled_m3": "gemm_q4k_mm16<3, 20, 9, 4, 1>",
-    "q4k_tiled_down_m3": "gemm_q4k_t32<3, 68, 4, 2>",
+    "q4k_tiled_down_m3": "gemm_q4k_t32r<3, 68, 8, 1>",
+    "q4k_tiled_out_m3": "gemm_q4k_t32r<3, 24, 8, 1>",
     "iq1m_gemm_m3": "gemm_iq1m_mfma<3, 20, 4, 2, true>",
 }
 # dense matrix-core peaks of MI355X, TOP/s: the Q4_K GEMM runs fp16 MFMA, IQ1_M int8
@@ -94,7 +101,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=None)
     p.add_argument("--warmup", type=int, default=None)
-    p.add_argument("--workload", default="decode", choices=["decode"] + sorted(WORKLOADS) + ["copy"])
+    p.add_argument("--workload", default="decode", choices=["decode", "prefill"] + sorted(WORKLOADS) + ["copy"])
     p.add_argument("--decode-tokens", type=int, default=None,
                    help="tokens decoded on every run (256 for q4km, 1024 for iq1m); --steps picks the timed window")
     p.add_argument("--layout", default="q4km", choices=["q4km", "iq1m"],
@@ -104,7 +111,12 @@ def parse():
     p.add_argument("--plain-tokens", type=int, default=32, help="plain greedy tokens after the timed region")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time per thread count")
+    p.add_argument("--no-extra", action="store_true",
+                   help="decode: only the headline line (no verify block, IQ1_M or accepted-draft runs)")
     p.add_argument("--cpu-worker", action="store_true", help=argparse.SUPPRESS)
+    p.add_argument("--cpu-gemv-worker", action="store_true", help=argparse.SUPPRESS)
+    p.add_argument("--cpu-workloads", default="", help=argparse.SUPPRESS)
+    p.add_argument("--cpu-calls", type=int, default=30, help=argparse.SUPPRESS)
     p.add_argument("--cpu-threads", default="", help=argparse.SUPPRESS)
     p.add_argument("--trace-summary", metavar="DIR", help="summarise a rocprofv3 kernel trace and exit")
     p.add_argument("--trace-transactions", type=int, default=0,
@@ -284,9 +296,9 @@ def trace_summary(directory, transactions=0):
         names = [r["short"] for r in rows]
         prefill = ("gemm_q4k_wide", "gemm_iq1m_wide", "gemm_q4k_tiled<8", "gemm_q4k_t32<8", "gemm_iq1m_mfma<8")
         first = max(i for i, n in enumerate(names) if n.startswith(prefill)) + 1
-        # the decode ends with the last transaction's acceptance kernel (the
+        # the decode ends with the last transaction's verify tail (the
         # roofline runs that follow launch none); the wall clock stops there
-        last = max(i for i, n in enumerate(names) if n.startswith("accept_kernel")) + 1
+        last = max(i for i, n in enumerate(names) if n.startswith(("accept_kernel", "verify_tail_kernel"))) + 1
         rows = rows[first:last]
         wall =int(rows[-1]["End_Timestamp"]) - int(rows[0]["Start_Timestamp"])
         busy = sum(r["ns"] for r in rows)
@@ -373,23 +385,100 @@ def cpu_decode_worker(args):
     print(json.dumps({"prefill_s": round(prefill_s, 2), "runs": runs}))
 
 
-def cpu_decode_baseline(args, label="Q4_K_M"):
+def cpu_gemv_worker(args):
+    """Child process of the GEMV baselines (no GPU use): the reference's
+    q38_quantize_q8_k + q38_tensor_gemv_q8_k (oracle/_ref, AVX2 + OpenMP
+    build of src/qwen38/qwen38_quant.c) on the GEMV workloads of
+    --cpu-workloads, each call timed on its own: warm-up, then the median of
+    --cpu-calls calls at each thread count of --cpu-threads.  The weights
+    rotate over >= 2 GB of copies so every call streams from DRAM.  Prints
+    one JSON line."""
+    import ctypes
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Reference
+    from q38hip import synth
+    ref = Reference()
+    gomp = ctypes.CDLL("libgomp.so.1")
+    threads = [int(t) for t in args.cpu_threads.split(",")]
+    out = {}
+    for workload in args.cpu_workloads.split(","):
+        qtype, rows, width, tokens, _, label = WORKLOADS[workload]
+        base = synth.matrix(qtype, rows, width, seed=1)
+        copies = max(2, -(-(2 << 30) // base.nbytes))
+        weights = [base] + [base.copy() for _ in range(copies - 1)]
+        x = synth.activations(width, seed=2).reshape(-1)
+        runs = []
+        for n in threads:
+            gomp.omp_set_num_threads(n)
+            for i in range(3):
+                ref.gemv(qtype, weights[i % copies], rows, ref.quantize(x))
+            times = []
+            for i in range(args.cpu_calls):
+                t0 = time.perf_counter()
+                ref.gemv(qtype, weights[i % copies], rows, ref.quantize(x))
+                times.append(time.perf_counter() - t0)
+            med = float(np.median(times))
+            runs.append({"threads": n, "median_us": round(med * 1e6, 1), "calls": len(times),
+                         "GB_s": round(algorithmic_bytes(qtype, rows, width) / med / 1e9, 3)})
+        out[workload] = {"runs": runs, "copies": copies, "label": label}
+    print(json.dumps(out))
+
+
+def cpu_threads_plan():
+    """(host info, thread counts): all physical cores of this process's CPU
+    share, and 12 (the reference CLI's default, src/cli/qwen38_main.c:
+    1431-1432) when different"""
+    info = host_cpu_info()
+    cores = min(info["physical_cores"] or info["usable_cpus"], info["usable_cpus"])
+    return info, [cores] + ([12] if cores != 12 else [])
+
+
+def cpu_gemv_baselines(workloads, calls=30):
+    """The reference GEMV on the host cores for each workload (child process,
+    OpenMP threads bound to cores); {workload: cpu_baseline object}."""
+    import subprocess
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Reference
+    if not Reference.available():
+        return {}
+    info, threads = cpu_threads_plan()
+    env = dict(os.environ, OMP_NUM_THREADS=str(threads[0]), OMP_PROC_BIND="close", OMP_PLACES="cores")
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-gemv-worker", "--cpu-workloads", ",".join(workloads),
+           "--cpu-calls", str(calls), "--cpu-threads", ",".join(str(t) for t in threads)]
+    out = subprocess.run(cmd, env=env, capture_output=True, text=True)
+    if out.returncode != 0:
+        return {w: {"value": None, "error": out.stderr[-400:]} for w in workloads}
+    res = json.loads(out.stdout.strip().splitlines()[-1])
+    result = {}
+    for w, r in res.items():
+        main = r["runs"][0]
+        result[w] = {"value": main["GB_s"], "unit": "GB/s", "cores": main["threads"], "kind": "reference",
+                     "median_us": main["median_us"],
+                     "sample": "median of %d calls of q38_quantize_q8_k + q38_tensor_gemv_q8_k (AVX2 + OpenMP build "
+                               "of the reference's own sources), %s, weights rotated over %d copies, after 3 "
+                               "warm-up calls, per thread count" % (main["calls"], r["label"], r["copies"]),
+                     "runs": r["runs"], "host": info}
+    return result
+
+
+def cpu_decode_baseline(args, label="Q4_K_M", layout=None, prompt=None, seconds=None):
     """The reference engine on the host cores, run in a child process (it
-    never touches the GPU) on the same GGUF and prompt as the GPU run: one
-    sample on all physical cores (OMP_PROC_BIND=close, OMP_PLACES=cores), one
-    at 12 threads, the reference CLI's default (src/cli/qwen38_main.c:
+    never touches the GPU) on the same GGUF as the GPU run: one sample on all
+    physical cores (OMP_PROC_BIND=close, OMP_PLACES=cores), one at 12
+    threads, the reference CLI's default (src/cli/qwen38_main.c:
     1431-1432)."""
     import subprocess
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Reference
     if not Reference.available():
         return None
-    info = host_cpu_info()
-    cores = min(info["physical_cores"] or info["usable_cpus"], info["usable_cpus"])
-    threads = [cores] + ([12] if cores != 12 else [])
-    env = dict(os.environ, OMP_NUM_THREADS=str(cores), OMP_PROC_BIND="close", OMP_PLACES="cores")
-    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-worker", "--layout", args.layout,
-           "--prompt", str(args.prompt), "--draft", str(args.draft), "--cpu-seconds", str(args.cpu_seconds),
+    layout = layout or args.layout
+    prompt = prompt or args.prompt
+    seconds = seconds or args.cpu_seconds
+    info, threads = cpu_threads_plan()
+    env = dict(os.environ, OMP_NUM_THREADS=str(threads[0]), OMP_PROC_BIND="close", OMP_PLACES="cores")
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-worker", "--layout", layout,
+           "--prompt", str(prompt), "--draft", str(args.draft), "--cpu-seconds", str(seconds),
            "--cpu-threads", ",".join(str(t) for t in threads)]
     out = subprocess.run(cmd, env=env, capture_output=True, text=True)
     if out.returncode != 0:
@@ -398,10 +487,12 @@ def cpu_decode_baseline(args, label="Q4_K_M"):
     main = res["runs"][0]
     return {"value": main["tokens_per_s"], "unit": "tokens/s", "cores": main["threads"], "kind": "reference",
             "sample": "reference engine (AVX2 + OpenMP build of its own sources) on the same synthetic 27B %s "
-                      "GGUF and %d-token prompt (prefill %.1f s), then q38_model_speculative_greedy(k=%d) "
-                      "transactions for %.0f s per thread count" % (label, args.prompt, res["prefill_s"], args.draft,
-                                                                      args.cpu_seconds),
-            "runs": res["runs"], "prefill_s": res["prefill_s"], "host": info}
+                      "GGUF and a %d-token prompt (prefill %.1f s), then q38_model_speculative_greedy(k=%d) "
+                      "transactions for %.0f s per thread count" % (label, prompt, res["prefill_s"], args.draft,
+                                                                      seconds),
+            "runs": res["runs"], "prefill_s": res["prefill_s"],
+            "prefill_tokens_per_s": round(prompt / res["prefill_s"], 2) if res["prefill_s"] else None,
+            "host": info}
 
 
 LAYOUTS = {
@@ -409,8 +500,13 @@ LAYOUTS = {
     "q4km": ("Q4_K_M", "q4k_tiled_m3", 512, 256),
     "iq1m": ("IQ1_M", "iq1m_gemm_m3", 4096, 1024),
 }
-# single-row GEMV rooflines reported beside the decode line (17408 x 5120)
-GEMV_ROOFLINES = ("q4k_gemv", "iq1m_gemv")
+# single-row GEMV rooflines reported beside the decode line, both shapes
+GEMV_ROOFLINES = ("q4k_gemv", "q4k_gemv_t", "iq1m_gemv", "iq1m_gemv_t")
+# the verify block: layer 3 (the first full-attention block) over a 2048-token cache
+VERIFY_LAYER, VERIFY_CACHE, VERIFY_ROWS = 3, 2048, (1, 2, 3, 4, 5)
+# Q4_K bytes of one full-attention block: q+gate 12288 rows, k and v 1024 rows
+# (20 blocks each), output 5120 x 24 blocks, gate|up 34816 x 20, down 5120 x 68
+BLOCK_WEIGHT_BYTES = 144 * (14336 * 20 + 5120 * 24 + 34816 * 20 + 5120 * 68)
 
 
 def decode_fixture(layout):
@@ -423,30 +519,32 @@ def decode_fixture(layout):
     return [int(t) for t in g["spec_tokens"]] if int(g["prompt_len"][0]) else None
 
 
-def run_decode(torch, args):
+def decode_measure(torch, variant, prompt_len, decode_tokens, draft, warmup=8, window=None, plain_tokens=0,
+                   mtp_variant=None, fixture=None):
+    """Open the synthetic `variant` model (and the separate MTP checkpoint
+    `mtp_variant`, if any), prefill `prompt_len` random ids, then decode
+    through q38_model_speculative_greedy(k=draft) until `decode_tokens` are
+    produced (or warmup + window transactions ran), timing the transactions
+    after the first `warmup`; then `plain_tokens` plain greedy steps."""
     from q38hip import synth
     from q38hip.model import Model
-    label, roof_workload, default_prompt, default_tokens = LAYOUTS[args.layout]
-    if args.prompt is None:
-        args.prompt = default_prompt
-    decode_tokens = args.decode_tokens if args.decode_tokens is not None else default_tokens
-    warmup = args.warmup if args.warmup is not None else 8
-    path = synth.model_path(1, args.layout)
+    path = synth.model_path(1, variant)
     if path is None:
         raise SystemExit("no directory with room for the synthetic model (set Q38_MODEL_DIR)")
     t0 = time.perf_counter()
-    synth.write_model_gguf(path, 1, args.layout)
+    synth.write_model_gguf(path, 1, variant)
+    mtp_path = None
+    if mtp_variant:
+        mtp_path = synth.write_model_gguf(synth.model_path(1, mtp_variant), 1, mtp_variant)
     t_synth = time.perf_counter() - t0
-    # every run decodes `decode_tokens` tokens; the timed window is transactions
-    # [warmup, warmup + steps) (default: all after the warm-up)
-    window = args.steps
-    context = (args.prompt + max(decode_tokens, (warmup + (window or 0)) * args.draft) + 4 * args.draft +
-               args.plain_tokens + 16)
+    context = prompt_len + max(decode_tokens, (warmup + (window or 0)) * draft) + 4 * draft + plain_tokens + 16
     t0 = time.perf_counter()
     model = Model.open(path, context)
+    if mtp_path:
+        model.attach_mtp(mtp_path)
     t_open = time.perf_counter() - t0
     model.enable_mtp()
-    prompt = prompt_ids(args.prompt)
+    prompt = prompt_ids(prompt_len)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     logits = model.prefill(prompt)
@@ -459,7 +557,7 @@ def run_decode(torch, args):
         if done == warmup:
             torch.cuda.synchronize()
             t_start = time.perf_counter()
-        accepted, _ = model.speculative_greedy(sequence[-1], 0xFFFFFFFF, args.draft, logits=False)
+        accepted, _ = model.speculative_greedy(sequence[-1], 0xFFFFFFFF, draft, logits=False)
         sequence.extend(int(t) for t in accepted)
         done += 1
         if done > warmup:
@@ -475,51 +573,163 @@ def run_decode(torch, args):
     wall = t_end - t_start
     steps = len(counts) if window is None else window
     produced = sum(counts[:steps])
-    want = decode_fixture(args.layout)
-    n = min(len(want), len(sequence)) if want else 0
-    parity = (sequence[:n] == want[:n]) if want else None
-    # plain greedy decode on the same model (no MTP) for reference
-    plain_n = args.plain_tokens
+    n = min(len(fixture), len(sequence)) if fixture else 0
+    parity = (sequence[:n] == fixture[:n]) if fixture else None
     token = sequence[-1]
     t1 = time.perf_counter()
-    for _ in range(plain_n):
+    for _ in range(plain_tokens):
         token = int(np.argmax(model.forward_token(token)))
     plain_wall = time.perf_counter() - t1
     model.close()
+    return {"tokens_per_s": round(produced / wall, 3), "ms_per_step": round(wall * 1e3 / steps, 4), "steps": steps,
+            "warmup": warmup, "prompt_tokens": prompt_len, "context": context,
+            "decoded_tokens": len(sequence) - 1, "transactions": done, "timed_transactions": steps,
+            "timed_tokens": produced, "accepted_per_transaction": round(produced / steps, 4),
+            "token_parity_with_reference": parity, "token_parity_checked": n,
+            "prefill_s": round(t_prefill, 3), "prefill_tokens_per_s": round(prompt_len / t_prefill, 1),
+            "open_upload_s": round(t_open, 3), "synth_s": round(t_synth, 3),
+            "plain_greedy_tokens_per_s": round(plain_tokens / plain_wall, 3) if plain_tokens else None}
 
+
+def committed_mfma(workload):
+    """MFMA busy fraction of a workload's kernel from the committed counter
+    summary profiles/mfma_util.*.pmc.txt (a line 'mfma_busy <workload>: F'),
+    or None"""
+    for path in glob.glob(os.path.join(ROOT, "profiles", "mfma_util.*.pmc.txt")):
+        with open(path) as f:
+            m = re.search(r"^mfma_busy %s:\s*([0-9.]+)" % re.escape(workload), f.read(), re.M)
+        if m:
+            return float(m.group(1))
+    return None
+
+
+def verify_block_measure(torch):
+    """cfg3: one full-attention block of the Q4_K_M model over `rows` verify
+    rows at a 2048-token cache, as the speculative verify runs it, and the
+    verify tail (argmax of the rows' logits, acceptance, row gather);
+    device times from q38hip_model_time_block."""
+    import ctypes
+    from q38hip import synth
+    from q38hip.model import Model
+    path = synth.write_model_gguf(synth.model_path(1, "q4km"), 1, "q4km")
+    model = Model.open(path, VERIFY_CACHE + 64)
+    model.enable_mtp()
+    lib = model.lib
+    lib.q38hip_model_time_block.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                            ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]
+    model.prefill(prompt_ids(VERIFY_CACHE, seed=3))
+    rows_out = {}
+    for rows in VERIFY_ROWS:
+        b, t = ctypes.c_float(), ctypes.c_float()
+        if not lib.q38hip_model_time_block(model.handle, VERIFY_LAYER, rows, 200, ctypes.byref(b), ctypes.byref(t)):
+            raise SystemExit("q38hip_model_time_block failed")
+        # weights + K and V of every cached position (fp32) + Q8_K inputs and fp32 outputs of the projections
+        kv = (VERIFY_CACHE + rows) * 1024 * 4 * 2
+        act = rows * ((20 + 24 + 20 + 68) * 292 + (14336 + 5120 + 34816 + 5120) * 4)
+        nbytes = BLOCK_WEIGHT_BYTES + kv + act
+        rows_out[str(rows)] = {"block_us": round(b.value, 2), "tail_us": round(t.value, 2), "bytes": nbytes,
+                               "achieved_GB_s": round(nbytes / (b.value * 1e-6) / 1e9, 1),
+                               "frac": round(nbytes / (b.value * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+    model.close()
+    return {"workload": "one full-attention block (layer %d) of the 27B Q4_K_M model over k+1 verify rows at a "
+                        "%d-token cache, then the verify tail (argmax of the rows' 248320 logits, greedy "
+                        "acceptance, logits row gather); each a captured graph replayed 200 times "
+                        "(q38hip_model_time_block)" % (VERIFY_LAYER, VERIFY_CACHE),
+            "weights_bytes": BLOCK_WEIGHT_BYTES, "time_at_peak_us": round(BLOCK_WEIGHT_BYTES / PEAK_HBM_GBS / 1e3, 2),
+            "rows": rows_out,
+            "gate_up_mfma_busy": committed_mfma("q4k_tiled_m3")}
+
+
+def run_prefill(torch, args):
+    """The prompt evaluation alone (q38_model_prefill): the layout's model,
+    its default prompt, one untimed call (module loads, first-use
+    allocations), a reset, then one timed call.  Prints one JSON line."""
+    from q38hip import synth
+    from q38hip.model import Model
+    label, _, default_prompt, _ = LAYOUTS[args.layout]
+    prompt_len = args.prompt or default_prompt
+    path = synth.write_model_gguf(synth.model_path(1, args.layout), 1, args.layout)
+    model = Model.open(path, prompt_len + 16)
+    model.enable_mtp()
+    prompt = prompt_ids(prompt_len)
+    model.prefill(prompt)
+    model.reset()
+    model.enable_mtp()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    model.prefill(prompt)
+    wall = time.perf_counter() - t0
+    model.close()
+    print(json.dumps({"metric": "prefill tokens/s (27B %s, MTP catch-up included)" % label,
+                      "value": round(prompt_len / wall, 1), "unit": "tokens/s", "n_gpus": 1, "steps": 1,
+                      "warmup": 1, "ms_per_step": round(wall * 1e3, 3), "higher_is_better": True,
+                      "config": {"workload": "prefill of a %d-token random prompt" % prompt_len}}))
+
+
+def run_decode(torch, args):
+    label, roof_workload, default_prompt, default_tokens = LAYOUTS[args.layout]
+    if args.prompt is None:
+        args.prompt = default_prompt
+    decode_tokens = args.decode_tokens if args.decode_tokens is not None else default_tokens
+    warmup = args.warmup if args.warmup is not None else 8
+    d = decode_measure(torch, args.layout, args.prompt, decode_tokens, args.draft, warmup, args.steps,
+                       args.plain_tokens, fixture=decode_fixture(args.layout))
     _, _, roofline, copies = kernel_roofline(torch, roof_workload, 200, 20)
     gemv = {}
     for workload in GEMV_ROOFLINES:
         _, _, r, _ = kernel_roofline(torch, workload, 200, 20)
         gemv[workload] = {k: r[k] for k in ("kernel", "achieved", "frac", "launch_us", "bytes_per_launch",
                                             "traffic")}
+    config = {"workload": "decode 27B %s + MTP k=%d" % (label, args.draft), "layers": 64, "hidden": 5120,
+              "ffn": 17408, "vocab": 248320}
+    config.update({k: d[k] for k in ("prompt_tokens", "context", "decoded_tokens", "transactions",
+                                     "timed_transactions", "timed_tokens", "accepted_per_transaction",
+                                     "token_parity_with_reference", "token_parity_checked", "prefill_s",
+                                     "prefill_tokens_per_s", "open_upload_s", "synth_s",
+                                     "plain_greedy_tokens_per_s")})
     result = {
         "metric": "decode tokens/s (27B %s + MTP k=%d, greedy)" % (label, args.draft),
-        "value": round(produced / wall, 3),
+        "value": d["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": steps,
+        "steps": d["steps"],
         "warmup": warmup,
-        "ms_per_step": round(wall * 1e3 / steps, 4),
+        "ms_per_step": d["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "i8x%s/Q6_K->i32, f32" % ("Q4_K" if args.layout == "q4km" else "IQ1_M"),
         "data": "synthetic (seeded random-init 27B %s GGUF, random prompt ids)" % label,
-        "config": {"workload": "decode 27B %s + MTP k=%d" % (label, args.draft), "layers": 64, "hidden": 5120,
-                   "ffn": 17408, "vocab": 248320, "prompt_tokens": args.prompt, "context": context,
-                   "decoded_tokens": len(sequence) - 1, "transactions": done,
-                   "timed_transactions": steps, "timed_tokens": produced,
-                   "accepted_per_transaction": round(produced / steps, 4),
-                   "token_parity_with_reference": parity, "token_parity_checked": n,
-                   "prefill_s": round(t_prefill, 3),
-                   "prefill_tokens_per_s": round(args.prompt / t_prefill, 1), "open_upload_s": round(t_open, 3),
-                   "synth_s": round(t_synth, 3),
-                   "plain_greedy_tokens_per_s": round(plain_n / plain_wall, 3) if plain_n else None},
+        "config": config,
         "roofline": roofline,
         "gemv_rooflines": gemv,
         "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(args, label),
     }
+    if args.layout == "q4km" and not args.no_extra:
+        # the other configurations of the path, measured in the same run
+        if not args.no_cpu:
+            for w, b in cpu_gemv_baselines(GEMV_ROOFLINES).items():
+                gemv[w]["cpu_baseline"] = b
+        result["verify_block"] = verify_block_measure(torch)
+        c5 = decode_measure(torch, "iq1m", 4096, 1024, args.draft, warmup=8, fixture=decode_fixture("iq1m"))
+        c5["workload"] = ("27B IQ1_M layout (IQ1_M layer matrices, Q4_K embedding, Q6_K LM head): a 4096-token "
+                          "prompt prefilled in 512-token batches on the matrix cores, then 1024 tokens decoded with "
+                          "MTP k=%d (context 4097-5120)" % args.draft)
+        c5["prefill_mfma_busy"] = {w: committed_mfma(w) for w in ("iq1m_wide_m512", "q4k_wide_m512")}
+        c5["cpu_baseline"] = None if args.no_cpu else cpu_decode_baseline(args, "IQ1_M", layout="iq1m", prompt=128,
+                                                                           seconds=10.0)
+        result["iq1m_prefill_decode"] = c5
+        acc = {}
+        for name, variant, mtp in (("all_drafts_accepted", "accept_all", None),
+                                   ("accept_pair", "accept", "accept_mtp")):
+            a = decode_measure(torch, variant, 512, 96, args.draft, warmup=4, mtp_variant=mtp)
+            acc[name] = {k: a[k] for k in ("tokens_per_s", "ms_per_step", "timed_transactions", "timed_tokens",
+                                           "accepted_per_transaction", "prefill_tokens_per_s")}
+        acc["note"] = ("all_drafts_accepted: the Q4_K_M model with every LM head row equal, so every draft is "
+                       "accepted; accept_pair: the 64-block model with a two-row LM head and its separate MTP "
+                       "checkpoint, where about a third of the drafts are accepted; 512-token prompt, k=%d"
+                       % args.draft)
+        result["accepted_drafts"] = acc
     print(json.dumps(result))
 
 
@@ -531,6 +741,9 @@ def main():
     if args.cpu_worker:
         cpu_decode_worker(args)
         return
+    if args.cpu_gemv_worker:
+        cpu_gemv_worker(args)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",
               file=sys.stderr)
@@ -541,6 +754,9 @@ def main():
         return
     if args.workload == "decode":
         run_decode(torch, args)
+        return
+    if args.workload == "prefill":
+        run_prefill(torch, args)
         return
     qtype, rows, width, tokens, tiled, label = WORKLOADS[args.workload]
     steps = args.steps if args.steps is not None else 200

@@ -1777,10 +1777,10 @@ int q38_model_speculative_greedy(Q38Model *m, uint32_t token, uint32_t stop_toke
                       q38::launch_argmax(m->logits, kVocab, 1, m->argmax_pv, m->argmax_pi, m->drafts + i + 1,
                                          m->stream);
                   }
-                  if (!target_rows(m, sv, k, k)) return false;
-                  q38::launch_argmax(m->logits, kVocab, k, m->argmax_pv, m->argmax_pi, m->targets, m->stream);
-                  q38::launch_accept(m->accept, m->targets, m->drafts + 1, k, m->stream, stop);
-                  q38::launch_copy_row(m->logits_stage, m->logits, kVocab, kVocab, m->accept, k, m->stream);
+                  if (!target_rows(m, sv, k, k) ||
+                      !q38::launch_verify_tail(m->logits, kVocab, k, m->argmax_pv, m->argmax_pi, m->targets,
+                                               m->drafts + 1, stop, m->accept, m->logits_stage, m->stream))
+                      return false;
                   return mtp_catchup(m, sc, k, m->ck_mtp_hidden, m->accept);
               }) &&
          /* then the acceptance words and the logits row: host words [64..)
@@ -1846,10 +1846,8 @@ int q38hip_model_time_block(Q38Model *m, uint32_t layer, uint32_t rows, uint32_t
         return ok;
     };
     auto tail = [&] {
-        q38::launch_argmax(m->logits, kVocab, rows, m->argmax_pv, m->argmax_pi, m->targets, m->stream);
-        q38::launch_accept(m->accept, m->targets, m->drafts + 1, rows, m->stream, stop);
-        q38::launch_copy_row(m->logits_stage, m->logits, kVocab, kVocab, m->accept, rows, m->stream);
-        return true;
+        return q38::launch_verify_tail(m->logits, kVocab, rows, m->argmax_pv, m->argmax_pi, m->targets, m->drafts + 1,
+                                       stop, m->accept, m->logits_stage, m->stream);
     };
     hipEvent_t e0 = nullptr, e1 = nullptr;
     bool ok = hip_ok(hipEventCreate(&e0), "event") && hip_ok(hipEventCreate(&e1), "event");

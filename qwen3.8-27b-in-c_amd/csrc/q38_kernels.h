@@ -97,6 +97,14 @@ void launch_accept(uint32_t *result, const uint32_t *targets, const uint32_t *dr
  * floats apart (index clamped to 1 .. rows) */
 void launch_copy_row(float *dst, const float *src, size_t stride, uint32_t count, const uint32_t *index,
                      uint32_t rows, hipStream_t stream);
+/* The verify tail of a speculative transaction (rows <= 8): the argmax of
+ * each of `rows` rows of `count` values into targets, the greedy acceptance
+ * of the drafts into result (3 + rows words, as launch_accept) and the copy
+ * of row consumed - 1 into dst; two launches.  count must be a multiple of
+ * 4; false for unsupported shapes. */
+bool launch_verify_tail(const float *values, uint32_t count, uint32_t rows, float *pv, uint32_t *pi,
+                        uint32_t *targets, const uint32_t *drafts, const uint32_t *stop, uint32_t *result, float *dst,
+                        hipStream_t stream);
 
 /* q38_sample.hip: q38_sample (qwen38_sampler.c:51-119) on a device logits
  * row; *token_out is a device word written on `stream`.  *state is the

@@ -184,4 +184,94 @@ void launch_copy_row(float *dst, const float *src, size_t stride, uint32_t count
                        count, index, rows);
 }
 
+/* The verify tail after argmax_partial_kernel, in one launch: the argmax of
+ * every row from its partials (argmax_final_kernel's selection, one
+ * wavefront per row), the greedy acceptance of accept_kernel, and the copy
+ * of row consumed - 1 (copy_row_kernel).  Every workgroup reduces the
+ * partials of every row (rows x nchunks pairs, a few KB from L2) and runs
+ * the acceptance itself, so no workgroup waits for another; workgroup 0
+ * writes the targets and the acceptance words, and each workgroup copies
+ * its share of the row. */
+constexpr uint32_t kTailMaxRows = 8;
+
+__global__ __launch_bounds__(256) void verify_tail_kernel(const float *__restrict__ values, uint32_t count,
+                                                          const float *__restrict__ pv, const uint32_t *__restrict__ pi,
+                                                          uint32_t nchunks, uint32_t rows,
+                                                          uint32_t *__restrict__ targets,
+                                                          const uint32_t *__restrict__ drafts,
+                                                          const uint32_t *__restrict__ stop,
+                                                          uint32_t *__restrict__ result, float *__restrict__ dst)
+{
+    __shared__ uint32_t tgt[kTailMaxRows];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (uint32_t r = wave; r < rows; r += 4) {
+        float bv = __builtin_nanf("");
+        uint32_t bi = 0xffffffffu;
+        for (uint32_t c = lane; c < nchunks; c += 64) {
+            const float x = pv[(size_t)r * nchunks + c];
+            const uint32_t i = pi[(size_t)r * nchunks + c];
+            if (better(x, i, bv, bi)) { bv = x; bi = i; }
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, 64);
+            const uint32_t oi = __shfl_xor(bi, off, 64);
+            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+        }
+        if (lane == 0) {
+            const float first = values[(size_t)r * count];
+            tgt[r] = (first != first || bi == 0xffffffffu) ? 0u : bi;
+        }
+    }
+    __syncthreads();
+    /* acceptance (src/qwen38/qwen38_model.c:1640-1702), as accept_kernel */
+    uint32_t n = rows;
+    if (stop) {
+        const uint32_t st = *stop;
+        for (uint32_t i = 0; i < rows; ++i)
+            if (drafts[i] == st) {
+                n = i + 1;
+                break;
+            }
+    }
+    uint32_t matched = 0, next = 0;
+    while (matched < n) {
+        if (tgt[matched] != drafts[matched]) { next = tgt[matched]; break; }
+        ++matched;
+    }
+    if (matched == n) next = drafts[n - 1];
+    const uint32_t consumed = matched < n ? matched + 1u : n;
+    if (blockIdx.x == 0) {
+        if (threadIdx.x < rows) targets[threadIdx.x] = tgt[threadIdx.x];
+        if (threadIdx.x == 0) {
+            result[0] = consumed;
+            result[1] = matched;
+            result[2] = next;
+        }
+        if (threadIdx.x < matched) result[3 + threadIdx.x] = drafts[threadIdx.x];
+        if (threadIdx.x == 0 && matched < n) result[3 + matched] = next;
+    }
+    const float *row = values + (size_t)(consumed - 1u) * count;
+    for (uint32_t i = (blockIdx.x * 256u + threadIdx.x) * 4u; i < count; i += gridDim.x * 1024u) {
+        if (i + 4u <= count) {
+            *reinterpret_cast<float4 *>(dst + i) = *reinterpret_cast<const float4 *>(row + i);
+        } else {
+            for (uint32_t k = i; k < count; ++k) dst[k] = row[k];
+        }
+    }
+}
+
+bool launch_verify_tail(const float *values, uint32_t count, uint32_t rows, float *pv, uint32_t *pi,
+                        uint32_t *targets, const uint32_t *drafts, const uint32_t *stop, uint32_t *result, float *dst,
+                        hipStream_t stream)
+{
+    if (rows == 0 || rows > kTailMaxRows || (count & 3u) != 0) return false;
+    const uint32_t chunks = argmax_chunks(count);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(chunks, rows), dim3(kArgmaxThreads), 0, stream, values, count, pv,
+                       pi);
+    const uint32_t blocks = (count + 1023u) / 1024u;
+    hipLaunchKernelGGL(verify_tail_kernel, dim3(blocks < 64u ? blocks : 64u), dim3(256), 0, stream, values, count, pv,
+                       pi, chunks, rows, targets, drafts, stop, result, dst);
+    return true;
+}
+
 }  // namespace q38

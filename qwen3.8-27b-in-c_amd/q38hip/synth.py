@@ -85,8 +85,8 @@ def activations(width, seed, count=1):
 
 
 SYNTH_GGUF = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "synth", "q38_synth_gguf")
-MODEL_GGUF_BYTES = {"q4km": 15704910464, "iq1m": 7188425344, "accept": 15465926368, "accept_mtp": 1997090400,
-                    "accept_all": 15704910464, "mixed": 13753227904}
+MODEL_GGUF_BYTES = {"q4km": 15709517280, "iq1m": 7193032160, "accept": 15470533184, "accept_mtp": 2001697184,
+                    "accept_all": 15709517280, "mixed": 13757834720}
 
 
 def write_model_gguf(path, seed, variant="q4km"):

@@ -48,6 +48,7 @@
  * mins are set to centre their sub-blocks as for Q4_K.
  *
  * Usage: q38_synth_gguf OUT.gguf SEED q4km|iq1m|accept|accept_mtp|accept_all|mixed
+ *        (OUT.gguf "-": print the file size only)
  */
 #define _GNU_SOURCE
 #include <fcntl.h>
@@ -414,6 +415,81 @@ static void put_u32(Buf *b, uint32_t v) { put(b, &v, 4); }
 static void put_u64(Buf *b, uint64_t v) { put(b, &v, 8); }
 static void put_str(Buf *b, const char *s) { put_u64(b, strlen(s)); put(b, s, strlen(s)); }
 static void meta_u32(Buf *b, const char *key, uint32_t v) { put_str(b, key); put_u32(b, 4); put_u32(b, v); }
+static void meta_str(Buf *b, const char *key, const char *v) { put_str(b, key); put_u32(b, 8); put_str(b, v); }
+
+/* ---- tokenizer metadata ----------------------------------------------------- *
+ * A byte-level BPE vocabulary of VOCAB entries that the reference's tokenizer
+ * (src/qwen38/qwen38_tokenizer.c:171-205) loads, so the reference CLI and
+ * server can run on the synthetic model: ids 0..255 are the 256 byte symbols
+ * of the GPT-2 byte map (every byte string encodes), ids 256..260 the results
+ * of the five merges below, the chat-template tokens at SPECIAL0.. (control
+ * tokens, type 3, and the think tags, type 4), every other id "w<id>".  The
+ * end-of-sequence token is <|im_end|>. */
+enum { SPECIAL0 = 248310, EOS_ID = SPECIAL0 + 2 };
+static const char *const kMerges[5][2] = {{"h", "e"}, {"l", "l"}, {"\xc4\xa0", "t"}, {"t", "h"}, {"i", "n"}};
+static const char *const kSpecials[5] = {"<|endoftext|>", "<|im_start|>", "<|im_end|>", "<think>", "</think>"};
+
+/* UTF-8 of the byte map's code point for byte b (33..126, 161..172 and
+ * 174..255 map to themselves, the rest to 256, 257, ... in byte order) */
+static int byte_symbol(int b, char *out)
+{
+    int cp = b, extra = 0;
+    const int direct = (b >= 33 && b <= 126) || (b >= 161 && b <= 172) || (b >= 174 && b <= 255);
+    if (!direct) {
+        for (int c = 0; c < b; ++c)
+            if (!((c >= 33 && c <= 126) || (c >= 161 && c <= 172) || (c >= 174 && c <= 255))) ++extra;
+        cp = 256 + extra;
+    }
+    if (cp < 0x80) {
+        out[0] = (char)cp;
+        out[1] = 0;
+        return 1;
+    }
+    out[0] = (char)(0xc0 | (cp >> 6));
+    out[1] = (char)(0x80 | (cp & 0x3f));
+    out[2] = 0;
+    return 2;
+}
+
+static void put_tokenizer(Buf *h)
+{
+    char text[32];
+    meta_str(h, "tokenizer.ggml.model", "gpt2");
+    meta_str(h, "tokenizer.ggml.pre", "qwen2");
+    put_str(h, "tokenizer.ggml.tokens");
+    put_u32(h, 9);
+    put_u32(h, 8);
+    put_u64(h, VOCAB);
+    for (int id = 0; id < VOCAB; ++id) {
+        if (id < 256) {
+            byte_symbol(id, text);
+        } else if (id < 261) {
+            snprintf(text, sizeof(text), "%s%s", kMerges[id - 256][0], kMerges[id - 256][1]);
+        } else if (id >= SPECIAL0 && id < SPECIAL0 + 5) {
+            snprintf(text, sizeof(text), "%s", kSpecials[id - SPECIAL0]);
+        } else {
+            snprintf(text, sizeof(text), "w%d", id);
+        }
+        put_str(h, text);
+    }
+    put_str(h, "tokenizer.ggml.token_type");
+    put_u32(h, 9);
+    put_u32(h, 5);
+    put_u64(h, VOCAB);
+    for (int id = 0; id < VOCAB; ++id) {
+        const int32_t type = id >= SPECIAL0 && id < SPECIAL0 + 3 ? 3 : id >= SPECIAL0 + 3 && id < SPECIAL0 + 5 ? 4 : 1;
+        put(h, &type, 4);
+    }
+    put_str(h, "tokenizer.ggml.merges");
+    put_u32(h, 9);
+    put_u32(h, 8);
+    put_u64(h, 5);
+    for (int i = 0; i < 5; ++i) {
+        snprintf(text, sizeof(text), "%s %s", kMerges[i][0], kMerges[i][1]);
+        put_str(h, text);
+    }
+    meta_u32(h, "tokenizer.ggml.eos_token_id", EOS_ID);
+}
 
 int main(int argc, char **argv)
 {
@@ -462,7 +538,7 @@ int main(int argc, char **argv)
     put_u32(&h, 0x46554747u);
     put_u32(&h, 3);
     put_u64(&h, (uint64_t)tensor_count);
-    put_u64(&h, 14);
+    put_u64(&h, 14 + 6);
     put_str(&h, "general.architecture"); put_u32(&h, 8); put_str(&h, "qwen35");
     meta_u32(&h, "general.alignment", 32);
     meta_u32(&h, "qwen35.block_count", block_count);
@@ -477,6 +553,7 @@ int main(int argc, char **argv)
     meta_u32(&h, "qwen35.ssm.time_step_rank", 48);
     meta_u32(&h, "qwen35.ssm.inner_size", 6144);
     meta_u32(&h, "general.file_type", m == Q4_K ? 15u : 31u);
+    put_tokenizer(&h);
     for (int i = 0; i < tensor_count; ++i) {
         const Tensor *t = &tensors[i];
         put_str(&h, t->name);
@@ -487,6 +564,11 @@ int main(int argc, char **argv)
     }
     const uint64_t data_start = (h.n + 31) & ~31ull;
     while (h.n < data_start) put(&h, "", 1);
+    if (strcmp(argv[1], "-") == 0) {
+        /* size only: the file this seed and variant would produce */
+        printf("%llu\n", (unsigned long long)(data_start + data_bytes));
+        return 0;
+    }
 
     const int fd = open(argv[1], O_CREAT | O_TRUNC | O_WRONLY, 0644);
     if (fd < 0) { perror(argv[1]); return 1; }
