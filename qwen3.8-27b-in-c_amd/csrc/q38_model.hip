@@ -182,14 +182,26 @@ __global__ __launch_bounds__(128) void deltanet_prep_kernel(float *__restrict__ 
  * accumulator of vector a, element j; result = ((H0+H1)+(H2+H3)) with
  * H[j] = Q[j] + Q[j+4], Q[j] = (P0[j]+P2[j]) + (P1[j]+P3[j]).
  * Operates on 32-lane halves of the wavefront; every lane gets the result. */
+/* lane l of each 16-lane row gets lane l + N of the row (DPP row_shl:N) */
+template <int N>
+__device__ __forceinline__ float dpp_shl(float v)
+{
+    return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x100 + N, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float avx2_tree32(float v)
 {
-    v = __fadd_rn(v, __shfl_down(v, 16, 32));   /* l<16: P0+P2 (l<8), P1+P3 (8..15) */
-    v = __fadd_rn(v, __shfl_down(v, 8, 32));    /* l<8:  Q[l] */
-    v = __fadd_rn(v, __shfl_down(v, 4, 32));    /* l<4:  H[l] */
-    v = __fadd_rn(v, __shfl_down(v, 1, 32));    /* l=0: H0+H1, l=2: H2+H3 */
-    v = __fadd_rn(v, __shfl_down(v, 2, 32));    /* l=0: (H0+H1)+(H2+H3) */
-    return __shfl(v, 0, 32);
+    /* lane l < 16 of each half gets lane l + 16 (v_permlane16_swap: the odd
+     * 16-lane rows of the first operand trade places with the even rows of
+     * the second) */
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __fadd_rn(v, __uint_as_float(sw[1]));   /* l<16: P0+P2 (l<8), P1+P3 (8..15) */
+    v = __fadd_rn(v, dpp_shl<8>(v));            /* l<8:  Q[l] */
+    v = __fadd_rn(v, dpp_shl<4>(v));            /* l<4:  H[l] */
+    v = __fadd_rn(v, dpp_shl<1>(v));            /* l=0: H0+H1, l=2: H2+H3 */
+    v = __fadd_rn(v, dpp_shl<2>(v));            /* l=0: (H0+H1)+(H2+H3) */
+    const float lo = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+    const float hi = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32));
+    return (threadIdx.x & 32) ? hi : lo;
 }
 
 /* State update of one value head (qwen38_model.c:759-783): S *= decay; per
@@ -197,12 +209,18 @@ __device__ __forceinline__ float avx2_tree32(float v)
  * S_c = fma(k, delta, S_c); out[c] = dot(S_c, q) * (1/sqrt(128)).
  * Columns are independent: 32 lanes per column (lane l owns elements
  * l, l+32, l+64, l+96, the reference's fixed 4 x 8-lane accumulators), two
- * columns per wavefront, eight per block of 256.  The column runs through
- * `rows` consecutive tokens (row t's prepared q|k|v at qkv + t * ld, beta
- * and alpha at + beta_off / alpha_off, output at out + t * kLinV): the
- * state before row t is slot (*slot_ptr + t), read once, kept in registers,
- * and each row's result is written to the next slot (with `last_only`, only
- * the last row's, to slot *slot_ptr + rows). */
+ * columns per wavefront, eight per block of 256, all of one value head h.
+ * The column runs through `rows` consecutive tokens (row t's prepared
+ * q|k|v at qkv + t * ld, beta and alpha at + beta_off / alpha_off, output
+ * at out + t * kLinV): the state before row t is slot (*slot_ptr + t), read
+ * once, kept in registers, and each row's result is written to the next
+ * slot (with `last_only`, only the last row's, to slot *slot_ptr + rows).
+ * The block's inputs (k and q of head h % 16, the block's eight v values,
+ * alpha and beta of head h) come through LDS in chunks of kScanChunk rows,
+ * the next chunk's global loads in flight while the current one is
+ * scanned, so the sequential scan reads only LDS. */
+constexpr int kScanChunk = 16;
+
 __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__ out, float *__restrict__ state,
                                                              long long slot_stride,
                                                              const uint32_t *__restrict__ slot_ptr, int rows,
@@ -210,57 +228,82 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
                                                              int beta_off, int alpha_off, float query_scale,
                                                              int last_only)
 {
-    const int column_global = blockIdx.x * 8 + (threadIdx.x >> 5);   /* 0 .. 48*128-1 */
+    __shared__ float kq_s[2][kScanChunk][2 * kHeadDim];   /* [parity][row][k 0..127 | q 0..127] */
+    __shared__ float v_s[2][kScanChunk][8];
+    __shared__ float ab_s[2][kScanChunk][2];               /* alpha, beta */
+    const int tid = threadIdx.x;
+    const int column_global = blockIdx.x * 8 + (tid >> 5);   /* 0 .. 48*128-1 */
     const int h = column_global >> 7;
     const int c = column_global & 127;
-    const int l = threadIdx.x & 31;
+    const int l = tid & 31;
     const int kh = h % 16;
+    const int c0 = (blockIdx.x * 8) & 127;
     const uint32_t slot0 = *slot_ptr;
     const size_t col_off = ((size_t)h * kHeadDim + c) * kHeadDim;
     const float *s = state + (size_t)(slot0 % kStateSlots) * slot_stride + col_off;
     float sv[4];
     for (int a = 0; a < 4; ++a) sv[a] = s[32 * a + l];
-    /* row t's inputs are loaded while row t - 1 computes */
-    struct RowIn {
-        float k[4], q[4], v, alpha, beta;
+
+    /* thread tid stages element tid of the k|q vector of every row of a
+     * chunk; threads 0..8R-1 a v value, 8R..8R+2R-1 an alpha or beta */
+    const int kq_src = tid < kHeadDim ? kQKDim + kh * kHeadDim + tid : kh * kHeadDim + (tid - kHeadDim);
+    float kq_r[kScanChunk], x_r = 0.0f;
+    const int nchunks = (rows + kScanChunk - 1) / kScanChunk;
+    auto fetch = [&](int ch) {
+        const int r0 = ch * kScanChunk;
+#pragma unroll
+        for (int i = 0; i < kScanChunk; ++i) {
+            const int t = r0 + i < rows ? r0 + i : rows - 1;
+            kq_r[i] = qkv[(long long)t * ld + kq_src];
+        }
+        if (tid < 10 * kScanChunk) {
+            const int i = tid < 8 * kScanChunk ? tid >> 3 : (tid - 8 * kScanChunk) >> 1;
+            const int t = r0 + i < rows ? r0 + i : rows - 1;
+            const float *row = qkv + (long long)t * ld;
+            x_r = tid < 8 * kScanChunk ? row[2 * kQKDim + h * kHeadDim + c0 + (tid & 7)]
+                                       : row[(tid & 1) ? beta_off + h : alpha_off + h];
+        }
     };
-    auto load_row = [&](int t) {
-        const float *row = qkv + (long long)t * ld;
-        RowIn in;
-        for (int a = 0; a < 4; ++a) {
-            in.k[a] = row[kQKDim + kh * kHeadDim + 32 * a + l];
-            in.q[a] = row[kh * kHeadDim + 32 * a + l];
-        }
-        in.v = row[2 * kQKDim + h * kHeadDim + c];
-        in.alpha = row[alpha_off + h];
-        in.beta = row[beta_off + h];
-        return in;
+    auto stage = [&](int par) {
+#pragma unroll
+        for (int i = 0; i < kScanChunk; ++i) kq_s[par][i][tid] = kq_r[i];
+        if (tid < 8 * kScanChunk) v_s[par][tid >> 3][tid & 7] = x_r;
+        else if (tid < 10 * kScanChunk) ab_s[par][(tid - 8 * kScanChunk) >> 1][tid & 1] = x_r;
     };
-    RowIn cur = load_row(0);
-    for (int t = 0; t < rows; ++t) {
-        const RowIn nxt = load_row(t + 1 < rows ? t + 1 : t);
-        const float decay = q38_expf(cur.alpha);
-        float kv[4], qv[4];
-        for (int a = 0; a < 4; ++a) {
-            sv[a] = __fmul_rn(sv[a], decay);
-            kv[a] = cur.k[a];
-            qv[a] = cur.q[a];
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int ch = 0; ch < nchunks; ++ch) {
+        const int par = ch & 1;
+        if (ch + 1 < nchunks) fetch(ch + 1);
+        const int r0 = ch * kScanChunk;
+        const int n = rows - r0 < kScanChunk ? rows - r0 : kScanChunk;
+        for (int i = 0; i < n; ++i) {
+            const int t = r0 + i;
+            const float decay = q38_expf(ab_s[par][i][0]);
+            float kv[4], qv[4];
+            for (int a = 0; a < 4; ++a) {
+                sv[a] = __fmul_rn(sv[a], decay);
+                kv[a] = kq_s[par][i][32 * a + l];
+                qv[a] = kq_s[par][i][kHeadDim + 32 * a + l];
+            }
+            float p = 0.0f;
+            for (int a = 0; a < 4; ++a) p = __builtin_fmaf(sv[a], kv[a], p);
+            const float pred = avx2_tree32(p);
+            const float delta = __fmul_rn(__fsub_rn(v_s[par][i][(tid >> 5) & 7], pred), ab_s[par][i][1]);
+            float *s_out = state + (size_t)((slot0 + t + 1) % kStateSlots) * slot_stride + col_off;
+            const bool store = !last_only || t == rows - 1;
+            float r = 0.0f;
+            for (int a = 0; a < 4; ++a) {
+                sv[a] = __builtin_fmaf(kv[a], delta, sv[a]);
+                if (store) s_out[32 * a + l] = sv[a];
+                r = __builtin_fmaf(sv[a], qv[a], r);
+            }
+            const float result = avx2_tree32(r);
+            if (l == 0) out[(size_t)t * kLinV + h * kHeadDim + c] = __fmul_rn(result, query_scale);
         }
-        float p = 0.0f;
-        for (int a = 0; a < 4; ++a) p = __builtin_fmaf(sv[a], kv[a], p);
-        const float pred = avx2_tree32(p);
-        const float delta = __fmul_rn(__fsub_rn(cur.v, pred), cur.beta);
-        float *s_out = state + (size_t)((slot0 + t + 1) % kStateSlots) * slot_stride + col_off;
-        const bool store = !last_only || t == rows - 1;
-        float r = 0.0f;
-        for (int a = 0; a < 4; ++a) {
-            sv[a] = __builtin_fmaf(kv[a], delta, sv[a]);
-            if (store) s_out[32 * a + l] = sv[a];
-            r = __builtin_fmaf(sv[a], qv[a], r);
-        }
-        const float result = avx2_tree32(r);
-        if (l == 0) out[(size_t)t * kLinV + h * kHeadDim + c] = __fmul_rn(result, query_scale);
-        cur = nxt;
+        if (ch + 1 < nchunks) stage(par ^ 1);
+        __syncthreads();
     }
 }
 
