@@ -283,10 +283,12 @@ bool launch_iq1m_nb(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_
  * (row, token) in registers.  A workgroup of 8 wavefronts covers 256 rows x
  * 64 tokens: wavefront w takes rows 32w .. 32w + 31 (two 16-row tiles)
  * against all 64 tokens (four token tiles), so each decoded weight operand
- * serves four token tiles and each activation operand two row tiles; the
- * workgroup's wavefronts read the same activations, which L1 serves after
- * the first.  Lane (r, q) of tile pair (rt, tt) owns tokens 16 tt + 4 q + j
- * of row 16 rt + r. */
+ * serves four token tiles and each activation operand two row tiles.  Lane
+ * (r, q) of tile pair (rt, tt) owns tokens 16 tt + 4 q + j of row 16 rt + r.
+ * The workgroup stages each block's activation quants of its 64 tokens in
+ * LDS once (one block ahead), and every wavefront reads its A operands from
+ * there, so the address unit handles only the weight loads and one 32-byte
+ * staging copy per thread and block. */
 constexpr int kIQWideRows = 256, kIQWideTokens = 64, kIQWideWaves = 8;
 
 template <int NB>
@@ -298,6 +300,11 @@ __global__ __launch_bounds__(64 * kIQWideWaves, 1) void gemm_iq1m_wide(const uin
 {
     __shared__ uint2 grid_s[2048];
     __shared__ float xs_s[NB * kIQWideTokens];   /* [block][token] */
+    /* the activation quants of one block for the 64 tokens, double-buffered:
+     * [parity][token][kActStride bytes] (256 quants + 16 bytes of padding, so
+     * the 16 tokens one A-operand read touches fall on distinct banks) */
+    constexpr int kActStride = 272;
+    __shared__ __attribute__((aligned(16))) uint8_t act_s[2][kIQWideTokens * kActStride];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int r = lane & 15, q = lane >> 4;
@@ -319,13 +326,33 @@ __global__ __launch_bounds__(64 * kIQWideWaves, 1) void gemm_iq1m_wide(const uin
     }
     __syncthreads();
 
-    /* weight rows of the lane (rows past the matrix read as zero) and the
-     * activation offsets of its token in each token tile */
-    uint32_t woff[2], xoff[4];
+    /* weight rows of the lane (rows past the matrix read as zero) */
+    uint32_t woff[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) woff[rt] = (row0 + 16 * rt + (uint32_t)r) * NB * kIQ1MBytes;
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) xoff[tt] = (uint32_t)((16 * tt + r) * NB * kQ8KBytes + 4 + 64 * q);
+    /* staging of a block's activations: thread i copies bytes 32 (i % 8) ..
+     * + 31 of token i / 8's quants (tokens past the batch read as zero) */
+    static_assert(64 * kIQWideWaves == 8 * kIQWideTokens, "one staging thread per 32 bytes");
+    const uint32_t st_tok = threadIdx.x >> 3, st_part = threadIdx.x & 7;
+    auto fetch_act = [&](int b, int4v (&v)[2]) {
+        const uint32_t off = (st_tok * NB + (uint32_t)b) * kQ8KBytes + 4 + 32 * st_part;
+        v[0] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+        v[1] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0);
+    };
+    auto store_act = [&](int par, const int4v (&v)[2]) {
+        int4v *d = reinterpret_cast<int4v *>(&act_s[par][st_tok * kActStride + 32 * st_part]);
+        d[0] = v[0];
+        d[1] = v[1];
+    };
+    /* the lane's A operand of token tile tt, chunk cc: 16 quants of token
+     * 16 tt + r at 64 q + 16 cc */
+    auto act = [&](int par, int tt, int cc) {
+        return *reinterpret_cast<const int4v *>(&act_s[par][(16 * tt + r) * kActStride + 64 * q + 16 * cc]);
+    };
+    int4v stage_v[2];
+    fetch_act(0, stage_v);
+    store_act(0, stage_v);
+    __syncthreads();
 
     struct WLoad {
         uint32_t qs[2], qh, sc[2];
@@ -353,16 +380,13 @@ __global__ __launch_bounds__(64 * kIQWideWaves, 1) void gemm_iq1m_wide(const uin
             for (int j = 0; j < 4; ++j) total[rt][tt][j] = 0.0f;
 
     WLoad wc[2] = {load_w(0, 0), load_w(1, 0)};
-    int4v ac[4][4];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) ac[tt][cc] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[tt] + 16 * cc, 0, 0);
 
 #pragma unroll 1
     for (int b = 0; b < NB; ++b) {
         const int bn = b + 1 < NB ? b + 1 : b;   /* the next block's loads (the last re-reads, unused) */
+        const int par = b & 1;
         const WLoad wn[2] = {load_w(0, bn), load_w(1, bn)};
+        if (b + 1 < NB) fetch_act(b + 1, stage_v);
         int4v d1[2][4], d2[2][4];
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
@@ -395,19 +419,16 @@ __global__ __launch_bounds__(64 * kIQWideWaves, 1) void gemm_iq1m_wide(const uin
                 bs[rt][3] = (int)c1;
             }
 #pragma unroll
-            for (int tt = 0; tt < 4; ++tt)
+            for (int tt = 0; tt < 4; ++tt) {
+                const int4v a = act(par, tt, cc);
 #pragma unroll
                 for (int rt = 0; rt < 2; ++rt) {
-                    d1[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ac[tt][cc], bw[rt], d1[rt][tt], 0, 0, 0);
-                    d2[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ac[tt][cc], bs[rt], d2[rt][tt], 0, 0, 0);
+                    d1[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw[rt], d1[rt][tt], 0, 0, 0);
+                    d2[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bs[rt], d2[rt][tt], 0, 0, 0);
                 }
+            }
         }
-        /* the next block's activations, then the chains of this block */
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc)
-                ac[tt][cc] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[tt] + 16 * cc, bn * kQ8KBytes, 0);
+        /* the chains of this block */
         float dsc[2];
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
@@ -431,6 +452,9 @@ __global__ __launch_bounds__(64 * kIQWideWaves, 1) void gemm_iq1m_wide(const uin
             }
         wc[0] = wn[0];
         wc[1] = wn[1];
+        /* the next block's activations into the other buffer */
+        if (b + 1 < NB) store_act(par ^ 1, stage_v);
+        __syncthreads();
     }
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
