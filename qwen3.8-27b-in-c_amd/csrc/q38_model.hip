@@ -887,9 +887,9 @@ __device__ __forceinline__ int mix_quad(int d, int u)
 
 /* 5 LDS reads: four quads of the lane's channel and one probability per
  * lane (each 16-lane row holds the half's 16 probabilities) */
-__device__ __forceinline__ void mix_read(MixHalf &r, const uint8_t *slot, int half, int lane)
+__device__ __forceinline__ void mix_read(MixHalf &r, const uint8_t *slot, int half, int lane, int pair = 0)
 {
-    const float *ps = reinterpret_cast<const float *>(slot + kMixChunk * 256) + half * kMixHalf;
+    const float *ps = reinterpret_cast<const float *>(slot + kMixChunk * 256) + pair * kMixChunk + half * kMixHalf;
     r.pr = ps[lane & 15];
 #pragma unroll
     for (int k = 0; k < kMixHalf / 4; ++k) {
@@ -938,18 +938,61 @@ __device__ __forceinline__ float mix_links(const MixHalf &r, float o)
  * wait only for that half's 12 reads, the other half's stay in flight.
  * After the last chunk the reads take a stale slot and are never used. */
 __device__ __forceinline__ float mix_step(float o, const MixHalf &a0, const MixHalf &a1, MixHalf &b0, MixHalf &b1,
-                                          const uint8_t *next_slot, int lane)
+                                          const uint8_t *next_slot, int lane, int pair = 0)
 {
     mix_barrier();
     __builtin_amdgcn_sched_barrier(0);
     o = mix_links(a0, o);
     __builtin_amdgcn_sched_barrier(0);
-    mix_read(b0, next_slot, 0, lane);
+    mix_read(b0, next_slot, 0, lane, pair);
     __builtin_amdgcn_sched_barrier(0);
     o = mix_links(a1, o);
     __builtin_amdgcn_sched_barrier(0);
-    mix_read(b1, next_slot, 1, lane);
+    mix_read(b1, next_slot, 1, lane, pair);
     __builtin_amdgcn_sched_barrier(0);
+    return o;
+}
+
+/* The chain wavefront's part of the mix: the links of positions 0 .. n - 1
+ * of its channel from the ring (chunk c in slot c % kMixSlots, probability
+ * record `pair` of each slot), one barrier per chunk as the streaming
+ * wavefront's (the chain of attn_mix_kernel). */
+__device__ __forceinline__ float mix_chain(const uint8_t *ring, int slot_bytes, int n, int lane, int pair)
+{
+    const int full = n / kMixChunk, rest = n % kMixChunk;
+    MixHalf a0, a1, b0, b1;
+    mix_barrier();
+    mix_read(a0, ring, 0, lane, pair);
+    mix_read(a1, ring, 1, lane, pair);
+    float o = 0.0f;
+    int c = 0;
+    static_assert(kMixSlots == 8, "the unrolled loop takes one ring turn per iteration");
+#pragma unroll 1
+    for (; c + kMixSlots <= full; c += kMixSlots) {
+        o = mix_step(o, a0, a1, b0, b1, ring + 1 * slot_bytes, lane, pair);
+        o = mix_step(o, b0, b1, a0, a1, ring + 2 * slot_bytes, lane, pair);
+        o = mix_step(o, a0, a1, b0, b1, ring + 3 * slot_bytes, lane, pair);
+        o = mix_step(o, b0, b1, a0, a1, ring + 4 * slot_bytes, lane, pair);
+        o = mix_step(o, a0, a1, b0, b1, ring + 5 * slot_bytes, lane, pair);
+        o = mix_step(o, b0, b1, a0, a1, ring + 6 * slot_bytes, lane, pair);
+        o = mix_step(o, a0, a1, b0, b1, ring + 7 * slot_bytes, lane, pair);
+        o = mix_step(o, b0, b1, a0, a1, ring, lane, pair);
+    }
+#pragma unroll 1
+    for (; c + 2 <= full; c += 2) {
+        o = mix_step(o, a0, a1, b0, b1, ring + ((c + 1) % kMixSlots) * slot_bytes, lane, pair);
+        o = mix_step(o, b0, b1, a0, a1, ring + ((c + 2) % kMixSlots) * slot_bytes, lane, pair);
+    }
+    if (c < full) o = mix_step(o, a0, a1, b0, b1, ring + ((c + 1) % kMixSlots) * slot_bytes, lane, pair);
+    if (rest) {
+        /* the partial last chunk (landed at the previous barrier), link by
+         * link up to position n - 1 */
+        mix_barrier();
+        const uint8_t *slot = ring + (full % kMixSlots) * slot_bytes;
+        const float *ps = reinterpret_cast<const float *>(slot + kMixChunk * 256) + pair * kMixChunk;
+        for (int k = 0; k < rest; ++k)
+            o = __builtin_fmaf(ps[k], *reinterpret_cast<const float *>(slot + mix_quad(lane, k >> 2) + 4 * (k & 3)), o);
+    }
     return o;
 }
 
@@ -997,41 +1040,106 @@ __global__ __launch_bounds__(128) void attn_mix_kernel(float *__restrict__ out, 
         return;
     }
     /* chain wavefront: one barrier per chunk, as the streaming wavefront */
-    const int full = n / kMixChunk, rest = n % kMixChunk;
-    MixHalf a0, a1, b0, b1;
-    mix_barrier();
-    mix_read(a0, ring, 0, lane);
-    mix_read(a1, ring, 1, lane);
-    float o = 0.0f;
-    int c = 0;
-    static_assert(kMixSlots == 8, "the unrolled loop takes one ring turn per iteration");
-    /* whole ring turns: chunk c + k sits in slot k, a constant LDS offset */
-#pragma unroll 1
-    for (; c + kMixSlots <= full; c += kMixSlots) {
-        o = mix_step(o, a0, a1, b0, b1, ring + 1 * kMixSlotBytes, lane);
-        o = mix_step(o, b0, b1, a0, a1, ring + 2 * kMixSlotBytes, lane);
-        o = mix_step(o, a0, a1, b0, b1, ring + 3 * kMixSlotBytes, lane);
-        o = mix_step(o, b0, b1, a0, a1, ring + 4 * kMixSlotBytes, lane);
-        o = mix_step(o, a0, a1, b0, b1, ring + 5 * kMixSlotBytes, lane);
-        o = mix_step(o, b0, b1, a0, a1, ring + 6 * kMixSlotBytes, lane);
-        o = mix_step(o, a0, a1, b0, b1, ring + 7 * kMixSlotBytes, lane);
-        o = mix_step(o, b0, b1, a0, a1, ring, lane);
-    }
-#pragma unroll 1
-    for (; c + 2 <= full; c += 2) {
-        o = mix_step(o, a0, a1, b0, b1, ring + ((c + 1) % kMixSlots) * kMixSlotBytes, lane);
-        o = mix_step(o, b0, b1, a0, a1, ring + ((c + 2) % kMixSlots) * kMixSlotBytes, lane);
-    }
-    if (c < full) o = mix_step(o, a0, a1, b0, b1, ring + ((c + 1) % kMixSlots) * kMixSlotBytes, lane);
-    if (rest) {
-        /* the partial last chunk (landed at the previous barrier), link by
-         * link up to position n - 1 */
+    const float o = mix_chain(ring, kMixSlotBytes, n, lane, 0);
+    const int dim = h * kAttnDim + 64 * slice + lane;
+    const float g = q_and_gate[(size_t)t * qg_stride + h * 2 * kAttnDim + kAttnDim + 64 * slice + lane];
+    out[(size_t)t * kQDim + dim] = __fmul_rn(o, sigmoidf_exact(g));
+}
+
+/* attn_mix_kernel for prompt batches: one workgroup per (KV head, 64-channel
+ * slice, group of kMixRows rows) streams the slice's value rows once for the
+ * 6 q heads of the KV head and the group's rows: wavefront w < 6 kMixRows
+ * runs the chains of (row w / 6, q head w % 6), each exactly as the chain
+ * wavefront of attn_mix_kernel over its own positions 0 .. n_row - 1, and
+ * the last wavefront streams the value chunks up to the group's last row
+ * and every pair's probabilities into the ring (a slot holds the chunk's
+ * values, then the pairs' probability records of kMixChunk floats).  A
+ * chain wavefront whose row has fewer chunks ends after its last barrier
+ * (an ended wavefront no longer takes part in the workgroup's barriers);
+ * wavefronts of rows past the batch end at once.  Workgroups go to the XCDs
+ * as in attn_mix_kernel. */
+constexpr int kMixRows = 2;
+constexpr int kMixPairs = 6 * kMixRows;
+constexpr int kMixRowsSlotBytes = kMixChunk * 256 + kMixPairs * kMixChunk * 4;
+constexpr int kMixProbOps = kMixPairs * kMixChunk / 64;   /* probability loads per chunk */
+constexpr int kMixRowsOps = kMixVOps + kMixProbOps;
+/* chunks loaded ahead: every load of kMixRowsAhead chunks in flight fits the
+ * vmcnt range; the ring keeps its kMixSlots slots (the chains' slot
+ * arithmetic), of which chunks c - 1 .. c + kMixRowsAhead are in use */
+constexpr int kMixRowsAhead = 4;
+static_assert(kMixRowsOps * kMixRowsAhead <= 63 && kMixRowsAhead + 2 <= kMixSlots,
+              "loads in flight within the vmcnt range");
+
+__global__ __launch_bounds__(64 * (kMixPairs + 1)) void attn_mix_rows_kernel(
+    float *__restrict__ out, const float *__restrict__ prob, const float *__restrict__ q_and_gate,
+    long long qg_stride, const float *__restrict__ value_cache, int context, const uint32_t *__restrict__ position_ptr,
+    int rows)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kMixSlots * kMixRowsSlotBytes];
+    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3, lane = threadIdx.x & 63;
+    const int kvh = xcd >> 1, slice = 2 * (xcd & 1) + (j & 1);
+    const int t0 = (j >> 1) * kMixRows;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int pos0 = (int)*position_ptr;
+    const int group_rows = rows - t0 < kMixRows ? rows - t0 : kMixRows;
+    const uint32_t pitch4 = value_pitch((uint32_t)context) * 4u;
+    if (wave == kMixPairs) {
+        /* streaming wavefront: chunks of positions 0 .. n_max - 1 */
+        const int n_max = pos0 + t0 + group_rows;
+        const int chunks = (n_max + kMixChunk - 1) / kMixChunk, last = chunks - 1;
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(value_cache), 0, (int)(kKVDim * pitch4), kMixRawBuffer);
+        /* the probabilities of the group's rows; pairs of rows past the batch read as zero */
+        const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(prob + (size_t)t0 * kAttnHeads * context), 0,
+            group_rows * kAttnHeads * context * 4, kMixRawBuffer);
+        uint32_t v_lane[kMixVOps];
+#pragma unroll
+        for (int jj = 0; jj < kMixVOps; ++jj)
+            v_lane[jj] = (uint32_t)(kvh * kAttnDim + 64 * slice + 8 * jj + (lane >> 3)) * pitch4 +
+                         16u * (uint32_t)((lane & 7) ^ ((lane >> 3) & 7) ^ (jj & 1));
+        /* probability load k, lane i: float 64 k + i of the slot's records =
+         * pair (64 k + i) / 32, position (64 k + i) % 32 of the chunk */
+        uint32_t p_lane[kMixProbOps];
+#pragma unroll
+        for (int k = 0; k < kMixProbOps; ++k) {
+            const int f = 64 * k + lane, pair = f / kMixChunk, pos = f % kMixChunk;
+            const int tt = pair / 6, hh = pair % 6;
+            p_lane[k] = (uint32_t)(((tt * kAttnHeads + kvh * 6 + hh) * context + pos) * 4);
+        }
+        const uint32_t ring_base = __builtin_amdgcn_readfirstlane(lds_address(ring));
+        auto load_chunk = [&](int c, uint32_t slot) {
+            const uint32_t chunk_off = (uint32_t)(c < last ? c : last) * (kMixChunk * 4);
+#pragma unroll
+            for (int jj = 0; jj < kMixVOps; ++jj)
+                asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, %3 offen lds"
+                             :: "v"(v_lane[jj]), "s"(slot + 1024 * jj), "s"(vr), "s"(chunk_off) : "memory", "m0");
+            /* the chunk offset goes into the range-checked lane offset */
+#pragma unroll
+            for (int k = 0; k < kMixProbOps; ++k)
+                asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, 0 offen lds"
+                             :: "v"(p_lane[k] + (uint32_t)c * (kMixChunk * 4)),
+                                "s"(slot + kMixChunk * 256 + 256 * k), "s"(pr)
+                             : "memory", "m0");
+        };
+#pragma unroll
+        for (int c = 0; c < kMixRowsAhead; ++c) load_chunk(c, ring_base + c * kMixRowsSlotBytes);
+        mix_wait_vmcnt<kMixRowsOps * (kMixRowsAhead - 1)>();   /* chunk 0 */
         mix_barrier();
-        const uint8_t *slot = ring + (full % kMixSlots) * kMixSlotBytes;
-        const float *ps = reinterpret_cast<const float *>(slot + kMixChunk * 256);
-        for (int k = 0; k < rest; ++k)
-            o = __builtin_fmaf(ps[k], *reinterpret_cast<const float *>(slot + mix_quad(lane, k >> 2) + 4 * (k & 3)), o);
+#pragma unroll 1
+        for (int c = 0; c < chunks; ++c) {
+            mix_wait_vmcnt<kMixRowsOps * (kMixRowsAhead - 2)>();   /* chunk c + 1 */
+            mix_barrier();
+            /* chunk c - 1 is consumed; the slot of chunk c + kMixRowsAhead is free */
+            load_chunk(c + kMixRowsAhead, ring_base + ((c + kMixRowsAhead) % kMixSlots) * kMixRowsSlotBytes);
+        }
+        mix_wait_vmcnt<0>();
+        return;
     }
+    const int tt = wave / 6, hh = wave % 6;
+    if (tt >= group_rows) return;
+    const int t = t0 + tt, h = kvh * 6 + hh;
+    const float o = mix_chain(ring, kMixRowsSlotBytes, pos0 + t + 1, lane, wave);
     const int dim = h * kAttnDim + 64 * slice + lane;
     const float g = q_and_gate[(size_t)t * qg_stride + h * 2 * kAttnDim + kAttnDim + 64 * slice + lane];
     out[(size_t)t * kQDim + dim] = __fmul_rn(o, sigmoidf_exact(g));
@@ -1169,8 +1277,12 @@ void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_
                                                                                               position);
     else
         attn_softmax_kernel<false><<<dim3(kAttnHeads, rows), 256, 0, stream>>>(scores, context, position);
-    attn_mix_kernel<<<dim3(8 * 12 * rows), 128, 0, stream>>>(attn, scores, q_and_gate, in_stride, value_cache, context,
-                                                            position);
+    if (rows > kMixRows)
+        attn_mix_rows_kernel<<<dim3(16 * ((rows + kMixRows - 1) / kMixRows)), 64 * (kMixPairs + 1), 0, stream>>>(
+            attn, scores, q_and_gate, in_stride, value_cache, context, position, rows);
+    else
+        attn_mix_kernel<<<dim3(8 * 12 * rows), 128, 0, stream>>>(attn, scores, q_and_gate, in_stride, value_cache,
+                                                                context, position);
     launch_quantize(attn, q_out, (uint32_t)(rows * kAttnHeads), stream);
 }
 
