@@ -216,8 +216,8 @@ __device__ __forceinline__ float avx2_tree32(float v)
  * once, kept in registers, and each row's result is written to the next
  * slot (with `last_only`, only the last row's, to slot *slot_ptr + rows).
  * The block's inputs (k and q of head h % 16, the block's eight v values,
- * alpha and beta of head h) come through LDS in chunks of kScanChunk rows,
- * the next chunk's global loads in flight while the current one is
+ * the decay and beta of head h) come through LDS in chunks of kScanChunk
+ * rows, the next chunk's global loads in flight while the current one is
  * scanned, so the sequential scan reads only LDS. */
 constexpr int kScanChunk = 16;
 
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
 {
     __shared__ float kq_s[2][kScanChunk][2 * kHeadDim];   /* [parity][row][k 0..127 | q 0..127] */
     __shared__ float v_s[2][kScanChunk][8];
-    __shared__ float ab_s[2][kScanChunk][2];               /* alpha, beta */
+    __shared__ float ab_s[2][kScanChunk][2];               /* decay = expf(alpha), beta */
     const int tid = threadIdx.x;
     const int column_global = blockIdx.x * 8 + (tid >> 5);   /* 0 .. 48*128-1 */
     const int h = column_global >> 7;
@@ -264,11 +264,31 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
                                        : row[(tid & 1) ? beta_off + h : alpha_off + h];
         }
     };
+    /* the chunk's inputs into LDS; the decay expf(alpha) of each row is
+     * computed here, in parallel, off the scan's dependent chain */
     auto stage = [&](int par) {
 #pragma unroll
         for (int i = 0; i < kScanChunk; ++i) kq_s[par][i][tid] = kq_r[i];
         if (tid < 8 * kScanChunk) v_s[par][tid >> 3][tid & 7] = x_r;
-        else if (tid < 10 * kScanChunk) ab_s[par][(tid - 8 * kScanChunk) >> 1][tid & 1] = x_r;
+        else if (tid < 10 * kScanChunk)
+            ab_s[par][(tid - 8 * kScanChunk) >> 1][tid & 1] = (tid & 1) ? x_r : q38_expf(x_r);
+    };
+    /* a row's inputs from LDS, its decay computed there too, so that the
+     * next row's reads and expf overlap the current row's dependent chain */
+    struct RowIn {
+        float k[4], q[4], v, beta, decay;
+    };
+    auto read_row = [&](int par, int i) {
+        RowIn in;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            in.k[a] = kq_s[par][i][32 * a + l];
+            in.q[a] = kq_s[par][i][kHeadDim + 32 * a + l];
+        }
+        in.v = v_s[par][i][(tid >> 5) & 7];
+        in.beta = ab_s[par][i][1];
+        in.decay = ab_s[par][i][0];
+        return in;
     };
     fetch(0);
     stage(0);
@@ -278,29 +298,26 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
         if (ch + 1 < nchunks) fetch(ch + 1);
         const int r0 = ch * kScanChunk;
         const int n = rows - r0 < kScanChunk ? rows - r0 : kScanChunk;
+        RowIn cur = read_row(par, 0);
         for (int i = 0; i < n; ++i) {
             const int t = r0 + i;
-            const float decay = q38_expf(ab_s[par][i][0]);
-            float kv[4], qv[4];
-            for (int a = 0; a < 4; ++a) {
-                sv[a] = __fmul_rn(sv[a], decay);
-                kv[a] = kq_s[par][i][32 * a + l];
-                qv[a] = kq_s[par][i][kHeadDim + 32 * a + l];
-            }
+            const RowIn nxt = read_row(par, i + 1 < n ? i + 1 : i);
+            for (int a = 0; a < 4; ++a) sv[a] = __fmul_rn(sv[a], cur.decay);
             float p = 0.0f;
-            for (int a = 0; a < 4; ++a) p = __builtin_fmaf(sv[a], kv[a], p);
+            for (int a = 0; a < 4; ++a) p = __builtin_fmaf(sv[a], cur.k[a], p);
             const float pred = avx2_tree32(p);
-            const float delta = __fmul_rn(__fsub_rn(v_s[par][i][(tid >> 5) & 7], pred), ab_s[par][i][1]);
+            const float delta = __fmul_rn(__fsub_rn(cur.v, pred), cur.beta);
             float *s_out = state + (size_t)((slot0 + t + 1) % kStateSlots) * slot_stride + col_off;
             const bool store = !last_only || t == rows - 1;
             float r = 0.0f;
             for (int a = 0; a < 4; ++a) {
-                sv[a] = __builtin_fmaf(kv[a], delta, sv[a]);
+                sv[a] = __builtin_fmaf(cur.k[a], delta, sv[a]);
                 if (store) s_out[32 * a + l] = sv[a];
-                r = __builtin_fmaf(sv[a], qv[a], r);
+                r = __builtin_fmaf(sv[a], cur.q[a], r);
             }
             const float result = avx2_tree32(r);
             if (l == 0) out[(size_t)t * kLinV + h * kHeadDim + c] = __fmul_rn(result, query_scale);
+            cur = nxt;
         }
         if (ch + 1 < nchunks) stage(par ^ 1);
         __syncthreads();
@@ -449,7 +466,7 @@ __global__ __launch_bounds__(256) void deltanet_fused_kernel(float *__restrict__
 {
     __shared__ float qk_s[kFusedRows][256];   /* SiLU outputs: q of head kh (0..127), k (128..255) */
     __shared__ float v_s[kFusedRows][8];
-    __shared__ float beta_s[kFusedRows], alpha_s[kFusedRows];
+    __shared__ float beta_s[kFusedRows], alpha_s[kFusedRows];   /* beta and decay = expf(alpha) */
     __shared__ double part_s[kFusedRows][4];
     __shared__ float scale_s[kFusedRows][2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -471,7 +488,10 @@ __global__ __launch_bounds__(256) void deltanet_fused_kernel(float *__restrict__
     if (tid >= 64 && tid < 64 + rows) {
         const float *row = qkv + (long long)(tid - 64) * ld;
         beta_s[tid - 64] = sigmoidf_exact(row[beta_off + h]);
-        alpha_s[tid - 64] = __fmul_rn(ssm_a[h], softplusf_exact(__fadd_rn(row[alpha_off + h], ssm_dt[h])));
+        /* the row's decay expf(alpha), here in parallel rather than on the
+         * state update's dependent chain */
+        alpha_s[tid - 64] =
+            q38_expf(__fmul_rn(ssm_a[h], softplusf_exact(__fadd_rn(row[alpha_off + h], ssm_dt[h]))));
     }
     /* L2 norms of q and k per row: the double sum of squares of each
      * 128-vector as block_sum_finish (two wavefronts each) */
@@ -498,7 +518,7 @@ __global__ __launch_bounds__(256) void deltanet_fused_kernel(float *__restrict__
 
     /* state update (deltanet_state_kernel) */
     for (int t = 0; t < rows; ++t) {
-        const float decay = q38_expf(alpha_s[t]);
+        const float decay = alpha_s[t];
         const float qs = scale_s[t][0], ks = scale_s[t][1];
         float kv[4], qv[4];
         for (int a = 0; a < 4; ++a) {
