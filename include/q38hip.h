@@ -53,6 +53,31 @@ typedef struct {
     void *iq1_s_repack;
 } Q38GGUFTensor;
 
+/* Layout-compatible with Q38GGUFMeta / Q38GGUF
+ * (include/qwen38/qwen38_gguf.h:59-90): the reference's mapped GGUF file,
+ * which q38_prepare_iq1_s_repacks takes. */
+typedef struct {
+    Q38GGUFString key;
+    uint32_t type;
+    uint32_t array_type;
+    uint64_t count;
+    const uint8_t *data;
+    uint64_t data_size;
+} Q38GGUFMeta;
+
+typedef struct {
+    int fd;
+    const uint8_t *mapping;
+    uint64_t mapping_size;
+    uint32_t version;
+    uint32_t alignment;
+    uint64_t data_offset;
+    uint64_t tensor_count;
+    uint64_t metadata_count;
+    Q38GGUFTensor *tensors;
+    Q38GGUFMeta *metadata;
+} Q38GGUF;
+
 /* ---- 1. reference kernel ABI, host pointers ------------------------------ */
 
 /* replaces q38_f16_to_f32, include/qwen38/qwen38_quant.h:20 */
@@ -102,8 +127,8 @@ int q38_tensor_gemm_q8_k(float *output, const Q38Q8KBlock *input,
  * include/qwen38/qwen38_quant.h:54-55 (argument: the caller's Q38GGUF).
  * The GPU kernels read IQ1_S blocks as stored, so no view is built:
  * prepare returns 1 for a non-NULL argument and changes nothing. */
-int q38_prepare_iq1_s_repacks(void *gguf);
-void q38_release_iq1_s_repacks(void *gguf);
+int q38_prepare_iq1_s_repacks(Q38GGUF *gguf);
+void q38_release_iq1_s_repacks(Q38GGUF *gguf);
 
 /* ---- 2. device-resident variants ---------------------------------------- */
 

@@ -540,7 +540,7 @@ int q38_tensor_row_f32(float *output, const Q38GGUFTensor *tensor, uint64_t row)
 
 /* The GPU kernels read the GGUF blocks as they are, so there is no IQ1_S
  * view to build: both calls succeed and leave every tensor unchanged. */
-int q38_prepare_iq1_s_repacks(void *gguf) { return gguf ? 1 : 0; }
-void q38_release_iq1_s_repacks(void *gguf) { (void)gguf; }
+int q38_prepare_iq1_s_repacks(Q38GGUF *gguf) { return gguf ? 1 : 0; }
+void q38_release_iq1_s_repacks(Q38GGUF *gguf) { (void)gguf; }
 
 }  // extern "C"

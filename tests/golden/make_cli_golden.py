@@ -36,21 +36,21 @@ sys.path.insert(0, os.path.join(ROOT, "qwen3.8-27b-in-c_amd"))
 SEED = 1
 # (name, arguments after --model PATH)
 CASES = [
-    ("greedy", ["--context", "256", "--prompt", "hello there", "--temperature", "0", "--max-tokens", "32",
+    ("greedy", ["--context", "512", "--prompt", "hello there", "--temperature", "0", "--max-tokens", "32",
                 "--no-thinking"]),
-    ("greedy_mtp", ["--context", "256", "--prompt", "hello there", "--temperature", "0", "--max-tokens", "32",
+    ("greedy_mtp", ["--context", "512", "--prompt", "hello there", "--temperature", "0", "--max-tokens", "32",
                     "--no-thinking", "--mtp"]),
-    ("mtp_depth5_system", ["--context", "256", "--system", "Answer in one line.", "--prompt", "the cat sat",
+    ("mtp_depth5_system", ["--context", "512", "--system", "Answer in one line.", "--prompt", "the cat sat",
                            "--temperature", "0", "--max-tokens", "20", "--mtp", "--mtp-depth", "5"]),
-    ("sampled", ["--context", "256", "--prompt", "write a haiku", "--temperature", "0.8", "--top-k", "20",
+    ("sampled", ["--context", "512", "--prompt", "write a haiku", "--temperature", "0.8", "--top-k", "20",
                  "--top-p", "0.95", "--seed", "7", "--max-tokens", "24"]),
-    ("sampled_presence", ["--context", "256", "--prompt", "tell me", "--no-thinking", "--seed", "11",
+    ("sampled_presence", ["--context", "512", "--prompt", "tell me", "--no-thinking", "--seed", "11",
                           "--max-tokens", "24"]),
 ]
 
 # (name, server arguments after --model PATH, requests: chat-completion bodies)
 SERVER_RUNS = [
-    ("server", ["--context", "256", "--no-thinking"], [
+    ("server", ["--context", "512", "--no-thinking"], [
         {"model": "qwen3.8-27b-in-c", "messages": [{"role": "user", "content": "hello there"}],
          "temperature": 0, "max_tokens": 16},
         {"model": "qwen3.8-27b-in-c", "messages": [{"role": "system", "content": "Be brief."},
@@ -59,7 +59,7 @@ SERVER_RUNS = [
         {"model": "qwen3.8-27b-in-c", "messages": [{"role": "user", "content": "hello there"}],
          "temperature": 0, "max_tokens": 16},
     ]),
-    ("server_mtp", ["--context", "256", "--no-thinking", "--mtp"], [
+    ("server_mtp", ["--context", "512", "--no-thinking", "--mtp"], [
         {"model": "qwen3.8-27b-in-c", "messages": [{"role": "user", "content": "hello there"}],
          "temperature": 0, "max_tokens": 16},
         {"model": "qwen3.8-27b-in-c", "messages": [{"role": "user", "content": "and again"}],
