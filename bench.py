@@ -82,8 +82,8 @@ WORKLOADS = {
 DEVICE_KERNEL = {
     "q4k_gemv": "gemm_q8k_stream<12, 1>",
     "q4k_gemv_t": "gemm_q8k_ring<12, 1, 3, 16, 2>",
-    "iq1m_gemv": "gemm_iq1m_mfma<1, 20, 8, 2, true>",
-    "iq1m_gemv_t": "gemm_iq1m_mfma<1, 68, 8, 2, true>",
+    "iq1m_gemv": "gemm_iq1m_dot4<20, 15, 2>",
+    "iq1m_gemv_t": "gemm_iq1m_dot4<68, 16, 2>",
     "q4k_tiled_m3": "gemm_q4k_mm16<3, 20, 9, 4, 1>",
     "q4k_tiled_down_m3": "gemm_q4k_t32r<3, 68, 8, 1>",
     "q4k_tiled_out_m3": "gemm_q4k_t32r<3, 24, 8, 1>",

@@ -73,10 +73,18 @@ DeviceState *device_state()
     if ((int)g_devices.size() <= device) g_devices.resize(device + 1);
     DeviceState &s = g_devices[device];
     if (!s.grid) {
-        int8_t host[2048 * 8];
+        /* 2048 entries of 8 ternary values, then the 4096-entry signed
+         * table of the one-token IQ1_M kernel: entry i + 2048 h holds the
+         * bytes 8 g + (h ? -1 : 1) of entry i */
+        static int8_t host[(2048 + 4096) * 8];
         for (int e = 0; e < 2048; ++e) {
             const uint32_t code = q38_iq1m_grid_codes[e];
-            for (int k = 0; k < 8; ++k) host[8 * e + k] = (int8_t)(((code >> (2 * k)) & 3u) - 1);
+            for (int k = 0; k < 8; ++k) {
+                const int g = (int)((code >> (2 * k)) & 3u) - 1;
+                host[8 * e + k] = (int8_t)g;
+                host[8 * (2048 + e) + k] = (int8_t)(8 * g + 1);
+                host[8 * (4096 + e) + k] = (int8_t)(8 * g - 1);
+            }
         }
         if (hipMalloc(&s.grid, sizeof(host)) != hipSuccess) return nullptr;
         if (hipMemcpy(s.grid, host, sizeof(host), hipMemcpyHostToDevice) != hipSuccess) return nullptr;

@@ -275,6 +275,256 @@ bool launch_iq1m_nb(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_
 
 }  // namespace
 
+/* IQ1_M x Q8_K for ONE token on the vector ALU (v_dot4_i32_i8), over the
+ * 16-row tiled copy.  The sign of each 8-element section is folded into the
+ * codebook: the table that follows the 2048 grid entries in device memory
+ * holds 4096 entries, index = qs byte | (qh nibble << 8) with the nibble's
+ * sign bit as index bit 11, whose bytes are 8 g + delta (g in {-1, 0, 1},
+ * delta = -1 when the bit is set, else +1: bytes in {-9, -7, -1, 1, 7, 9}).
+ * For a 16-element half group with odd sub-scale s the block integer of the
+ * reference (E = 8 weighted + correction, see the header) gains
+ * s * sum_e (8 g(e) + delta) a(e): four v_dot4_i32_i8 of codebook bytes and
+ * activation quants and one multiply-add.  E is exact in int32 and the fp32
+ * chain is the reference's, total += d * (float(E) * 0.125f),
+ * d = dscale * xs, in block order.
+ *
+ * Work unit: a quad of 4 weight rows.  Workgroup w of G owns quads
+ * [w Q / G, (w + 1) Q / G) (Q = rows / 4), so 256 workgroups split both the
+ * 17408- and the 5120-row shapes evenly.  A wavefront item is one quad x 4
+ * consecutive blocks (4 pieces of 224 contiguous bytes, copied into the
+ * wavefront's LDS ring by one global_load_lds_dwordx4 of 56 lanes): lane
+ * (j, r, q) = (lane / 16, lane / 4 % 4, lane % 4) takes row r of the quad,
+ * block 4 g + j of the item's block group g and elements 64 q .. 64 q + 63
+ * of it (qs[8q..8q+7], qh[4q..4q+3], scale word q: its 4 half groups); the
+ * 4 lanes of a row sum their E with two DPP quad permutations.  Items go to
+ * the S wavefronts round-robin; when S is a multiple of the number of block
+ * groups every item of a wavefront has the same blocks and its activation
+ * quants stay in registers.  Each item's per-(row, block) products
+ * t = d * (E * 0.125f) land in LDS; after the last item and one barrier one
+ * thread per row adds its terms in block order.
+ *
+ * Every global read is an LDS copy with explicit vmcnt waits: per
+ * wavefront, first its share of the staging (the 32 KiB table, the
+ * activation quants, the scales), then the first P items; copies retire in
+ * issue order, so after the staging wait and one barrier an item's wait
+ * only counts the items issued after it. */
+constexpr uint32_t kDot4Groups = 256;   /* persistent workgroups: one per CU */
+constexpr int kDot4TFloats = 6144;      /* LDS terms [quad][block][row % 4] */
+constexpr int kDot4ActStride = 272;     /* activation quants per block in LDS (256 + 16: no bank aliasing) */
+constexpr int kDot4Slot = 896;          /* LDS ring slot: one item */
+
+namespace {
+
+__device__ __forceinline__ uint32_t dot4_lds_address(const void *p)
+{
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+}
+
+/* 16 bytes per lane from gaddr to LDS at m0 + 16 * lane, or 4 bytes to
+ * m0 + 4 * lane.  Inline assembly keeps the compiler's wait-count pass
+ * from draining these copies before unrelated LDS accesses; callers wait. */
+__device__ __forceinline__ void dot4_copy16(const void *gaddr, uint32_t m0)
+{
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(m0) : "memory", "m0");
+}
+
+__device__ __forceinline__ void dot4_copy4(const void *gaddr, uint32_t m0)
+{
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(gaddr), "s"(m0) : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void dot4_wait_vm()
+{
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+/* wait until at most c (0..7, wave-uniform) vector memory operations are
+ * outstanding */
+__device__ __forceinline__ void dot4_wait_vm_upto(int c)
+{
+    switch (c) {
+    case 0: dot4_wait_vm<0>(); break;
+    case 1: dot4_wait_vm<1>(); break;
+    case 2: dot4_wait_vm<2>(); break;
+    case 3: dot4_wait_vm<3>(); break;
+    case 4: dot4_wait_vm<4>(); break;
+    case 5: dot4_wait_vm<5>(); break;
+    case 6: dot4_wait_vm<6>(); break;
+    default: dot4_wait_vm<7>(); break;
+    }
+}
+
+}  // namespace
+
+template <int NB, int S, int P>
+__global__ __launch_bounds__(64 * S) void gemm_iq1m_dot4(const uint8_t *__restrict__ w, const uint8_t *__restrict__ x,
+                                                         float *__restrict__ y, uint32_t rows,
+                                                         const uint2 *__restrict__ grid)
+{
+    constexpr int NG = NB / 4;              /* block groups */
+    constexpr bool ACT_REG = S % NG == 0;   /* fixed block group per wavefront */
+    static_assert(NB % 4 == 0, "blocks per row must be a multiple of 4");
+    static_assert(P >= 1 && P <= 4, "1..4 items in flight");
+    __shared__ __attribute__((aligned(16))) uint2 cb_s[4096];
+    __shared__ __attribute__((aligned(16))) uint8_t act_s[NB * kDot4ActStride];
+    __shared__ float xs_s[NB > 64 ? 128 : 64];
+    __shared__ float t_s[kDot4TFloats];
+    __shared__ __attribute__((aligned(16))) uint8_t ring_s[S * P * kDot4Slot];
+
+    const uint32_t nquads = (rows + 3) / 4;
+    const uint32_t q0 = (uint32_t)(((uint64_t)blockIdx.x * nquads) / gridDim.x);
+    const uint32_t q1 = (uint32_t)(((uint64_t)(blockIdx.x + 1) * nquads) / gridDim.x);
+    if (q0 == q1) return;
+    const int items = (int)(q1 - q0) * NG;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane >> 4, r = (lane >> 2) & 3, q = lane & 3;
+    const int mine = wv < items ? (items - wv + S - 1) / S : 0;   /* the wavefront's items: wv + S n */
+
+    /* staging copies, round-robin over the wavefronts: 32 x 1 KiB of the
+     * table, one 256-byte block of activation quants per copy (16 lanes),
+     * the scales (4 bytes per lane) */
+    const uint8_t *table = reinterpret_cast<const uint8_t *>(grid + 2048);
+    for (int k = wv; k < 32; k += S) dot4_copy16(table + 1024 * k + 16 * lane, dot4_lds_address(cb_s) + 1024 * k);
+    for (int b = (wv + S - 32 % S) % S; b < NB; b += S)
+        if (lane < 16)
+            dot4_copy16(x + (size_t)b * kQ8KBytes + 4 + 16 * lane, dot4_lds_address(act_s) + b * kDot4ActStride);
+    if (wv == S - 1) {
+        if (lane < NB) dot4_copy4(x + (size_t)lane * kQ8KBytes, dot4_lds_address(xs_s));
+        if (NB > 64 && lane < NB - 64) dot4_copy4(x + (size_t)(lane + 64) * kQ8KBytes, dot4_lds_address(xs_s) + 256);
+    }
+
+    /* item n of the wavefront into ring slot n % P: lane l < 56 copies
+     * bytes 16 (l % 14) .. + 15 of piece l / 14 (block 4 g + l / 14, the
+     * quad's 4 rows) to slot byte 16 l */
+    const uint32_t ring = dot4_lds_address(ring_s) + (uint32_t)(wv * P * kDot4Slot);
+    const int cj = lane / 14, cp = lane - 14 * (lane / 14);
+    auto issue = [&](int n, int slot) {
+        const int i = wv + S * n;
+        const uint32_t quad = q0 + (uint32_t)(i / NG);
+        const uint32_t b = (uint32_t)(4 * (i % NG) + cj);
+        const uint8_t *src = w + (size_t)(((quad >> 2) * NB + b) * 16u + ((quad & 3u) << 2)) * kIQ1MBytes + 16 * cp;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   /* the slot's previous reads are done */
+        if (lane < 56) dot4_copy16(src, ring + (uint32_t)(slot * kDot4Slot));
+    };
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+        if (i < mine) issue(i, i);
+    dot4_wait_vm_upto(mine < P ? mine : P);   /* this wavefront's staging copies have landed */
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    int4v ar[4];   /* activation quants of the fixed block group */
+    if (ACT_REG) {
+        const int b = 4 * (wv % NG) + j;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            ar[k] = *reinterpret_cast<const int4v *>(act_s + b * kDot4ActStride + 64 * q + 16 * k);
+    }
+    const uint8_t *rowp = ring_s + wv * P * kDot4Slot + 224 * j + 56 * r;
+
+    auto item = [&](int n, int slot) {
+        const int left = mine - 1 - n;   /* copies issued after this item's */
+        dot4_wait_vm_upto(left < P - 1 ? left : P - 1);
+        const uint8_t *bp = rowp + slot * kDot4Slot;
+        const int2v qs = *reinterpret_cast<const int2v *>(bp + 8 * q);
+        const uint32_t qh = *reinterpret_cast<const uint32_t *>(bp + 32 + 4 * q);
+        const int2v sc = *reinterpret_cast<const int2v *>(bp + 48);
+        const uint32_t qs0 = (uint32_t)qs[0], qs1 = (uint32_t)qs[1], sc0 = (uint32_t)sc[0], sc1 = (uint32_t)sc[1];
+        const int i = wv + S * n;
+        const int ql = i / NG;
+        const int b = 4 * (i % NG) + j;
+        int4v a[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            a[k] = ACT_REG ? ar[k] : *reinterpret_cast<const int4v *>(act_s + b * kDot4ActStride + 64 * q + 16 * k);
+        /* 12-bit table indices of the lane's 8 sections, two per dword,
+         * pre-shifted to byte offsets (x 8) */
+        const uint32_t nlo = qh & 0x0f0f0f0fu, nhi = (qh >> 4) & 0x0f0f0f0fu;
+        const uint32_t n03 = __builtin_amdgcn_perm(nhi, nlo, 0x05010400u);   /* nibbles 0, 1, 2, 3 */
+        const uint32_t n47 = __builtin_amdgcn_perm(nhi, nlo, 0x07030602u);   /* nibbles 4, 5, 6, 7 */
+        const uint32_t p[4] = {__builtin_amdgcn_perm(n03, qs0, 0x05010400u) << 3,
+                               __builtin_amdgcn_perm(n03, qs0, 0x07030602u) << 3,
+                               __builtin_amdgcn_perm(n47, qs1, 0x05010400u) << 3,
+                               __builtin_amdgcn_perm(n47, qs1, 0x07030602u) << 3};
+        const char *cb = reinterpret_cast<const char *>(cb_s);
+        const uint32_t scw = ((q & 2) ? sc1 : sc0) >> (16 * (q & 1));   /* scale word q */
+        int e = 0;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            /* half group h: sections 2h, 2h + 1 = elements 64 q + 16 h .. + 15 */
+            const uint2 e0 = *reinterpret_cast<const uint2 *>(cb + (p[h] & 0x7ff8u));
+            const uint2 e1 = *reinterpret_cast<const uint2 *>(cb + (p[h] >> 16));
+            const int4v av4 = a[h];
+            int acc = dot4z((int)e0.x, av4[0]);
+            acc = dot4((int)e0.y, av4[1], acc);
+            acc = dot4((int)e1.x, av4[2], acc);
+            acc = dot4((int)e1.y, av4[3], acc);
+            e = mad24((int)(2u * ((scw >> (3 * h)) & 7u) + 1u), acc, e);
+        }
+        /* sum over the 4 lanes of the row (quad_perm [1,0,3,2], [2,3,0,1]) */
+        e += __builtin_amdgcn_update_dpp(0, e, 0xb1, 0xf, 0xf, false);
+        e += __builtin_amdgcn_update_dpp(0, e, 0x4e, 0xf, 0xf, false);
+        const uint32_t bits =
+            ((sc0 >> 12) & 0x000fu) | ((sc0 >> 24) & 0x00f0u) | ((sc1 >> 4) & 0x0f00u) | ((sc1 >> 16) & 0xf000u);
+        const float d = fmul_rn(f16_to_f32(bits), xs_s[b]);
+        const float t = fmul_rn(d, fmul_rn((float)e, 0.125f));
+        if (q == 0) t_s[(ql * NB + b) * 4 + r] = t;
+    };
+
+    const int full = mine / P, rem = mine % P;
+#pragma unroll 1
+    for (int it = 0; it < full; ++it) {
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int n = it * P + i;
+            item(n, i);
+            if (n + P < mine) issue(n + P, i);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+        if (i < rem) item(full * P + i, i);
+    __syncthreads();
+
+    /* one thread per row: the fp32 chain in block order */
+    for (int c = tid; c < (int)(q1 - q0) * 4; c += 64 * S) {
+        const int ql = c >> 2, rr = c & 3;
+        float total = 0.0f;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) total = fadd_rn(total, t_s[(ql * NB + b) * 4 + rr]);
+        const uint32_t row = (q0 + (uint32_t)ql) * 4 + (uint32_t)rr;
+        if (row < rows) y[row] = total;
+    }
+}
+
+namespace {
+
+/* wavefronts per workgroup: a multiple of the block groups (NB / 4) where
+ * that fits in 16, so the activation quants stay in registers */
+template <int NB>
+constexpr int dot4_waves()
+{
+    return NB == 20 ? 15 : NB == 24 ? 12 : NB == 40 ? 10 : 16;
+}
+constexpr int kDot4Prefetch = 2;
+
+template <int NB>
+bool launch_iq1m_dot4(const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, const uint2 *grid,
+                      hipStream_t stream)
+{
+    const uint32_t nquads = (rows + 3) / 4;
+    const uint32_t groups = nquads < kDot4Groups ? nquads : kDot4Groups;
+    const uint32_t per = (nquads + groups - 1) / groups;
+    if ((size_t)per * NB * 4 > (size_t)kDot4TFloats) return false;
+    hipLaunchKernelGGL((gemm_iq1m_dot4<NB, dot4_waves<NB>(), kDot4Prefetch>), dim3(groups), dim3(64 * dot4_waves<NB>()),
+                       0, stream, w, x, y, rows, grid);
+    return hipGetLastError() == hipSuccess;
+}
+
+}  // namespace
+
 /* IQ1_M x Q8_K for prefill batches (any token count): the products of
  * gemm_iq1m_mfma (per 16-row x 16-token tile and 64-element chunk,
  * E = 8 * A.[s grid] + A.[s sign] on v_mfma_i32_16x16x64_i8, the lane
@@ -516,6 +766,17 @@ bool launch_gemm_iq1m_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, flo
 {
     if (!rows || ldy < rows || !grid) return false;
     const uint2 *g = static_cast<const uint2 *>(grid);
+    if (m == 1) {
+        bool ok = false;
+        switch (nb) {
+        case 20: ok = launch_iq1m_dot4<20>(w_tiled, x, y, rows, g, stream); break;
+        case 24: ok = launch_iq1m_dot4<24>(w_tiled, x, y, rows, g, stream); break;
+        case 40: ok = launch_iq1m_dot4<40>(w_tiled, x, y, rows, g, stream); break;
+        case 68: ok = launch_iq1m_dot4<68>(w_tiled, x, y, rows, g, stream); break;
+        default: break;
+        }
+        if (ok) return true;
+    }
     switch (nb) {
     case 20: return launch_iq1m_nb<20, true>(m, w_tiled, x, y, ldy, rows, g, stream);
     case 24: return launch_iq1m_nb<24, true>(m, w_tiled, x, y, ldy, rows, g, stream);

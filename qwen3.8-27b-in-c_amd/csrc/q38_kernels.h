@@ -10,7 +10,8 @@ namespace q38 {
 constexpr uint32_t kRecurrentStateSlots = 9;
 
 /* q38_gemm.hip: y[m][rows] = W (rows x nblk*256, GGUF type) . x (m Q8_K rows);
- * m <= 8.  `grid` is the device IQ1_M codebook (2048 x 8 int8). */
+ * m <= 8.  `grid` is the device IQ1_M codebook: 2048 x 8 int8 grid values,
+ * followed by the one-token kernel's 4096 x 8 table of 8 g + delta (q38_abi.hip). */
 bool launch_gemm(int type, int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, uint32_t nblk,
                  const void *grid, hipStream_t stream);
 /* lane-chain kernel for 2..4 tokens; false when it does not apply */

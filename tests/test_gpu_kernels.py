@@ -186,12 +186,14 @@ def test_tiled_repack_and_gemm_bit_exact(hip, oracle, device, rows, width):
         assert np.array_equal(bits(got), bits(want)), "M=%d" % m
 
 
-@pytest.mark.parametrize("rows,width", [(48, 5120), (1000, 5120), (520, 10240), (5136, 17408), (2064, 6144)])
+@pytest.mark.parametrize("rows,width", [(48, 5120), (1000, 5120), (520, 10240), (5136, 17408), (2064, 6144),
+                                        (1003, 5120), (3, 6144)])
 def test_tiled_iq1m_repack_and_gemm_bit_exact(hip, oracle, device, rows, width):
     """16-row tiled IQ1_M copy ([tile][block][row % 16][56 bytes], zero rows
     past the last): the repack equals the host restatement of the layout, and
     the matrix-core kernel over it equals the oracle bit for bit for 1..8
-    tokens, with row counts that end inside a tile (1000, 520, 5136)."""
+    tokens, with row counts that end inside a tile (1000, 520, 5136) and
+    inside a 4-row quad (1003, 3: the one-token kernel's unit)."""
     w = synth.matrix(IQ1_M, rows, width, seed=rows + 2 * width)
     wd = to_dev(w, device)
     tiled = hip.repack_iq1m_tiles(wd, width, rows)
