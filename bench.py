@@ -59,8 +59,8 @@ PEAK_HBM_GBS = 8000.0
 
 WORKLOADS = {
     # name: (type, rows, width, tokens, tiled, label)
-    "q4k_gemv": (12, 17408, 5120, 1, False, "Q4_K GEMV 17408x5120"),
-    "q4k_gemv_t": (12, 5120, 17408, 1, False, "Q4_K GEMV 5120x17408"),
+    "q4k_gemv": (12, 17408, 5120, 1, True, "Q4_K GEMV 17408x5120"),
+    "q4k_gemv_t": (12, 5120, 17408, 1, True, "Q4_K GEMV 5120x17408"),
     "iq1m_gemv": (29, 17408, 5120, 1, True, "IQ1_M GEMV 17408x5120"),
     "iq1m_gemv_t": (29, 5120, 17408, 1, True, "IQ1_M GEMV 5120x17408"),
     "q6k_gemv": (14, 17408, 5120, 1, False, "Q6_K GEMV 17408x5120"),
@@ -80,8 +80,8 @@ WORKLOADS = {
 # device kernel each launch of a workload runs (q38hip dispatch for that shape; the
 # trace summaries and counter profiles under profiles/ name the same kernels)
 DEVICE_KERNEL = {
-    "q4k_gemv": "gemm_q8k_stream<12, 1>",
-    "q4k_gemv_t": "gemm_q8k_ring<12, 1, 3, 16, 2>",
+    "q4k_gemv": "gemv_q4k_lanes<20, 4, 1>",
+    "q4k_gemv_t": "gemv_q4k_lanes<68, 12, 1>",
     "iq1m_gemv": "gemm_iq1m_dot4<20, 15, 2>",
     "iq1m_gemv_t": "gemm_iq1m_dot4<68, 16, 2>",
     "q4k_tiled_m3": "gemm_q4k_mm16<3, 20, 9, 4, 1>",

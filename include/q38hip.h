@@ -203,7 +203,7 @@ int q38hip_accept(uint32_t *result, const uint32_t *targets,
 
 /* Library extension (no counterpart in the reference): the 16-row tiled
  * layout of a Q4_K matrix that the model engine keeps beside the GGUF
- * layout for GEMMs of 2..8 tokens.  Tile k holds rows 16k..16k+15 as
+ * layout for its GEMVs and GEMMs.  Tile k holds rows 16k..16k+15 as
  * [block][row][144 bytes]; the last tile is zero-padded.
  * q38hip_tiled_q4k_bytes: size of the tiled copy of `rows` rows of
  * `input_length` elements.  q38hip_repack_q4k_tiles: write it from the
@@ -213,9 +213,9 @@ int q38hip_repack_q4k_tiles(void *tiled, const void *q4k_rows, uint32_t rows,
                             uint64_t input_length, void *stream);
 
 /* q38hip_gemm_q8_k over a tiled Q4_K copy: output[t * rows + r] for
- * t < batch_size (at least 2; launches of 2..8 tokens), input_length 5120,
- * 6144, 10240 or 17408.  The results are those of q38hip_gemm_q8_k bit for
- * bit. */
+ * t < batch_size (at least 1: one launch for one token or a prefill batch,
+ * else launches of 2..8 tokens), input_length 5120, 6144, 10240 or 17408.
+ * The results are those of q38hip_gemm_q8_k bit for bit. */
 int q38hip_gemm_q8_k_tiled(float *output, const Q38Q8KBlock *input,
                            uint32_t batch_size, uint64_t input_length,
                            const void *tiled, uint32_t rows, void *stream);

@@ -342,15 +342,15 @@ int q38hip_gemm_q8_k_tiled(float *output, const Q38Q8KBlock *input, uint32_t bat
                            const void *tiled, uint32_t rows, void *stream)
 {
     if (!output || !input || !tiled || !rows) return fail("null argument");
-    if (batch_size < 2) return fail("batch_size must be at least 2");
+    if (batch_size < 1) return fail("batch_size must be at least 1");
     if (!device_state()) return fail("device initialisation failed");
     if (input_length % Q38_Q8_K_BLOCK_SIZE) return fail("input length is not a multiple of 256");
     const uint32_t nb = (uint32_t)(input_length / 256);
-    /* one launch from kWideMinTokens tokens on, else launches of 2..8
-     * tokens (see q38hip_gemm_q8_k) */
+    /* one launch for one token or from kWideMinTokens tokens on, else
+     * launches of 2..8 tokens (see q38hip_gemm_q8_k) */
     for (uint32_t t0 = 0; t0 < batch_size;) {
-        const uint32_t n = batch_size - t0 >= (uint32_t)q38::kWideMinTokens ? batch_size - t0
-                                                                              : token_chunk(batch_size - t0, 2);
+        const uint32_t left = batch_size - t0;
+        const uint32_t n = left == 1 || left >= (uint32_t)q38::kWideMinTokens ? left : token_chunk(left, 2);
         if (!q38::launch_gemm_q4k_tiled((int)n, static_cast<const uint8_t *>(tiled),
                                         reinterpret_cast<const uint8_t *>(input) + (size_t)t0 * nb * sizeof(Q38Q8KBlock),
                                         output + (size_t)t0 * rows, rows, rows, nb, static_cast<hipStream_t>(stream)))

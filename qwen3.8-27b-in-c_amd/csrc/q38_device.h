@@ -26,9 +26,10 @@ __device__ __forceinline__ int dot4(int a, int b, int c)
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
-/* Same with a zero accumulator, as the three-operand VOP3P encoding with an
- * inline 0 (the builtin form is otherwise lowered to v_dot4c plus a v_mov
- * to clear the tied accumulator). */
+/* Same with a zero accumulator.  The builtin is lowered to v_dot4c plus a
+ * v_mov that clears the tied accumulator; the three-operand encoding written
+ * as inline assembly computed wrong sums in a kernel here (inline assembly
+ * is outside the compiler's hazard handling), so it is not used. */
 __device__ __forceinline__ int dot4z(int a, int b)
 {
     return __builtin_amdgcn_sdot4(a, b, 0, false);

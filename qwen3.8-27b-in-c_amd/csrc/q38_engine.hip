@@ -861,16 +861,16 @@ bool gemm_float(Q38Model *m, const DevTensor &w, uint32_t count, const float *xf
     return true;
 }
 
-/* the tiled copy's kernel where there is one: Q4_K for 2..8 rows and
- * prefill batches, IQ1_M for 1..8 rows (prefill batches keep the row-major
- * blocks); false when none ran */
+/* the tiled copy's kernel where there is one: Q4_K for any row count
+ * (one row, 2..8 rows and prefill batches), IQ1_M for 1..8 rows (prefill
+ * batches keep the row-major blocks); false when none ran */
 bool gemm_tiled(Q38Model *m, const DevTensor &w, uint32_t count, const uint8_t *x, float *out, uint32_t ldy,
                 uint32_t rows)
 {
     if (!w.tiled) return false;
     const uint32_t nb = (uint32_t)(w.width / 256);
     if (w.type == Q4_K)
-        return count >= 2 && q38::launch_gemm_q4k_tiled((int)count, w.tiled, x, out, ldy, rows, nb, m->stream);
+        return count >= 1 && q38::launch_gemm_q4k_tiled((int)count, w.tiled, x, out, ldy, rows, nb, m->stream);
     if (w.type == IQ1_M)
         return count >= 1 && count <= kBatch &&
                q38::launch_gemm_iq1m_tiled((int)count, w.tiled, x, out, ldy, rows, nb, m->grid, m->stream);

@@ -38,6 +38,10 @@ size_t tiled_iq1m_bytes(uint32_t rows, uint32_t nb);
 bool launch_repack_iq1m_tiles(uint8_t *dst, const uint8_t *src, uint32_t rows, uint32_t nb, hipStream_t stream);
 bool launch_gemm_q4k_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                            uint32_t nb, hipStream_t stream);
+/* one token over the 16-row Q4_K tiled copy (q38_q4k_gemv.hip): y[row] for
+ * widths of 20, 24, 40 or 68 blocks; false otherwise */
+bool launch_gemv_q4k_tiled(const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t rows, uint32_t nb,
+                           hipStream_t stream);
 /* same product, 32 weight rows per wavefront (v_mfma_f32_32x32x16_f16) */
 bool launch_gemm_q4k_t32(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                          uint32_t nb, hipStream_t stream);

@@ -421,7 +421,10 @@ bool launch_tiled_nb(int m, const uint8_t *w, const uint8_t *x, float *y, uint32
 bool launch_gemm_q4k_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                            uint32_t nb, hipStream_t stream)
 {
-    if (!rows || ldy < rows || m < 2) return false;
+    if (!rows || ldy < rows || m < 1) return false;
+    /* one token: v_dot4 / v_dot2 lanes, one per AVX2 accumulator lane
+     * (q38_q4k_gemv.hip) */
+    if (m == 1) return launch_gemv_q4k_tiled(w_tiled, x, y, rows, nb, stream);
     /* prefill batches: the 64 x 64 matrix-core tiles of q38_wide.hip */
     if (m >= kWideMinTokens) return launch_gemm_q4k_wide((uint32_t)m, w_tiled, x, y, ldy, rows, nb, stream);
     /* 2..4 tokens on the widest 20-block matrices (FFN gate|up): 16 rows

@@ -59,7 +59,7 @@ SERVER_RUNS = [
         {"model": "qwen3.8-27b-in-c", "messages": [{"role": "user", "content": "hello there"}],
          "temperature": 0, "max_tokens": 16},
     ]),
-    ("server_mtp", ["--context", "512", "--no-thinking", "--mtp"], [
+    ("server_mtp", ["--context", "512", "--no-thinking", "--mtp", "--temperature", "0"], [
         {"model": "qwen3.8-27b-in-c", "messages": [{"role": "user", "content": "hello there"}],
          "temperature": 0, "max_tokens": 16},
         {"model": "qwen3.8-27b-in-c", "messages": [{"role": "user", "content": "and again"}],

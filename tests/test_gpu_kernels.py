@@ -165,13 +165,14 @@ def tiled_numpy(w, rows, width):
 
 
 @pytest.mark.parametrize("rows,width", [(1000, 5120), (48, 5120), (2064, 6144), (520, 10240), (1040, 17408),
-                                        (4112, 5120), (4100, 6144), (5136, 17408)])
+                                        (4112, 5120), (4100, 6144), (5136, 17408), (3, 5120), (1003, 17408)])
 def test_tiled_repack_and_gemm_bit_exact(hip, oracle, device, rows, width):
-    """Tiled Q4_K copy (2..8 tokens, matrix cores) equals the oracle bit for bit;
-    the repack equals the host restatement of the layout (zero-padded tail).
-    From 4096 rows on, 2..8 tokens run the 32-row kernel (5..8 with a second
-    token set): 4112 and 5136 rows end on an unpaired 16-row tile, 4100 also
-    on a padded one."""
+    """Tiled Q4_K copy (one token on the dot4/dot2 lanes, 2..8 tokens on the
+    matrix cores) equals the oracle bit for bit; the repack equals the host
+    restatement of the layout (zero-padded tail).  From 4096 rows on, 2..8
+    tokens run the 32-row kernel (5..8 with a second token set): 4112 and
+    5136 rows end on an unpaired 16-row tile, 4100 also on a padded one; 3
+    and 1003 rows end inside the one-token kernel's 8-row groups."""
     w = synth.matrix(Q4_K, rows, width, seed=rows + width)
     wd = to_dev(w, device)
     tiled = hip.repack_q4k_tiles(wd, width, rows)
@@ -180,7 +181,7 @@ def test_tiled_repack_and_gemm_bit_exact(hip, oracle, device, rows, width):
     q = oracle.quantize(x.reshape(-1))
     xq = hip.quantize_q8_k(to_dev(x, device))
     nb = width // 256
-    for m in range(2, 9):
+    for m in range(1, 9):
         want = oracle.gemm(Q4_K, w, rows, q[:m * nb], m)
         got = hip.gemm_q8_k_tiled(tiled, width, rows, xq[:m * nb * 292], m).cpu().numpy()
         assert np.array_equal(bits(got), bits(want)), "M=%d" % m
@@ -226,7 +227,7 @@ def test_tiled_iq1m_full_shape_matches_row_major(hip, device, m):
         assert np.array_equal(bits(got), bits(want)), (rows, width)
 
 
-@pytest.mark.parametrize("m", [2, 3, 4, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
 def test_tiled_gemm_full_shape_matches_row_major(hip, device, m):
     """34816x5120 (fused gate|up) and 5120x17408 (down): tiled = row-major kernels;
     24584x5120 ends on an unpaired 16-row tile at a size where the 32-row
