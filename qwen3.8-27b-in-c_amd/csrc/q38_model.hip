@@ -1297,7 +1297,11 @@ void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_
                                                                                               position);
     else
         attn_softmax_kernel<false><<<dim3(kAttnHeads, rows), 256, 0, stream>>>(scores, context, position);
-    if (rows > kMixRows)
+    /* the row-group kernel only for prompt batches: at decode batches its
+     * few workgroups lose to one workgroup per (row, head group, slice)
+     * (3 rows: 40.3 against 23.1 us at a 4K cache, 8.8 against 6.2 us at
+     * 512 positions) */
+    if (rows > (int)kRecurrentStateSlots - 1)
         attn_mix_rows_kernel<<<dim3(16 * ((rows + kMixRows - 1) / kMixRows)), 64 * (kMixPairs + 1), 0, stream>>>(
             attn, scores, q_and_gate, in_stride, value_cache, context, position, rows);
     else
