@@ -76,6 +76,12 @@ WORKLOADS = {
     "q4k_wide_down_m256": (12, 5120, 17408, 256, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 256 tokens (prefill)"),
     "q4k_wide_m512": (12, 34816, 5120, 512, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 512 tokens (prefill)"),
     "iq1m_wide_m512": (29, 34816, 5120, 512, False, "IQ1_M GEMM 34816x5120 (FFN gate|up), 512 tokens (prefill)"),
+    "q4k_wide_m4096": (12, 34816, 5120, 4096, True,
+                       "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 4096 tokens (one prefill batch)"),
+    "iq1m_wide_m4096": (29, 34816, 5120, 4096, False,
+                        "IQ1_M GEMM 34816x5120 (FFN gate|up), 4096 tokens (one prefill batch)"),
+    "iq1m_wide_down_m4096": (29, 5120, 17408, 4096, False,
+                             "IQ1_M GEMM 5120x17408 (FFN down), 4096 tokens (one prefill batch)"),
 }
 # device kernel each launch of a workload runs (q38hip dispatch for that shape; the
 # trace summaries and counter profiles under profiles/ name the same kernels)

@@ -35,6 +35,8 @@
  * activation quants (at most 17 KB) are staged in LDS too, once per
  * workgroup, since every tile reads the same ones.
  */
+#include <type_traits>
+
 #include "q38_device.h"
 #include "q38_kernels.h"
 
@@ -629,64 +631,72 @@ __global__ __launch_bounds__(64 * kIQWideWaves, 1) void gemm_iq1m_wide(const uin
 #pragma unroll
             for (int j = 0; j < 4; ++j) total[rt][tt][j] = 0.0f;
 
-    WLoad wc[2] = {load_w(0, 0), load_w(1, 0)};
-
-#pragma unroll 1
-    for (int b = 0; b < NB; ++b) {
-        const int bn = b + 1 < NB ? b + 1 : b;   /* the next block's loads (the last re-reads, unused) */
+    /* E of block b for the lane's 32 (row, token) pairs: both products
+     * accumulate into one int32 per pair, the grid operand carrying 8 s g
+     * (at most 8 * 15 = 120 in magnitude) and the sign operand s (-1)^sign,
+     * so acc = 8 A.[s grid] + A.[s sign] = E exactly */
+    auto products = [&](int b, const WLoad (&c)[2], int4v (&acc)[2][4]) {
         const int par = b & 1;
-        const WLoad wn[2] = {load_w(0, bn), load_w(1, bn)};
-        if (b + 1 < NB) fetch_act(b + 1, stage_v);
-        int4v d1[2][4], d2[2][4];
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-            for (int tt = 0; tt < 4; ++tt) d1[rt][tt] = d2[rt][tt] = (int4v){0, 0, 0, 0};
+            for (int tt = 0; tt < 4; ++tt) acc[rt][tt] = (int4v){0, 0, 0, 0};
+        uint32_t scw[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) scw[rt] = (q & 2 ? c[rt].sc[1] : c[rt].sc[0]) >> (16 * (q & 1));
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
             int4v bw[2], bs[2];
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) {
-                const WLoad &c = wc[rt];
-                const uint32_t scw = (q & 2 ? c.sc[1] : c.sc[0]) >> (16 * (q & 1));   /* scale word q */
-                const uint32_t ib = (c.qs[cc >> 1] >> (16 * (cc & 1))) & 0xffffu;
-                const uint32_t hb = (c.qh >> (8 * cc)) & 0xffu;
+                const uint32_t ib = (c[rt].qs[cc >> 1] >> (16 * (cc & 1))) & 0xffffu;
+                const uint32_t hb = (c[rt].qh >> (8 * cc)) & 0xffu;
                 const uint32_t i0 = (ib & 0xffu) | ((hb & 7u) << 8);
                 const uint32_t i1 = (ib >> 8) | ((hb & 0x70u) << 4);
-                const uint32_t sv = 2u * ((scw >> (3 * cc)) & 7u) + 1u;
                 const uint2 g0 = grid_s[i0], g1 = grid_s[i1];
-                const uint32_t ns = 256u - sv;
-                const uint32_t lut = ns | (sv << 16);
+                const uint32_t t3 = (scw[rt] >> (3 * cc)) & 7u;
+                /* grid selectors 0 / 1 / 2 pick -8 s / 0 / 8 s, s = 2 t3 + 1 */
+                const uint32_t s8 = (t3 << 4) | 8u;
+                const uint32_t lut = (256u - s8) | (s8 << 16);
                 bw[rt][0] = (int)__builtin_amdgcn_perm(0u, lut, g0.x);
                 bw[rt][1] = (int)__builtin_amdgcn_perm(0u, lut, g0.y);
                 bw[rt][2] = (int)__builtin_amdgcn_perm(0u, lut, g1.x);
                 bw[rt][3] = (int)__builtin_amdgcn_perm(0u, lut, g1.y);
-                const uint32_t c0 = __builtin_amdgcn_perm(0u, (hb & 0x08u) ? ns : sv, 0u);
-                const uint32_t c1 = __builtin_amdgcn_perm(0u, (hb & 0x80u) ? ns : sv, 0u);
-                bs[rt][0] = (int)c0;
-                bs[rt][1] = (int)c0;
-                bs[rt][2] = (int)c1;
-                bs[rt][3] = (int)c1;
+                /* s and -s in every byte; the group's sign bit picks one */
+                const uint32_t pos = __builtin_amdgcn_perm(0u, (t3 << 1) | 1u, 0u);
+                const uint32_t neg = 0x01010100u - pos;
+                const uint32_t m0 = (uint32_t)((int32_t)(c[rt].qh << (28 - 8 * cc)) >> 31);
+                const uint32_t m1 = (uint32_t)((int32_t)(c[rt].qh << (24 - 8 * cc)) >> 31);
+                const int c0 = (int)((m0 & neg) | (~m0 & pos)), c1 = (int)((m1 & neg) | (~m1 & pos));
+                bs[rt] = (int4v){c0, c0, c1, c1};
             }
+            int4v a[4];
 #pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                const int4v a = act(par, tt, cc);
+            for (int tt = 0; tt < 4; ++tt) a[tt] = act(par, tt, cc);
 #pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
-                    d1[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw[rt], d1[rt][tt], 0, 0, 0);
-                    d2[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bs[rt], d2[rt][tt], 0, 0, 0);
-                }
-            }
+            for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+                    acc[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[tt], bw[rt], acc[rt][tt], 0, 0, 0);
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+                    acc[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[tt], bs[rt], acc[rt][tt], 0, 0, 0);
         }
-        /* the chains of this block */
-        float dsc[2];
+    };
+    /* the block's dscale per row tile */
+    auto dscale = [&](const WLoad (&c)[2], float (&dsc)[2]) {
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
-            const uint32_t u0 = wc[rt].sc[0] & 0xffffu, u1 = wc[rt].sc[0] >> 16, u2 = wc[rt].sc[1] & 0xffffu,
-                           u3 = wc[rt].sc[1] >> 16;
+            const uint32_t u0 = c[rt].sc[0] & 0xffffu, u1 = c[rt].sc[0] >> 16, u2 = c[rt].sc[1] & 0xffffu,
+                           u3 = c[rt].sc[1] >> 16;
             const uint32_t bits = (u0 >> 12) | ((u1 >> 8) & 0x00f0u) | ((u2 >> 4) & 0x0f00u) | (u3 & 0xf000u);
             dsc[rt] = f16_to_f32(bits);
         }
+    };
+    /* the fp32 chain step of block b */
+    auto chain = [&](int b, const int4v (&e)[2][4], const float (&dsc)[2]) {
         const float *xsb = xs_s + b * kIQWideTokens + 4 * q;
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt)
@@ -696,21 +706,307 @@ __global__ __launch_bounds__(64 * kIQWideWaves, 1) void gemm_iq1m_wide(const uin
 #pragma unroll
                 for (int rt = 0; rt < 2; ++rt) {
                     const float d = fmul_rn(dsc[rt], xsv);
-                    const float e = (float)(8 * d1[rt][tt][j] + d2[rt][tt][j]);
-                    total[rt][tt][j] = fadd_rn(total[rt][tt][j], fmul_rn(d, fmul_rn(e, 0.125f)));
+                    total[rt][tt][j] = fadd_rn(total[rt][tt][j], fmul_rn(d, fmul_rn((float)e[rt][tt][j], 0.125f)));
                 }
             }
-        wc[0] = wn[0];
-        wc[1] = wn[1];
+    };
+    /* one block: its loads one block ahead, its products, and the chain step
+     * of the block before (independent of the products, so the two
+     * interleave); with_prev false only for block 0 */
+    auto block = [&](int b, int4v (&cur)[2][4], float (&dcur)[2], const int4v (&prev)[2][4],
+                     const float (&dprev)[2], bool with_prev, const WLoad (&wc)[2], WLoad (&wn)[2]) {
+        const int bn = b + 1 < NB ? b + 1 : b;   /* the next block's loads (the last re-reads, unused) */
+        wn[0] = load_w(0, bn);
+        wn[1] = load_w(1, bn);
+        if (b + 1 < NB) fetch_act(b + 1, stage_v);
+        products(b, wc, cur);
+        dscale(wc, dcur);
+        if (with_prev) {
+            chain(b - 1, prev, dprev);
+#pragma unroll
+            for (int i = 0; i < 64; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+            }
+        }
         /* the next block's activations into the other buffer */
-        if (b + 1 < NB) store_act(par ^ 1, stage_v);
+        if (b + 1 < NB) store_act((b & 1) ^ 1, stage_v);
         __syncthreads();
+    };
+    static_assert(NB % 2 == 0, "blocks taken in pairs");
+    int4v acc0[2][4], acc1[2][4];
+    float dsc0[2], dsc1[2];
+    WLoad w0[2] = {load_w(0, 0), load_w(1, 0)}, w1[2];
+    block(0, acc0, dsc0, acc1, dsc1, false, w0, w1);
+#pragma unroll 1
+    for (int b = 1; b + 1 < NB; b += 2) {
+        block(b, acc1, dsc1, acc0, dsc0, true, w1, w0);
+        block(b + 1, acc0, dsc0, acc1, dsc1, true, w0, w1);
     }
+    block(NB - 1, acc1, dsc1, acc0, dsc0, true, w1, w0);
+    chain(NB - 1, acc1, dsc1);
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
         const uint32_t row = row0 + 16 * rt + (uint32_t)r;
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t tok = tok0 + 16 * tt + 4 * q + j;
+                if (row < rows && tok < tokens) y[(size_t)tok * ldy + row] = total[rt][tt][j];
+            }
+    }
+}
+
+/* IQ1_M x Q8_K for prompt batches of 128 tokens and more: the same E and
+ * fp32 chain as gemm_iq1m_wide, with two changes that take work off the
+ * vector ALU, which bounds that kernel.
+ *
+ * 1. The sign products.  A.[s sign] is constant over each 8-element group,
+ *    so it equals sum_g s_g sign_g A8_g with A8_g the group's activation sum
+ *    (in -1024..1016).  Split A8 = 8 h + l (h = A8 >> 3 in -128..127,
+ *    l = A8 & 7): then 8 A.[s grid] + A.[s sign] =
+ *      A.[8 s grid] + sum_g (h_g * 8 s_g sign_g + l_g * s_g sign_g),
+ *    all int8 operands (8 s <= 120), so E takes the four grid products of
+ *    the block with the B operand 8 s grid, plus ONE more K = 64 product whose
+ *    A operand holds (h_g, l_g) byte pairs for the 32 groups (staged per token
+ *    and block) and whose B operand holds (8 s_g sign_g, s_g sign_g): five
+ *    products per tile and block where gemm_iq1m_wide takes eight, and no
+ *    per-chunk sign operand.  Lane q's 16 bytes are groups 8q..8q+7, the
+ *    groups of the sub-blocks 4q..4q+3 whose scale word and high nibbles the
+ *    lane already holds; its sign word per sub-block comes from a 32-entry
+ *    LDS table indexed by (sub-scale, both group signs).
+ * 2. The chain step.  float(E) * 0.125f is exact, and d * (E / 8) equals
+ *    (d / 8) * E bit for bit whenever d / 8 = fmul(dscale / 8, xs) is exact,
+ *    i.e. unless 0 < |dscale * xs| < 2^-123; dscale >= 2^-24 (smallest
+ *    fp16), so every Q8_K scale xs of the workgroup's tokens being 0 or
+ *    >= 2^-99 in magnitude rules that out.  A workgroup checks its scales
+ *    once and runs total += fmul(dscale / 8 * xs, float(E)) (three steps
+ *    per pair and block instead of four, plus the scale product), else the
+ *    literal chain.
+ * A workgroup covers 256 rows x 128 tokens (wavefront w: rows 32w..32w+31,
+ * two row tiles, against all eight token tiles), so each decoded weight
+ * operand serves eight token tiles. */
+constexpr int kIQW2Tokens = 128, kIQW2Waves = 8;
+
+/* RT row tiles of 16 per wavefront: 128 RT rows per workgroup */
+template <int NB, int RT>
+__global__ __launch_bounds__(64 * kIQW2Waves, 1) void gemm_iq1m_wide128(const uint8_t *__restrict__ w,
+                                                                         const uint8_t *__restrict__ x,
+                                                                         float *__restrict__ y, uint32_t ldy,
+                                                                         uint32_t rows, uint32_t tokens,
+                                                                         const uint2 *__restrict__ grid)
+{
+    /* per token row: 256 quants + 16 bytes of padding / 64 (h, l) bytes +
+     * 16 bytes of padding, so the 16 tokens of one A-operand read fall on
+     * distinct banks */
+    constexpr int kActStride = 272, kA8Stride = 80;
+    __shared__ uint2 grid_s[2048];
+    __shared__ uint32_t sign_s[32];               /* entry sign_a + 16 sign_b + 2 t (t: sub-scale) */
+    __shared__ float xs_s[NB * kIQW2Tokens];      /* [block][token] */
+    __shared__ __attribute__((aligned(16))) uint8_t act_s[2][kIQW2Tokens * kActStride];
+    __shared__ __attribute__((aligned(16))) uint8_t a8_s[2][kIQW2Tokens * kA8Stride];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int r = lane & 15, q = lane >> 4;
+    const uint32_t row0 = blockIdx.x * (128 * RT) + 16 * RT * wv, tok0 = blockIdx.y * kIQW2Tokens;
+    const uint32_t wtok = tokens - tok0 < (uint32_t)kIQW2Tokens ? tokens - tok0 : kIQW2Tokens;
+
+    for (int i = threadIdx.x; i < 2048; i += 64 * kIQW2Waves) {
+        const uint2 v = grid[i];
+        grid_s[i] = make_uint2(((v.x & 0x7f7f7f7fu) + 0x01010101u) ^ (v.x & 0x80808080u),
+                               ((v.y & 0x7f7f7f7fu) + 0x01010101u) ^ (v.y & 0x80808080u));
+    }
+    if (threadIdx.x < 32) {
+        /* bytes (8 s sign_a, s sign_a, 8 s sign_b, s sign_b), s = 2 t + 1; the
+         * 32 entries sit in 32 distinct banks */
+        const uint32_t i = threadIdx.x, s = 2u * ((i >> 1) & 7u) + 1u;
+        const uint32_t pa = (i & 1u) ? ((256u - 8u * s) | ((256u - s) << 8)) : ((8u * s) | (s << 8));
+        const uint32_t pb = (i & 16u) ? ((256u - 8u * s) | ((256u - s) << 8)) : ((8u * s) | (s << 8));
+        sign_s[i] = pa | (pb << 16);
+    }
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w), 0, rows * NB * kIQ1MBytes, kRawBuf);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(x + (size_t)tok0 * NB * kQ8KBytes), 0, wtok * NB * kQ8KBytes, kRawBuf);
+    int tiny = 0;
+    for (int i = threadIdx.x; i < NB * kIQW2Tokens; i += 64 * kIQW2Waves) {
+        const int t = i % kIQW2Tokens, b = i / kIQW2Tokens;
+        const float v =
+            __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, (uint32_t)((t * NB + b) * kQ8KBytes), 0, 0));
+        xs_s[i] = v;
+        tiny |= v != 0.0f && fabsf(v) < 0x1p-99f;
+    }
+    const bool fold = !__syncthreads_or(tiny);
+
+    uint32_t woff[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) woff[rt] = (row0 + 16 * rt + (uint32_t)r) * NB * kIQ1MBytes;
+    /* staging of a block: thread i takes quants 64 (i % 4) .. + 63 of token
+     * i / 4 (tokens past the batch read as zero), i.e. groups 8 (i % 4) ..
+     * + 7, and writes their (h, l) pairs too */
+    static_assert(64 * kIQW2Waves == 4 * kIQW2Tokens, "one staging thread per 64 quants");
+    const uint32_t st_tok = threadIdx.x >> 2, st_part = threadIdx.x & 3;
+    auto fetch_act = [&](int b, int4v (&v)[4]) {
+        const uint32_t off = (st_tok * NB + (uint32_t)b) * kQ8KBytes + 4 + 64 * st_part;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16 * k, 0, 0);
+    };
+    auto store_act = [&](int par, const int4v (&v)[4]) {
+        int4v *d = reinterpret_cast<int4v *>(&act_s[par][st_tok * kActStride + 64 * st_part]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) d[k] = v[k];
+        int4v hl;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t half[2];
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const int j = 2 * k + g;   /* group j of the part: dwords 2j, 2j + 1 */
+                const int s8 = __builtin_amdgcn_sdot4(v[j >> 1][(2 * j) & 3 | 1], 0x01010101,
+                                                      dot4z(v[j >> 1][(2 * j) & 3], 0x01010101), false);
+                half[g] = ((uint32_t)s8 >> 3 & 0xffu) | (((uint32_t)s8 & 7u) << 8);
+            }
+            hl[k] = (int)(half[0] | (half[1] << 16));
+        }
+        *reinterpret_cast<int4v *>(&a8_s[par][st_tok * kA8Stride + 16 * st_part]) = hl;
+    };
+    int4v stage_v[4];
+    fetch_act(0, stage_v);
+    store_act(0, stage_v);
+    __syncthreads();
+
+    struct WLoad {
+        uint32_t qs[2], qh, sc[2];
+    };
+    auto load_w = [&](int rt, int b) {
+        WLoad c;
+        const int2v qs = __builtin_bit_cast(
+            int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff[rt] + 8 * q, b * kIQ1MBytes, 0));
+        c.qs[0] = (uint32_t)qs[0];
+        c.qs[1] = (uint32_t)qs[1];
+        c.qh = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, woff[rt] + 32 + 4 * q, b * kIQ1MBytes, 0);
+        const int2v sc = __builtin_bit_cast(
+            int2v, __builtin_amdgcn_raw_buffer_load_b64(wr, woff[rt] + 48, b * kIQ1MBytes, 0));
+        c.sc[0] = (uint32_t)sc[0];
+        c.sc[1] = (uint32_t)sc[1];
+        return c;
+    };
+
+    float total[RT][8][4];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) total[rt][tt][j] = 0.0f;
+
+    auto run = [&](auto fold_tag) {
+        constexpr bool kFold = decltype(fold_tag)::value;
+        WLoad wc[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) wc[rt] = load_w(rt, 0);
+#pragma unroll 1
+        for (int b = 0; b < NB; ++b) {
+            const int bn = b + 1 < NB ? b + 1 : b;   /* the next block's loads (the last re-reads, unused) */
+            const int par = b & 1;
+            WLoad wn[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) wn[rt] = load_w(rt, bn);
+            if (b + 1 < NB) fetch_act(b + 1, stage_v);
+            int4v acc[RT][8];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int tt = 0; tt < 8; ++tt) acc[rt][tt] = (int4v){0, 0, 0, 0};
+            uint32_t scw[RT];
+            int4v xb[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                scw[rt] = (q & 2 ? wc[rt].sc[1] : wc[rt].sc[0]) >> (16 * (q & 1));
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    /* sign bits 3 and 7 of high byte cc to bits 2 and 6: the byte offset of
+                     * entry sign_a + 16 sign_b + 2 t */
+                    const uint32_t sb = (wc[rt].qh >> (8 * cc + 1)) & 0x44u;
+                    xb[rt][cc] = (int)sign_s[(sb | (((scw[rt] >> (3 * cc)) & 7u) << 3)) >> 2];
+                }
+            }
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                int4v bw[RT];
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const WLoad &c = wc[rt];
+                    const uint32_t ib = (c.qs[cc >> 1] >> (16 * (cc & 1))) & 0xffffu;
+                    const uint32_t hb = (c.qh >> (8 * cc)) & 0xffu;
+                    const uint32_t i0 = (ib & 0xffu) | ((hb & 7u) << 8);
+                    const uint32_t i1 = (ib >> 8) | ((hb & 0x70u) << 4);
+                    const uint2 g0 = grid_s[i0], g1 = grid_s[i1];
+                    /* grid selectors 0 / 1 / 2 pick -8 s / 0 / 8 s, s = 2 t + 1 */
+                    const uint32_t s8 = (((scw[rt] >> (3 * cc)) & 7u) << 4) | 8u;
+                    const uint32_t lut = (256u - s8) | (s8 << 16);
+                    bw[rt][0] = (int)__builtin_amdgcn_perm(0u, lut, g0.x);
+                    bw[rt][1] = (int)__builtin_amdgcn_perm(0u, lut, g0.y);
+                    bw[rt][2] = (int)__builtin_amdgcn_perm(0u, lut, g1.x);
+                    bw[rt][3] = (int)__builtin_amdgcn_perm(0u, lut, g1.y);
+                }
+#pragma unroll
+                for (int tt = 0; tt < 8; ++tt) {
+                    const int4v a = *reinterpret_cast<const int4v *>(
+                        &act_s[par][(16 * tt + r) * kActStride + 64 * q + 16 * cc]);
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+                        acc[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw[rt], acc[rt][tt], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) {
+                const int4v a = *reinterpret_cast<const int4v *>(&a8_s[par][(16 * tt + r) * kA8Stride + 16 * q]);
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+                    acc[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, xb[rt], acc[rt][tt], 0, 0, 0);
+            }
+            /* the chain step of this block */
+            float dsc[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const uint32_t u0 = wc[rt].sc[0] & 0xffffu, u1 = wc[rt].sc[0] >> 16, u2 = wc[rt].sc[1] & 0xffffu,
+                               u3 = wc[rt].sc[1] >> 16;
+                const uint32_t bits =
+                    (u0 >> 12) | ((u1 >> 8) & 0x00f0u) | ((u2 >> 4) & 0x0f00u) | (u3 & 0xf000u);
+                dsc[rt] = kFold ? f16_to_f32(bits) * 0.125f : f16_to_f32(bits);   /* exact */
+            }
+            const float *xsb = xs_s + b * kIQW2Tokens + 4 * q;
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float xsv = xsb[16 * tt + j];
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        const float d = fmul_rn(dsc[rt], xsv);
+                        const float e = (float)acc[rt][tt][j];
+                        total[rt][tt][j] =
+                            fadd_rn(total[rt][tt][j], kFold ? fmul_rn(d, e) : fmul_rn(d, fmul_rn(e, 0.125f)));
+                    }
+                }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) wc[rt] = wn[rt];
+            /* the next block's activations into the other buffer */
+            if (b + 1 < NB) store_act(par ^ 1, stage_v);
+            __syncthreads();
+        }
+    };
+    if (fold)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const uint32_t row = row0 + 16 * rt + (uint32_t)r;
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t tok = tok0 + 16 * tt + 4 * q + j;
@@ -729,6 +1025,22 @@ bool launch_iq1m_wide_nb(const uint8_t *w, const uint8_t *x, float *y, uint32_t 
                        dim3(64 * kIQWideWaves), 0, stream, w, x, y, ldy, rows, tokens, grid);
     return hipGetLastError() == hipSuccess;
 }
+
+template <int NB>
+bool launch_iq1m_wide128_nb(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                            uint32_t tokens, const uint2 *grid, hipStream_t stream)
+{
+    /* 256-row workgroups also where 128-row ones would fill the chip better
+     * (the 5120-row down projection at 4096 tokens: 640 workgroups take
+     * 916 us, 1280 of 128 rows 1119 us, each of those reading its activation
+     * operands for half as many rows) */
+    hipLaunchKernelGGL((gemm_iq1m_wide128<NB, 2>), dim3((rows + 255) / 256, (tokens + kIQW2Tokens - 1) / kIQW2Tokens),
+                       dim3(64 * kIQW2Waves), 0, stream, w, x, y, ldy, rows, tokens, grid);
+    return hipGetLastError() == hipSuccess;
+}
+
+/* batches from this size on take the 128-token tiles */
+constexpr uint32_t kIQW2MinTokens = 128;
 }  // namespace
 
 bool launch_gemm_iq1m_wide(uint32_t tokens, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
@@ -736,6 +1048,13 @@ bool launch_gemm_iq1m_wide(uint32_t tokens, const uint8_t *w, const uint8_t *x, 
 {
     if (!rows || !tokens || ldy < rows || !grid || tokens > 65535u * kIQWideTokens) return false;
     const uint2 *g = static_cast<const uint2 *>(grid);
+    if (tokens >= kIQW2MinTokens) switch (nb) {
+        case 20: return launch_iq1m_wide128_nb<20>(w, x, y, ldy, rows, tokens, g, stream);
+        case 24: return launch_iq1m_wide128_nb<24>(w, x, y, ldy, rows, tokens, g, stream);
+        case 40: return launch_iq1m_wide128_nb<40>(w, x, y, ldy, rows, tokens, g, stream);
+        case 68: return launch_iq1m_wide128_nb<68>(w, x, y, ldy, rows, tokens, g, stream);
+        default: return false;
+        }
     switch (nb) {
     case 20: return launch_iq1m_wide_nb<20>(w, x, y, ldy, rows, tokens, g, stream);
     case 24: return launch_iq1m_wide_nb<24>(w, x, y, ldy, rows, tokens, g, stream);

@@ -320,20 +320,58 @@ def test_wide_gemm_full_shapes_match_decode_kernels(hip, device, rows, width):
 
 @pytest.mark.parametrize("rows,width", [(300, 5120), (40, 17408), (520, 6144)])
 def test_iq1m_wide_gemm_prefill_batches_bit_exact(hip, oracle, device, rows, width):
-    """IQ1_M prefill batches (9 tokens and more, 256 x 64 matrix-core tiles):
-    every token's row equals the oracle's one-token GEMV bit for bit, with a
-    row count that ends inside a wavefront's 32 rows and token counts that
-    end inside a 64-token tile."""
+    """IQ1_M prefill batches (9 tokens and more: 256 x 64 matrix-core tiles,
+    from 128 tokens on 256 x 128 tiles): every token's row equals the
+    oracle's one-token GEMV bit for bit, with a row count that ends inside a
+    wavefront's 32 rows and token counts that end inside a token tile."""
     w = synth.matrix(IQ1_M, rows, width, seed=rows * 5 + width)
-    x = synth.activations(width, seed=rows + 2 * width, count=100)
+    x = synth.activations(width, seed=rows + 2 * width, count=200)
     q = oracle.quantize(x.reshape(-1))
     nb = width // 256
     wd = to_dev(w, device)
     xq = hip.quantize_q8_k(to_dev(x, device))
-    want = oracle.gemm(IQ1_M, w, rows, q, 100)
-    for m in (9, 16, 33, 64, 100):
+    want = oracle.gemm(IQ1_M, w, rows, q, 200)
+    for m in (9, 16, 33, 64, 100, 128, 200):
         got = hip.gemm_q8_k(wd, IQ1_M, width, rows, xq[:m * nb * 292], m).cpu().numpy()
         assert np.array_equal(bits(got), bits(want[:m])), "M=%d" % m
+
+
+@pytest.mark.parametrize("rows,width,m", [(34744, 5120, 1100), (5120, 17408, 4096)])
+def test_iq1m_wide_gemm_large_batches_bit_exact(hip, oracle, device, rows, width, m):
+    """Prompt batches large enough for the 256-row workgroups (gate|up, a
+    ragged last row group and token tile) and a full 4096-token down
+    projection on the 128-row ones: token windows equal the 8-token kernel
+    on the same activations, and the first window the oracle."""
+    w = synth.matrix(IQ1_M, rows, width, seed=rows + 21)
+    wd = to_dev(w, device)
+    x = synth.activations(width, seed=width + 23, count=m)
+    xq = hip.quantize_q8_k(to_dev(x, device))
+    got = hip.gemm_q8_k(wd, IQ1_M, width, rows, xq, m).cpu().numpy()
+    nb = width // 256
+    for t0 in (0, 8, 640, m - 8):
+        want = hip.gemm_q8_k(wd, IQ1_M, width, rows, xq[t0 * nb * 292:(t0 + 8) * nb * 292], 8).cpu().numpy()
+        assert np.array_equal(bits(got[t0:t0 + 8]), bits(want)), (rows, width, t0)
+    q = oracle.quantize(x[:8].reshape(-1))
+    assert np.array_equal(bits(got[:8]), bits(oracle.gemm(IQ1_M, w, rows, q, 8)))
+
+
+def test_iq1m_wide_gemm_tiny_scales_bit_exact(hip, oracle, device):
+    """Tokens whose Q8_K scales are below 2^-99 (activations near 1e-30) or
+    zero: a 128-token tile holding one runs the literal chain
+    d * (E * 0.125f), the others the folded one; both equal the oracle bit
+    for bit."""
+    rows, width, m = 264, 5120, 256
+    w = synth.matrix(IQ1_M, rows, width, seed=77)
+    x = synth.activations(width, seed=78, count=m).reshape(m, width).copy()
+    x[5] *= np.float32(1e-33)       # scales near 3e-35: the first tile's chain is the literal one
+    x[140] = 0.0                    # zero scale: the second tile folds
+    x[141] *= np.float32(1e-20)
+    q = oracle.quantize(x.reshape(-1))
+    xq = hip.quantize_q8_k(to_dev(x, device))
+    assert np.array_equal(xq.cpu().numpy(), q.view(np.uint8)), "quantized activations differ"
+    want = oracle.gemm(IQ1_M, w, rows, q, m)
+    got = hip.gemm_q8_k(to_dev(w, device), IQ1_M, width, rows, xq, m).cpu().numpy()
+    assert np.array_equal(bits(got), bits(want))
 
 
 @pytest.mark.parametrize("rows,width", [(34816, 5120), (5120, 17408)])
