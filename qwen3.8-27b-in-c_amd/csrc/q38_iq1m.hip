@@ -527,12 +527,15 @@ bool launch_iq1m_dot4(const uint8_t *w, const uint8_t *x, float *y, uint32_t row
 
 }  // namespace
 
-/* IQ1_M x Q8_K for prefill batches (any token count): the products of
- * gemm_iq1m_mfma (per 16-row x 16-token tile and 64-element chunk,
- * E = 8 * A.[s grid] + A.[s sign] on v_mfma_i32_16x16x64_i8, the lane
- * (r, q) taking sub-block 4q + c of the chunk c) with the fp32 chain
- * total += d * (float(E) * 0.125f), d = dscale * xs, in block order per
- * (row, token) in registers.  A workgroup of 8 wavefronts covers 256 rows x
+/* IQ1_M x Q8_K for prefill batches of 9..127 tokens: the products of
+ * gemm_iq1m_mfma (per 16-row x 16-token tile and 64-element chunk on
+ * v_mfma_i32_16x16x64_i8, the lane (r, q) taking sub-block 4q + c of the
+ * chunk c), both into one int32 per (row, token) -- the grid operand carries
+ * 8 s grid (at most 120 in magnitude), the sign operand s sign, so the sum is
+ * E itself -- with the fp32 chain total += d * (float(E) * 0.125f),
+ * d = dscale * xs, in block order per (row, token) in registers.  The chain
+ * step of block b runs while block b + 1's products do (two accumulator
+ * sets).  A workgroup of 8 wavefronts covers 256 rows x
  * 64 tokens: wavefront w takes rows 32w .. 32w + 31 (two 16-row tiles)
  * against all 64 tokens (four token tiles), so each decoded weight operand
  * serves four token tiles and each activation operand two row tiles.  Lane
