@@ -719,9 +719,10 @@ def run_decode(torch, args):
         result["verify_block"] = verify_block_measure(torch)
         c5 = decode_measure(torch, "iq1m", 4096, 1024, args.draft, warmup=8, fixture=decode_fixture("iq1m"))
         c5["workload"] = ("27B IQ1_M layout (IQ1_M layer matrices, Q4_K embedding, Q6_K LM head): a 4096-token "
-                          "prompt prefilled in 512-token batches on the matrix cores, then 1024 tokens decoded with "
+                          "prompt prefilled as one 4096-token batch on the matrix cores, then 1024 tokens decoded with "
                           "MTP k=%d (context 4097-5120)" % args.draft)
-        c5["prefill_mfma_busy"] = {w: committed_mfma(w) for w in ("iq1m_wide_m512", "q4k_wide_m512")}
+        c5["prefill_mfma_busy"] = {w: committed_mfma(w) for w in ("iq1m_wide_m4096", "iq1m_wide_m512",
+                                                                   "q4k_wide_m512")}
         c5["cpu_baseline"] = None if args.no_cpu else cpu_decode_baseline(args, "IQ1_M", layout="iq1m", prompt=128,
                                                                            seconds=10.0)
         result["iq1m_prefill_decode"] = c5
