@@ -594,6 +594,8 @@ constexpr int kScoreChunk = 64;
 /* q heads per lane in the score kernel (more heads: fewer wavefronts, more
  * independent chains per lane) */
 constexpr int kScoreHeadsPerLane = 6;
+/* rows per workgroup of the prompt-batch scores kernel */
+constexpr int kScoreRows = 8;
 constexpr int kMaxLdsPositions = 32768;   /* softmax weights kept in LDS up to this many positions */
 constexpr int kAttnLoadBatch = 32;        /* softmax weights read ahead of the denominator's adds */
 constexpr int kSoftmaxPad = 64;           /* LDS floats past the context in the softmax kernel */
@@ -713,6 +715,68 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(float *__restrict__ sco
     if (p >= n) return;
     for (int j = 0; j < HPL; ++j)
         scores[((size_t)t * kAttnHeads + h0 + j) * context + p] = __fmul_rn(acc[j], 0.0625f);
+}
+
+/* Attention scores of a prompt batch: T rows x 64 positions x the six q
+ * heads of one KV head per workgroup, the same fmaf chain over the 256 dims
+ * in order per (row, head, position) as attn_scores_kernel.  Each lane
+ * takes its key row 16 dims at a time and runs them against all T rows, so a
+ * key chunk is read once per T rows instead of once per row; the q values
+ * are wave-uniform and come in through scalar loads (no LDS operand per
+ * multiply-add).  Same XCD placement as attn_scores_kernel; workgroups
+ * whose chunk starts past the tile's last visible position exit at once. */
+template <int T>
+__global__ __launch_bounds__(64) void attn_scores_rows_kernel(float *__restrict__ scores, const float *__restrict__ q,
+                                                              const float *__restrict__ key_cache, int context,
+                                                              const uint32_t *__restrict__ position_ptr, int rows)
+{
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, lane = threadIdx.x;
+    const int half_chunks = ((context + kScoreChunk - 1) / kScoreChunk + 1) / 2;
+    const int kvh = xcd >> 1;
+    const int chunk = 2 * (slot % half_chunks) + (xcd & 1);
+    const int t0 = (slot / half_chunks) * T;
+    const int pos0 = (int)*position_ptr;
+    const int tlast = (t0 + T < rows ? t0 + T : rows) - 1;
+    const int nmax = pos0 + tlast + 1;   /* positions the tile's last row sees */
+    if (t0 >= rows || chunk * kScoreChunk >= nmax) return;
+    const int p = chunk * kScoreChunk + lane;
+    const float4 *k4 =
+        reinterpret_cast<const float4 *>(key_cache + (size_t)(p < nmax ? p : nmax - 1) * kKVDim + kvh * kAttnDim);
+    float acc[T][6];
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+        for (int j = 0; j < 6; ++j) acc[tt][j] = 0.0f;
+    /* rows past the batch run on the last row's q and store nothing */
+    const float *qrow[T];
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt)
+        qrow[tt] = q + (size_t)(t0 + tt < rows ? t0 + tt : rows - 1) * kQDim + kvh * 6 * kAttnDim;
+    /* the chains run over d in order, 16 dims per step */
+#pragma unroll 1
+    for (int d0 = 0; d0 < kAttnDim; d0 += 16) {
+        float4 kk[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) kk[m] = k4[d0 / 4 + m];
+        const float kv[16] = {kk[0].x, kk[0].y, kk[0].z, kk[0].w, kk[1].x, kk[1].y, kk[1].z, kk[1].w,
+                              kk[2].x, kk[2].y, kk[2].z, kk[2].w, kk[3].x, kk[3].y, kk[3].z, kk[3].w};
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+            for (int j = 0; j < 6; ++j) {
+                const float *qd = qrow[tt] + j * kAttnDim + d0;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[tt][j] = __builtin_fmaf(qd[e], kv[e], acc[tt][j]);
+            }
+    }
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) {
+        const int t = t0 + tt;
+        if (t >= rows || p >= pos0 + t + 1) continue;
+#pragma unroll
+        for (int j = 0; j < 6; ++j)
+            scores[((size_t)t * kAttnHeads + kvh * 6 + j) * context + p] = __fmul_rn(acc[tt][j], 0.0625f);
+    }
 }
 
 /* Softmax of q head blockIdx.x of row blockIdx.y (qwen38_model.c:863-876):
@@ -1066,103 +1130,84 @@ __global__ __launch_bounds__(128) void attn_mix_kernel(float *__restrict__ out, 
     out[(size_t)t * kQDim + dim] = __fmul_rn(o, sigmoidf_exact(g));
 }
 
-/* attn_mix_kernel for prompt batches: one workgroup per (KV head, 64-channel
- * slice, group of kMixRows rows) streams the slice's value rows once for the
- * 6 q heads of the KV head and the group's rows: wavefront w < 6 kMixRows
- * runs the chains of (row w / 6, q head w % 6), each exactly as the chain
- * wavefront of attn_mix_kernel over its own positions 0 .. n_row - 1, and
- * the last wavefront streams the value chunks up to the group's last row
- * and every pair's probabilities into the ring (a slot holds the chunk's
- * values, then the pairs' probability records of kMixChunk floats).  A
- * chain wavefront whose row has fewer chunks ends after its last barrier
- * (an ended wavefront no longer takes part in the workgroup's barriers);
- * wavefronts of rows past the batch end at once.  Workgroups go to the XCDs
- * as in attn_mix_kernel. */
-constexpr int kMixRows = 2;
-constexpr int kMixPairs = 6 * kMixRows;
-constexpr int kMixRowsSlotBytes = kMixChunk * 256 + kMixPairs * kMixChunk * 4;
-constexpr int kMixProbOps = kMixPairs * kMixChunk / 64;   /* probability loads per chunk */
-constexpr int kMixRowsOps = kMixVOps + kMixProbOps;
-/* chunks loaded ahead: every load of kMixRowsAhead chunks in flight fits the
- * vmcnt range; the ring keeps its kMixSlots slots (the chains' slot
- * arithmetic), of which chunks c - 1 .. c + kMixRowsAhead are in use */
-constexpr int kMixRowsAhead = 4;
-static_assert(kMixRowsOps * kMixRowsAhead <= 63 && kMixRowsAhead + 2 <= kMixSlots,
-              "loads in flight within the vmcnt range");
+/* rows per workgroup of attn_mix_tile_kernel */
+constexpr int kMixTileRows = 4;
 
-__global__ __launch_bounds__(64 * (kMixPairs + 1)) void attn_mix_rows_kernel(
-    float *__restrict__ out, const float *__restrict__ prob, const float *__restrict__ q_and_gate,
-    long long qg_stride, const float *__restrict__ value_cache, int context, const uint32_t *__restrict__ position_ptr,
-    int rows)
+/* attn_mix_kernel for prompt batches, register form: one 64-lane workgroup
+ * per (KV head, 64-channel slice, R rows); lane = channel, and the lane runs
+ * the 6 q heads x R rows of its channel as 6 R chains o = fmaf(prob, v, o)
+ * over positions 0 .. n_row - 1 in order (the chain of attn_mix_kernel).
+ * Each value is loaded once into a register and serves all 6 R chains; the
+ * probabilities are wave-uniform and come in through scalar loads, 16
+ * positions at a time while every row of the tile is still inside its
+ * positions, then position by position to each row's end.  Tiles of later
+ * rows (longer chains) are dispatched first. */
+template <int R>
+__global__ __launch_bounds__(64) void attn_mix_tile_kernel(float *__restrict__ out, const float *__restrict__ prob,
+                                                           const float *__restrict__ q_and_gate, long long qg_stride,
+                                                           const float *__restrict__ value_cache, int context,
+                                                           const uint32_t *__restrict__ position_ptr, int rows)
 {
-    __shared__ __attribute__((aligned(16))) uint8_t ring[kMixSlots * kMixRowsSlotBytes];
-    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3, lane = threadIdx.x & 63;
+    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3, lane = threadIdx.x;
     const int kvh = xcd >> 1, slice = 2 * (xcd & 1) + (j & 1);
-    const int t0 = (j >> 1) * kMixRows;
-    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int tiles = (rows + R - 1) / R;
+    const int t0 = (tiles - 1 - (j >> 1)) * R;
+    if (t0 < 0) return;
     const int pos0 = (int)*position_ptr;
-    const int group_rows = rows - t0 < kMixRows ? rows - t0 : kMixRows;
-    const uint32_t pitch4 = value_pitch((uint32_t)context) * 4u;
-    if (wave == kMixPairs) {
-        /* streaming wavefront: chunks of positions 0 .. n_max - 1 */
-        const int n_max = pos0 + t0 + group_rows;
-        const int chunks = (n_max + kMixChunk - 1) / kMixChunk, last = chunks - 1;
-        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float *>(value_cache), 0, (int)(kKVDim * pitch4), kMixRawBuffer);
-        /* the probabilities of the group's rows; pairs of rows past the batch read as zero */
-        const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float *>(prob + (size_t)t0 * kAttnHeads * context), 0,
-            group_rows * kAttnHeads * context * 4, kMixRawBuffer);
-        uint32_t v_lane[kMixVOps];
+    const int nr = rows - t0 < R ? rows - t0 : R;
+    const int nmin = pos0 + t0 + 1, nmax = pos0 + t0 + nr;
+    const float *vrow = value_cache + (size_t)(kvh * kAttnDim + 64 * slice + lane) * value_pitch((uint32_t)context);
+    /* probability rows of (row t0 + tt, head kvh * 6 + jh): prow[tt] + jh *
+     * context; rows past the batch read row t0 and store nothing */
+    const float *prow[R];
 #pragma unroll
-        for (int jj = 0; jj < kMixVOps; ++jj)
-            v_lane[jj] = (uint32_t)(kvh * kAttnDim + 64 * slice + 8 * jj + (lane >> 3)) * pitch4 +
-                         16u * (uint32_t)((lane & 7) ^ ((lane >> 3) & 7) ^ (jj & 1));
-        /* probability load k, lane i: float 64 k + i of the slot's records =
-         * pair (64 k + i) / 32, position (64 k + i) % 32 of the chunk */
-        uint32_t p_lane[kMixProbOps];
+    for (int tt = 0; tt < R; ++tt)
+        prow[tt] = prob + ((size_t)(t0 + (tt < nr ? tt : 0)) * kAttnHeads + kvh * 6) * context;
+    float acc[R][6];
 #pragma unroll
-        for (int k = 0; k < kMixProbOps; ++k) {
-            const int f = 64 * k + lane, pair = f / kMixChunk, pos = f % kMixChunk;
-            const int tt = pair / 6, hh = pair % 6;
-            p_lane[k] = (uint32_t)(((tt * kAttnHeads + kvh * 6 + hh) * context + pos) * 4);
-        }
-        const uint32_t ring_base = __builtin_amdgcn_readfirstlane(lds_address(ring));
-        auto load_chunk = [&](int c, uint32_t slot) {
-            const uint32_t chunk_off = (uint32_t)(c < last ? c : last) * (kMixChunk * 4);
+    for (int tt = 0; tt < R; ++tt)
 #pragma unroll
-            for (int jj = 0; jj < kMixVOps; ++jj)
-                asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, %3 offen lds"
-                             :: "v"(v_lane[jj]), "s"(slot + 1024 * jj), "s"(vr), "s"(chunk_off) : "memory", "m0");
-            /* the chunk offset goes into the range-checked lane offset */
-#pragma unroll
-            for (int k = 0; k < kMixProbOps; ++k)
-                asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, 0 offen lds"
-                             :: "v"(p_lane[k] + (uint32_t)c * (kMixChunk * 4)),
-                                "s"(slot + kMixChunk * 256 + 256 * k), "s"(pr)
-                             : "memory", "m0");
-        };
-#pragma unroll
-        for (int c = 0; c < kMixRowsAhead; ++c) load_chunk(c, ring_base + c * kMixRowsSlotBytes);
-        mix_wait_vmcnt<kMixRowsOps * (kMixRowsAhead - 1)>();   /* chunk 0 */
-        mix_barrier();
+        for (int jh = 0; jh < 6; ++jh) acc[tt][jh] = 0.0f;
+    int p0 = 0;
 #pragma unroll 1
-        for (int c = 0; c < chunks; ++c) {
-            mix_wait_vmcnt<kMixRowsOps * (kMixRowsAhead - 2)>();   /* chunk c + 1 */
-            mix_barrier();
-            /* chunk c - 1 is consumed; the slot of chunk c + kMixRowsAhead is free */
-            load_chunk(c + kMixRowsAhead, ring_base + ((c + kMixRowsAhead) % kMixSlots) * kMixRowsSlotBytes);
-        }
-        mix_wait_vmcnt<0>();
-        return;
+    for (; p0 + 16 <= nmin; p0 += 16) {
+        float4 v4[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) v4[m] = reinterpret_cast<const float4 *>(vrow + p0)[m];
+        const float v[16] = {v4[0].x, v4[0].y, v4[0].z, v4[0].w, v4[1].x, v4[1].y, v4[1].z, v4[1].w,
+                             v4[2].x, v4[2].y, v4[2].z, v4[2].w, v4[3].x, v4[3].y, v4[3].z, v4[3].w};
+#pragma unroll
+        for (int tt = 0; tt < R; ++tt)
+#pragma unroll
+            for (int jh = 0; jh < 6; ++jh) {
+                const float *pp = prow[tt] + (size_t)jh * context + p0;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[tt][jh] = __builtin_fmaf(pp[e], v[e], acc[tt][jh]);
+            }
     }
-    const int tt = wave / 6, hh = wave % 6;
-    if (tt >= group_rows) return;
-    const int t = t0 + tt, h = kvh * 6 + hh;
-    const float o = mix_chain(ring, kMixRowsSlotBytes, pos0 + t + 1, lane, wave);
-    const int dim = h * kAttnDim + 64 * slice + lane;
-    const float g = q_and_gate[(size_t)t * qg_stride + h * 2 * kAttnDim + kAttnDim + 64 * slice + lane];
-    out[(size_t)t * kQDim + dim] = __fmul_rn(o, sigmoidf_exact(g));
+    /* the last positions, each row up to its own end */
+#pragma unroll 1
+    for (; p0 < nmax; ++p0) {
+        const float v = vrow[p0];
+#pragma unroll
+        for (int tt = 0; tt < R; ++tt) {
+            if (tt >= nr || p0 >= nmin + tt) continue;
+#pragma unroll
+            for (int jh = 0; jh < 6; ++jh) acc[tt][jh] = __builtin_fmaf(prow[tt][(size_t)jh * context + p0], v,
+                                                                        acc[tt][jh]);
+        }
+    }
+#pragma unroll
+    for (int tt = 0; tt < R; ++tt) {
+        if (tt >= nr) break;
+        const int t = t0 + tt;
+#pragma unroll
+        for (int jh = 0; jh < 6; ++jh) {
+            const int h = kvh * 6 + jh;
+            const float g = q_and_gate[(size_t)t * qg_stride + h * 2 * kAttnDim + kAttnDim + 64 * slice + lane];
+            out[(size_t)t * kQDim + h * kAttnDim + 64 * slice + lane] = __fmul_rn(acc[tt][jh], sigmoidf_exact(g));
+        }
+    }
 }
 
 /* ---- launchers ----------------------------------------------------------- */
@@ -1288,9 +1333,13 @@ void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_
         (int)value_pitch((uint32_t)context), position, 0);
     {
         const int half_chunks = ((context + kScoreChunk - 1) / kScoreChunk + 1) / 2;
-        attn_scores_kernel<kScoreHeadsPerLane>
-            <<<dim3(8 * (6 / kScoreHeadsPerLane) * half_chunks * rows), 64, 0, stream>>>(scores, q_buf, key_cache,
-                                                                                        context, position);
+        if (rows > (int)kRecurrentStateSlots - 1)
+            attn_scores_rows_kernel<kScoreRows><<<dim3(8 * half_chunks * ((rows + kScoreRows - 1) / kScoreRows)), 64, 0,
+                                                  stream>>>(scores, q_buf, key_cache, context, position, rows);
+        else
+            attn_scores_kernel<kScoreHeadsPerLane>
+                <<<dim3(8 * (6 / kScoreHeadsPerLane) * half_chunks * rows), 64, 0, stream>>>(scores, q_buf, key_cache,
+                                                                                            context, position);
     }
     if (context <= kMaxLdsPositions)
         attn_softmax_kernel<true><<<dim3(kAttnHeads, rows), 256, (size_t)(context + kSoftmaxPad) * 4, stream>>>(scores, context,
@@ -1302,7 +1351,7 @@ void launch_attention(float *attn, uint8_t *q_out, float *q_buf, const float *q_
      * (3 rows: 40.3 against 23.1 us at a 4K cache, 8.8 against 6.2 us at
      * 512 positions) */
     if (rows > (int)kRecurrentStateSlots - 1)
-        attn_mix_rows_kernel<<<dim3(16 * ((rows + kMixRows - 1) / kMixRows)), 64 * (kMixPairs + 1), 0, stream>>>(
+        attn_mix_tile_kernel<kMixTileRows><<<dim3(16 * ((rows + kMixTileRows - 1) / kMixTileRows)), 64, 0, stream>>>(
             attn, scores, q_and_gate, in_stride, value_cache, context, position, rows);
     else
         attn_mix_kernel<<<dim3(8 * 12 * rows), 128, 0, stream>>>(attn, scores, q_and_gate, in_stride, value_cache,

@@ -7,7 +7,9 @@ Bar: bit-identical outputs, K/V cache rows and Q8_K blocks of the output.
 Cases: the 2048-token cache of a verify block with M = 1..5 rows (the last
 row at position 2047), a 5124-token cache with 5 rows at positions
 4096-4100 and 5119-5123, contexts of 1..66 positions around the 32-position
-chunks of the value stream, a 12-row prefill batch, a 16384-token cache,
+chunks of the value stream, prefill batches of 9-130 rows (8-row score
+tiles, a ragged last tile, batches starting at position 0, a context that
+is not a multiple of four floats), a 16384-token cache,
 and a context above 32768 positions, where the softmax weights stay in the
 scores buffer instead of LDS.  Cache rows past the last row's position hold
 NaN, so a kernel that read them would fail the comparison."""
@@ -30,6 +32,10 @@ CASES = [
     (5124, 4096, 5),
     (5124, 5119, 5),
     (700, 600, 12),
+    (160, 100, 9),
+    (300, 0, 64),
+    (1100, 37, 130),
+    (203, 150, 11),
     (40, 0, 2),
     (80, 30, 4),
     (80, 62, 4),
