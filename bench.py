@@ -69,6 +69,9 @@ WORKLOADS = {
     "q4k_tiled_out_m3": (12, 5120, 6144, 3, True,
                          "Q4_K tiled GEMM 5120x6144 (attention output / DeltaNet output), 3 tokens"),
     "iq1m_gemm_m3": (29, 34816, 5120, 3, True, "IQ1_M GEMM 34816x5120 (FFN gate|up), 3 tokens"),
+    "iq1m_gemm_down_m3": (29, 5120, 17408, 3, True, "IQ1_M GEMM 5120x17408 (FFN down), 3 tokens"),
+    "iq1m_gemm_out_m3": (29, 5120, 6144, 3, True,
+                         "IQ1_M GEMM 5120x6144 (attention output / DeltaNet output), 3 tokens"),
     "q4k_tiled_m8": (12, 34816, 5120, 8, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
     "iq1m_gemm_m8": (29, 34816, 5120, 8, True, "IQ1_M GEMM 34816x5120 (FFN gate|up), 8 tokens (prefill batch)"),
     "q4k_wide_m256": (12, 34816, 5120, 256, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 256 tokens (prefill)"),
@@ -88,12 +91,14 @@ WORKLOADS = {
 DEVICE_KERNEL = {
     "q4k_gemv": "gemv_q4k_lanes<20, 4, 1>",
     "q4k_gemv_t": "gemv_q4k_lanes<68, 12, 1>",
-    "iq1m_gemv": "gemm_iq1m_dot4<20, 15, 2>",
-    "iq1m_gemv_t": "gemm_iq1m_dot4<68, 16, 2>",
+    "iq1m_gemv": "gemm_iq1m_dot4<20, 15, 2, 1>",
+    "iq1m_gemv_t": "gemm_iq1m_dot4<68, 16, 2, 1>",
     "q4k_tiled_m3": "gemm_q4k_mm16<3, 20, 9, 4, 1>",
     "q4k_tiled_down_m3": "gemm_q4k_t32r<3, 68, 8, 1>",
     "q4k_tiled_out_m3": "gemm_q4k_t32r<3, 24, 8, 1>",
-    "iq1m_gemm_m3": "gemm_iq1m_mfma<3, 20, 4, 2, true>",
+    "iq1m_gemm_m3": "gemm_iq1m_dot4<20, 15, 2, 3>",
+    "iq1m_gemm_down_m3": "gemm_iq1m_dot4<68, 16, 2, 3>",
+    "iq1m_gemm_out_m3": "gemm_iq1m_dot4<24, 12, 2, 3>",
 }
 # dense matrix-core peaks of MI355X, TOP/s: the Q4_K GEMM runs fp16 MFMA, IQ1_M int8
 MFMA_PEAK_TOPS = {12: ("f16", 2500.0), 29: ("i8", 5000.0)}

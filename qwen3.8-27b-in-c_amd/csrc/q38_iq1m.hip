@@ -311,7 +311,14 @@ bool launch_iq1m_nb(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_
  * issue order, so after the staging wait and one barrier an item's wait
  * only counts the items issued after it. */
 constexpr uint32_t kDot4Groups = 256;   /* persistent workgroups: one per CU */
-constexpr int kDot4TFloats = 6144;      /* LDS terms [quad][block][row % 4] */
+constexpr int kDot4TFloats = 6144;      /* LDS terms [quad][block][row % 4], one token */
+/* LDS terms for MT tokens: 34816 x 20-block matrices put 34 quads on a
+ * workgroup, 34 x 20 x 4 x 3 = 8160 terms */
+template <int MT>
+constexpr int dot4_t_floats()
+{
+    return MT == 1 ? kDot4TFloats : 8192;
+}
 constexpr int kDot4ActStride = 272;     /* activation quants per block in LDS (256 + 16: no bank aliasing) */
 constexpr int kDot4Slot = 896;          /* LDS ring slot: one item */
 
@@ -359,19 +366,20 @@ __device__ __forceinline__ void dot4_wait_vm_upto(int c)
 
 }  // namespace
 
-template <int NB, int S, int P>
+template <int NB, int S, int P, int MT>
 __global__ __launch_bounds__(64 * S) void gemm_iq1m_dot4(const uint8_t *__restrict__ w, const uint8_t *__restrict__ x,
-                                                         float *__restrict__ y, uint32_t rows,
+                                                         float *__restrict__ y, uint32_t ldy, uint32_t rows,
                                                          const uint2 *__restrict__ grid)
 {
+    static_assert(MT >= 1 && MT <= 3, "1..3 tokens");
     constexpr int NG = NB / 4;              /* block groups */
     constexpr bool ACT_REG = S % NG == 0;   /* fixed block group per wavefront */
     static_assert(NB % 4 == 0, "blocks per row must be a multiple of 4");
     static_assert(P >= 1 && P <= 4, "1..4 items in flight");
     __shared__ __attribute__((aligned(16))) uint2 cb_s[4096];
-    __shared__ __attribute__((aligned(16))) uint8_t act_s[NB * kDot4ActStride];
-    __shared__ float xs_s[NB > 64 ? 128 : 64];
-    __shared__ float t_s[kDot4TFloats];
+    __shared__ __attribute__((aligned(16))) uint8_t act_s[MT * NB * kDot4ActStride];   /* [token][block] */
+    __shared__ float xs_s[MT * NB > 64 ? (MT * NB > 128 ? 256 : 128) : 64];            /* [token][block] */
+    __shared__ float t_s[dot4_t_floats<MT>()];                                         /* [quad][block][row % 4][token] */
     __shared__ __attribute__((aligned(16))) uint8_t ring_s[S * P * kDot4Slot];
 
     const uint32_t nquads = (rows + 3) / 4;
@@ -386,16 +394,18 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_dot4(const uint8_t *__restri
     const int mine = wv < items ? (items - wv + S - 1) / S : 0;   /* the wavefront's items: wv + S n */
 
     /* staging copies, round-robin over the wavefronts: 32 x 1 KiB of the
-     * table, one 256-byte block of activation quants per copy (16 lanes),
-     * the scales (4 bytes per lane) */
+     * table, one 256-byte block of activation quants per copy (16 lanes;
+     * the tokens' Q8_K blocks are consecutive), the scales (4 bytes per
+     * lane) */
     const uint8_t *table = reinterpret_cast<const uint8_t *>(grid + 2048);
     for (int k = wv; k < 32; k += S) dot4_copy16(table + 1024 * k + 16 * lane, dot4_lds_address(cb_s) + 1024 * k);
-    for (int b = (wv + S - 32 % S) % S; b < NB; b += S)
+    for (int b = (wv + S - 32 % S) % S; b < MT * NB; b += S)
         if (lane < 16)
             dot4_copy16(x + (size_t)b * kQ8KBytes + 4 + 16 * lane, dot4_lds_address(act_s) + b * kDot4ActStride);
     if (wv == S - 1) {
-        if (lane < NB) dot4_copy4(x + (size_t)lane * kQ8KBytes, dot4_lds_address(xs_s));
-        if (NB > 64 && lane < NB - 64) dot4_copy4(x + (size_t)(lane + 64) * kQ8KBytes, dot4_lds_address(xs_s) + 256);
+#pragma unroll
+        for (int k0 = 0; k0 < MT * NB; k0 += 64)
+            if (lane < MT * NB - k0) dot4_copy4(x + (size_t)(lane + k0) * kQ8KBytes, dot4_lds_address(xs_s) + 4 * k0);
     }
 
     /* item n of the wavefront into ring slot n % P: lane l < 56 copies
@@ -417,12 +427,15 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_dot4(const uint8_t *__restri
     dot4_wait_vm_upto(mine < P ? mine : P);   /* this wavefront's staging copies have landed */
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-    int4v ar[4];   /* activation quants of the fixed block group */
+    int4v ar[MT][4];   /* activation quants of the fixed block group */
     if (ACT_REG) {
         const int b = 4 * (wv % NG) + j;
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-            ar[k] = *reinterpret_cast<const int4v *>(act_s + b * kDot4ActStride + 64 * q + 16 * k);
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                ar[t][k] =
+                    *reinterpret_cast<const int4v *>(act_s + (t * NB + b) * kDot4ActStride + 64 * q + 16 * k);
     }
     const uint8_t *rowp = ring_s + wv * P * kDot4Slot + 224 * j + 56 * r;
 
@@ -437,10 +450,14 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_dot4(const uint8_t *__restri
         const int i = wv + S * n;
         const int ql = i / NG;
         const int b = 4 * (i % NG) + j;
-        int4v a[4];
+        int4v a[MT][4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-            a[k] = ACT_REG ? ar[k] : *reinterpret_cast<const int4v *>(act_s + b * kDot4ActStride + 64 * q + 16 * k);
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                a[t][k] = ACT_REG ? ar[t][k]
+                                  : *reinterpret_cast<const int4v *>(act_s + (t * NB + b) * kDot4ActStride + 64 * q +
+                                                                     16 * k);
         /* 12-bit table indices of the lane's 8 sections, two per dword,
          * pre-shifted to byte offsets (x 8) */
         const uint32_t nlo = qh & 0x0f0f0f0fu, nhi = (qh >> 4) & 0x0f0f0f0fu;
@@ -452,27 +469,38 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_dot4(const uint8_t *__restri
                                __builtin_amdgcn_perm(n47, qs1, 0x07030602u) << 3};
         const char *cb = reinterpret_cast<const char *>(cb_s);
         const uint32_t scw = ((q & 2) ? sc1 : sc0) >> (16 * (q & 1));   /* scale word q */
-        int e = 0;
+        int e[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) e[t] = 0;
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
             /* half group h: sections 2h, 2h + 1 = elements 64 q + 16 h .. + 15 */
             const uint2 e0 = *reinterpret_cast<const uint2 *>(cb + (p[h] & 0x7ff8u));
             const uint2 e1 = *reinterpret_cast<const uint2 *>(cb + (p[h] >> 16));
-            const int4v av4 = a[h];
-            int acc = dot4z((int)e0.x, av4[0]);
-            acc = dot4((int)e0.y, av4[1], acc);
-            acc = dot4((int)e1.x, av4[2], acc);
-            acc = dot4((int)e1.y, av4[3], acc);
-            e = mad24((int)(2u * ((scw >> (3 * h)) & 7u) + 1u), acc, e);
+            const int sv = (int)(2u * ((scw >> (3 * h)) & 7u) + 1u);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const int4v av4 = a[t][h];
+                int acc = dot4z((int)e0.x, av4[0]);
+                acc = dot4((int)e0.y, av4[1], acc);
+                acc = dot4((int)e1.x, av4[2], acc);
+                acc = dot4((int)e1.y, av4[3], acc);
+                e[t] = mad24(sv, acc, e[t]);
+            }
         }
-        /* sum over the 4 lanes of the row (quad_perm [1,0,3,2], [2,3,0,1]) */
-        e += __builtin_amdgcn_update_dpp(0, e, 0xb1, 0xf, 0xf, false);
-        e += __builtin_amdgcn_update_dpp(0, e, 0x4e, 0xf, 0xf, false);
         const uint32_t bits =
             ((sc0 >> 12) & 0x000fu) | ((sc0 >> 24) & 0x00f0u) | ((sc1 >> 4) & 0x0f00u) | ((sc1 >> 16) & 0xf000u);
-        const float d = fmul_rn(f16_to_f32(bits), xs_s[b]);
-        const float t = fmul_rn(d, fmul_rn((float)e, 0.125f));
-        if (q == 0) t_s[(ql * NB + b) * 4 + r] = t;
+        const float ds = f16_to_f32(bits);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            /* sum over the 4 lanes of the row (quad_perm [1,0,3,2], [2,3,0,1]) */
+            int et = e[t];
+            et += __builtin_amdgcn_update_dpp(0, et, 0xb1, 0xf, 0xf, false);
+            et += __builtin_amdgcn_update_dpp(0, et, 0x4e, 0xf, 0xf, false);
+            const float d = fmul_rn(ds, xs_s[t * NB + b]);
+            const float term = fmul_rn(d, fmul_rn((float)et, 0.125f));
+            if (q == 0) t_s[((ql * NB + b) * 4 + r) * MT + t] = term;
+        }
     };
 
     const int full = mine / P, rem = mine % P;
@@ -490,14 +518,14 @@ __global__ __launch_bounds__(64 * S) void gemm_iq1m_dot4(const uint8_t *__restri
         if (i < rem) item(full * P + i, i);
     __syncthreads();
 
-    /* one thread per row: the fp32 chain in block order */
-    for (int c = tid; c < (int)(q1 - q0) * 4; c += 64 * S) {
-        const int ql = c >> 2, rr = c & 3;
+    /* one thread per (row, token): the fp32 chain in block order */
+    for (int c = tid; c < (int)(q1 - q0) * 4 * MT; c += 64 * S) {
+        const int t = c % MT, ql = c / (4 * MT), rr = (c / MT) & 3;
         float total = 0.0f;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) total = fadd_rn(total, t_s[(ql * NB + b) * 4 + rr]);
+        for (int b = 0; b < NB; ++b) total = fadd_rn(total, t_s[((ql * NB + b) * 4 + rr) * MT + t]);
         const uint32_t row = (q0 + (uint32_t)ql) * 4 + (uint32_t)rr;
-        if (row < rows) y[row] = total;
+        if (row < rows) y[(size_t)t * ldy + row] = total;
     }
 }
 
@@ -512,17 +540,29 @@ constexpr int dot4_waves()
 }
 constexpr int kDot4Prefetch = 2;
 
-template <int NB>
-bool launch_iq1m_dot4(const uint8_t *w, const uint8_t *x, float *y, uint32_t rows, const uint2 *grid,
+template <int NB, int MT>
+bool launch_iq1m_dot4(const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows, const uint2 *grid,
                       hipStream_t stream)
 {
     const uint32_t nquads = (rows + 3) / 4;
     const uint32_t groups = nquads < kDot4Groups ? nquads : kDot4Groups;
     const uint32_t per = (nquads + groups - 1) / groups;
-    if ((size_t)per * NB * 4 > (size_t)kDot4TFloats) return false;
-    hipLaunchKernelGGL((gemm_iq1m_dot4<NB, dot4_waves<NB>(), kDot4Prefetch>), dim3(groups), dim3(64 * dot4_waves<NB>()),
-                       0, stream, w, x, y, rows, grid);
+    if ((size_t)per * NB * 4 * MT > (size_t)dot4_t_floats<MT>()) return false;
+    hipLaunchKernelGGL((gemm_iq1m_dot4<NB, dot4_waves<NB>(), kDot4Prefetch, MT>), dim3(groups),
+                       dim3(64 * dot4_waves<NB>()), 0, stream, w, x, y, ldy, rows, grid);
     return hipGetLastError() == hipSuccess;
+}
+
+template <int NB>
+bool launch_iq1m_dot4_m(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
+                        const uint2 *grid, hipStream_t stream)
+{
+    switch (m) {
+    case 1: return launch_iq1m_dot4<NB, 1>(w, x, y, ldy, rows, grid, stream);
+    case 2: return launch_iq1m_dot4<NB, 2>(w, x, y, ldy, rows, grid, stream);
+    case 3: return launch_iq1m_dot4<NB, 3>(w, x, y, ldy, rows, grid, stream);
+    default: return false;
+    }
 }
 
 }  // namespace
@@ -1088,13 +1128,13 @@ bool launch_gemm_iq1m_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, flo
 {
     if (!rows || ldy < rows || !grid) return false;
     const uint2 *g = static_cast<const uint2 *>(grid);
-    if (m == 1) {
+    if (m <= 3) {
         bool ok = false;
         switch (nb) {
-        case 20: ok = launch_iq1m_dot4<20>(w_tiled, x, y, rows, g, stream); break;
-        case 24: ok = launch_iq1m_dot4<24>(w_tiled, x, y, rows, g, stream); break;
-        case 40: ok = launch_iq1m_dot4<40>(w_tiled, x, y, rows, g, stream); break;
-        case 68: ok = launch_iq1m_dot4<68>(w_tiled, x, y, rows, g, stream); break;
+        case 20: ok = launch_iq1m_dot4_m<20>(m, w_tiled, x, y, ldy, rows, g, stream); break;
+        case 24: ok = launch_iq1m_dot4_m<24>(m, w_tiled, x, y, ldy, rows, g, stream); break;
+        case 40: ok = launch_iq1m_dot4_m<40>(m, w_tiled, x, y, ldy, rows, g, stream); break;
+        case 68: ok = launch_iq1m_dot4_m<68>(m, w_tiled, x, y, ldy, rows, g, stream); break;
         default: break;
         }
         if (ok) return true;

@@ -213,11 +213,12 @@ def test_tiled_iq1m_repack_and_gemm_bit_exact(hip, oracle, device, rows, width):
         assert np.array_equal(bits(got), bits(want)), "M=%d" % m
 
 
-@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("m", [1, 2, 3])
 def test_tiled_iq1m_full_shape_matches_row_major(hip, device, m):
-    """34816x5120 (fused gate|up) and 5120x17408 (down) IQ1_M: the tiled copy's
-    kernel equals the row-major kernel bit for bit."""
-    for rows, width in ((34816, 5120), (5120, 17408)):
+    """34816x5120 (fused gate|up), 5120x17408 (down) and 16480x5120 (the
+    DeltaNet input group) IQ1_M: the tiled copy's kernel (the v_dot4 one for
+    1..3 tokens) equals the row-major matrix-core kernel bit for bit."""
+    for rows, width in ((34816, 5120), (5120, 17408), (16480, 5120)):
         w = synth.matrix(IQ1_M, rows, width, seed=m + rows + 1)
         wd = to_dev(w, device)
         x = synth.activations(width, seed=m * 11 + width, count=m)
