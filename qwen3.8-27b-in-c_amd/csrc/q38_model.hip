@@ -182,26 +182,37 @@ __global__ __launch_bounds__(128) void deltanet_prep_kernel(float *__restrict__ 
  * accumulator of vector a, element j; result = ((H0+H1)+(H2+H3)) with
  * H[j] = Q[j] + Q[j+4], Q[j] = (P0[j]+P2[j]) + (P1[j]+P3[j]).
  * Operates on 32-lane halves of the wavefront; every lane gets the result. */
-/* lane l of each 16-lane row gets lane l + N of the row (DPP row_shl:N) */
+/* lane l of each 16-lane row gets lane (l - N) mod 16 of the row (DPP row_ror:N) */
 template <int N>
-__device__ __forceinline__ float dpp_shl(float v)
+__device__ __forceinline__ float dpp_ror(float v)
 {
-    return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x100 + N, 0xf, 0xf, false));
+    return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x120 + N, 0xf, 0xf, false));
 }
+/* lane l of each quad gets lane CTRL-selected within the quad (DPP quad_perm) */
+template <int CTRL>
+__device__ __forceinline__ float dpp_quad(float v)
+{
+    return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), CTRL, 0xf, 0xf, false));
+}
+/* As a butterfly, so that every lane of the half ends with the result and no
+ * broadcast follows: each step adds the partner lane that holds the other
+ * operand of the reference's pair.  Lane 0 adds exactly the reference's
+ * operand pairs in its order; every other lane adds the same pairs, some
+ * with the operands swapped, which rounds to the same float. */
 __device__ __forceinline__ float avx2_tree32(float v)
 {
-    /* lane l < 16 of each half gets lane l + 16 (v_permlane16_swap: the odd
-     * 16-lane rows of the first operand trade places with the even rows of
-     * the second) */
+    /* lane l's partner l ^ 16 (v_permlane16_swap of v with itself: the odd
+     * 16-lane rows of the first copy trade places with the even rows of the
+     * second, so an even row finds its partner in the second result and an
+     * odd row in the first) */
     const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __fadd_rn(v, __uint_as_float(sw[1]));   /* l<16: P0+P2 (l<8), P1+P3 (8..15) */
-    v = __fadd_rn(v, dpp_shl<8>(v));            /* l<8:  Q[l] */
-    v = __fadd_rn(v, dpp_shl<4>(v));            /* l<4:  H[l] */
-    v = __fadd_rn(v, dpp_shl<1>(v));            /* l=0: H0+H1, l=2: H2+H3 */
-    v = __fadd_rn(v, dpp_shl<2>(v));            /* l=0: (H0+H1)+(H2+H3) */
-    const float lo = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
-    const float hi = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32));
-    return (threadIdx.x & 32) ? hi : lo;
+    const float partner = __uint_as_float((threadIdx.x & 16) ? sw[0] : sw[1]);
+    v = __fadd_rn(v, partner);                  /* lane 8a + j (+ 16): P_a[j] + P_{a+2}[j], a = 0, 1 */
+    v = __fadd_rn(v, dpp_ror<8>(v));            /* lane l: Q[l % 8] (partner l ^ 8) */
+    v = __fadd_rn(v, dpp_ror<4>(v));            /* lane l: Q[j] + Q[j ^ 4], j = l % 8: H[l % 4] */
+    v = __fadd_rn(v, dpp_quad<0xb1>(v));        /* quad partner l ^ 1: H0 + H1 or H2 + H3 */
+    v = __fadd_rn(v, dpp_quad<0x4e>(v));        /* quad partner l ^ 2: (H0 + H1) + (H2 + H3) */
+    return v;
 }
 
 /* State update of one value head (qwen38_model.c:759-783): S *= decay; per
