@@ -64,6 +64,8 @@ WORKLOADS = {
     "iq1m_gemv": (29, 17408, 5120, 1, True, "IQ1_M GEMV 17408x5120"),
     "iq1m_gemv_t": (29, 5120, 17408, 1, True, "IQ1_M GEMV 5120x17408"),
     "q6k_gemv": (14, 17408, 5120, 1, False, "Q6_K GEMV 17408x5120"),
+    "q6k_lmhead": (14, 248320, 5120, 1, False, "Q6_K LM head 248320x5120, one row (an MTP draft)"),
+    "q6k_lmhead_m3": (14, 248320, 5120, 3, False, "Q6_K LM head 248320x5120, 3 rows (the verify batch)"),
     "q4k_tiled_m3": (12, 34816, 5120, 3, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 3 tokens"),
     "q4k_tiled_down_m3": (12, 5120, 17408, 3, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 3 tokens"),
     "q4k_tiled_out_m3": (12, 5120, 6144, 3, True,
