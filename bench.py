@@ -68,6 +68,8 @@ WORKLOADS = {
     "q6k_lmhead_m3": (14, 248320, 5120, 3, False, "Q6_K LM head 248320x5120, 3 rows (the verify batch)"),
     "q4k_tiled_m3": (12, 34816, 5120, 3, True, "Q4_K tiled GEMM 34816x5120 (FFN gate|up), 3 tokens"),
     "q4k_tiled_down_m3": (12, 5120, 17408, 3, True, "Q4_K tiled GEMM 5120x17408 (FFN down), 3 tokens"),
+    "q4k_tiled_dnin_m3": (12, 16480, 5120, 3, True, "Q4_K tiled GEMM 16480x5120 (DeltaNet input group), 3 tokens"),
+    "q4k_tiled_qkv_m3": (12, 14336, 5120, 3, True, "Q4_K tiled GEMM 14336x5120 (attention q|gate|k|v), 3 tokens"),
     "q4k_tiled_out_m3": (12, 5120, 6144, 3, True,
                          "Q4_K tiled GEMM 5120x6144 (attention output / DeltaNet output), 3 tokens"),
     "iq1m_gemm_m3": (29, 34816, 5120, 3, True, "IQ1_M GEMM 34816x5120 (FFN gate|up), 3 tokens"),
