@@ -1086,10 +1086,17 @@ bool launch_iq1m_wide128_nb(const uint8_t *w, const uint8_t *x, float *y, uint32
 constexpr uint32_t kIQW2MinTokens = 128;
 }  // namespace
 
+/* the buffer-resource kernels address a matrix with 32-bit byte offsets */
+static bool iq1m_extent_ok(uint32_t rows, uint32_t nb)
+{
+    return (uint64_t)((rows + 15) / 16 * 16) * nb * kIQ1MBytes <= 0xffffffffull;
+}
+
 bool launch_gemm_iq1m_wide(uint32_t tokens, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                            uint32_t nb, const void *grid, hipStream_t stream)
 {
-    if (!rows || !tokens || ldy < rows || !grid || tokens > 65535u * kIQWideTokens) return false;
+    if (!rows || !tokens || ldy < rows || !grid || tokens > 65535u * kIQWideTokens || !iq1m_extent_ok(rows, nb))
+        return false;
     const uint2 *g = static_cast<const uint2 *>(grid);
     if (tokens >= kIQW2MinTokens) switch (nb) {
         case 20: return launch_iq1m_wide128_nb<20>(w, x, y, ldy, rows, tokens, g, stream);
@@ -1112,7 +1119,7 @@ bool launch_gemm_iq1m_wide(uint32_t tokens, const uint8_t *w, const uint8_t *x, 
 bool launch_gemm_iq1m_mfma(int m, const uint8_t *w, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                            uint32_t nb, const void *grid, hipStream_t stream)
 {
-    if (!rows || ldy < rows || !grid) return false;
+    if (!rows || ldy < rows || !grid || !iq1m_extent_ok(rows, nb)) return false;
     const uint2 *g = static_cast<const uint2 *>(grid);
     switch (nb) {
     case 20: return launch_iq1m_nb<20, false>(m, w, x, y, ldy, rows, g, stream);
@@ -1126,7 +1133,7 @@ bool launch_gemm_iq1m_mfma(int m, const uint8_t *w, const uint8_t *x, float *y, 
 bool launch_gemm_iq1m_tiled(int m, const uint8_t *w_tiled, const uint8_t *x, float *y, uint32_t ldy, uint32_t rows,
                             uint32_t nb, const void *grid, hipStream_t stream)
 {
-    if (!rows || ldy < rows || !grid) return false;
+    if (!rows || ldy < rows || !grid || !iq1m_extent_ok(rows, nb)) return false;
     const uint2 *g = static_cast<const uint2 *>(grid);
     if (m <= 3) {
         bool ok = false;
