@@ -18,7 +18,7 @@ prefill logits.  The reference's own invariant is asserted as the fixture is
 written: its speculative tokens equal its greedy tokens
 (src/cli/qwen38_spec_bench.c:100-119).
 
-Run from the repository root (about 10 min for q4km and 2 h for iq1m on
+Run from the repository root (about 10 min for q4km and 5.5 h for iq1m on
 8 cores):
   python tests/golden/make_decode_golden.py q4km|iq1m [GGUF_PATH]
 """

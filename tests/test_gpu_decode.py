@@ -5,8 +5,9 @@ tests/golden/make_decode_golden.py from oracle/_ref on the same synthetic
 
   q4km  512-token prompt, then speculative_greedy(k=3) until 256 tokens are
         produced, and from a reset the same prompt + 256 greedy tokens
-  iq1m  4096-token prompt prefilled as one batch, 32 speculative tokens and
-        16 greedy tokens (context past 4096 positions)
+  iq1m  4096-token prompt prefilled as one batch, then speculative_greedy(k=3)
+        until 1024 tokens are produced, and from a reset the same prompt +
+        1024 greedy tokens (context 4097..5120)
 
 Bar: bit-identical.  The prefill logits, every transaction's logits and
 every greedy step's logits compare by SHA-256 of their float32 bytes; the
