@@ -215,50 +215,75 @@ __device__ __forceinline__ float avx2_tree32(float v)
     return v;
 }
 
-/* State update of one value head (qwen38_model.c:759-783): S *= decay; per
- * column c: pred = dot(S_c, k); delta = (v[c] - pred) * beta;
- * S_c = fma(k, delta, S_c); out[c] = dot(S_c, q) * (1/sqrt(128)).
- * Columns are independent: 32 lanes per column (lane l owns elements
- * l, l+32, l+64, l+96, the reference's fixed 4 x 8-lane accumulators), two
- * columns per wavefront, eight per block of 256, all of one value head h.
- * The column runs through `rows` consecutive tokens (row t's prepared
- * q|k|v at qkv + t * ld, beta and alpha at + beta_off / alpha_off, output
- * at out + t * kLinV): the state before row t is slot (*slot_ptr + t), read
- * once, kept in registers, and each row's result is written to the next
- * slot (with `last_only`, only the last row's, to slot *slot_ptr + rows).
- * The block's inputs (k and q of head h % 16, the block's eight v values,
- * the decay and beta of head h) come through LDS in chunks of kScanChunk
- * rows, the next chunk's global loads in flight while the current one is
- * scanned, so the sequential scan reads only LDS. */
 constexpr int kScanChunk = 16;
 
+/* avx2_tree32 for a 16-lane row whose lane l holds the accumulators P[l]
+ * (a) and P[l + 16] (b) of the 32-lane form: the first pair is added inside
+ * the lane, the other four steps are the same row shifts and quad
+ * permutations, so the result is the same float. */
+__device__ __forceinline__ float avx2_tree16(float a, float b)
+{
+    float v = __fadd_rn(a, b);
+    v = __fadd_rn(v, dpp_ror<8>(v));
+    v = __fadd_rn(v, dpp_ror<4>(v));
+    v = __fadd_rn(v, dpp_quad<0xb1>(v));
+    v = __fadd_rn(v, dpp_quad<0x4e>(v));
+    return v;
+}
+
+/* State update of one value head over a batch of rows
+ * (qwen38_model.c:759-783): S *= decay; per column c: pred = dot(S_c, k);
+ * delta = (v[c] - pred) * beta; S_c = fma(k, delta, S_c);
+ * out[c] = dot(S_c, q) * (1/sqrt(128)).  Columns are independent.  The
+ * reference's dots are 32 fixed accumulators P[j] (element j + 32a added in
+ * a = 0..3 order) and a tree; here 16 lanes run a column: lane l owns
+ * elements l + 32a and l + 16 + 32a, i.e. P[l] and P[l + 16] as two
+ * independent fmaf chains, and avx2_tree16 adds them in the reference's
+ * order (measured on MI355X against one column per 32 lanes: 4096-token
+ * prefill 422 -> 415 ms).  Sixteen columns of one value head per block of
+ * 256.  The columns run through `rows` consecutive tokens (row t's prepared
+ * q|k|v at qkv + t * ld, beta and alpha at + beta_off / alpha_off, output at
+ * out + t * kLinV): the state before row t is slot (*slot_ptr + t), read
+ * once, kept in registers, and each row's result is written to the next
+ * slot (with `last_only`, only the last row's, to slot *slot_ptr + rows).
+ * The block's inputs (k and q of head h % 16, the block's v values, the
+ * decay and beta of head h) come through LDS in chunks of kScanChunk rows,
+ * the next chunk's global loads in flight while the current one is
+ * scanned, so the sequential scan reads only LDS. */
+constexpr int kScan16Cols = 16;
+
 __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__ out, float *__restrict__ state,
-                                                             long long slot_stride,
-                                                             const uint32_t *__restrict__ slot_ptr, int rows,
-                                                             const float *__restrict__ qkv, long long ld,
-                                                             int beta_off, int alpha_off, float query_scale,
-                                                             int last_only)
+                                                              long long slot_stride,
+                                                              const uint32_t *__restrict__ slot_ptr, int rows,
+                                                              const float *__restrict__ qkv, long long ld,
+                                                              int beta_off, int alpha_off, float query_scale,
+                                                              int last_only)
 {
     __shared__ float kq_s[2][kScanChunk][2 * kHeadDim];   /* [parity][row][k 0..127 | q 0..127] */
-    __shared__ float v_s[2][kScanChunk][8];
+    __shared__ float v_s[2][kScanChunk][kScan16Cols];
     __shared__ float ab_s[2][kScanChunk][2];               /* decay = expf(alpha), beta */
     const int tid = threadIdx.x;
-    const int column_global = blockIdx.x * 8 + (tid >> 5);   /* 0 .. 48*128-1 */
-    const int h = column_global >> 7;
-    const int c = column_global & 127;
-    const int l = tid & 31;
+    const int col0 = blockIdx.x * kScan16Cols;   /* 0 .. 48*128-1 */
+    const int h = col0 >> 7;
+    const int c0 = col0 & 127;
+    const int cl = tid >> 4, l = tid & 15;
+    const int c = c0 + cl;
     const int kh = h % 16;
-    const int c0 = (blockIdx.x * 8) & 127;
     const uint32_t slot0 = *slot_ptr;
     const size_t col_off = ((size_t)h * kHeadDim + c) * kHeadDim;
     const float *s = state + (size_t)(slot0 % kStateSlots) * slot_stride + col_off;
-    float sv[4];
-    for (int a = 0; a < 4; ++a) sv[a] = s[32 * a + l];
+    float sv[8];   /* elements 32a + l (a = 0..3), then 32a + l + 16 */
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        sv[a] = s[32 * a + l];
+        sv[4 + a] = s[32 * a + l + 16];
+    }
 
     /* thread tid stages element tid of the k|q vector of every row of a
-     * chunk; threads 0..8R-1 a v value, 8R..8R+2R-1 an alpha or beta */
+     * chunk, the v value of row tid / 16 and column tid % 16, and threads
+     * 0..2R-1 an alpha or beta */
     const int kq_src = tid < kHeadDim ? kQKDim + kh * kHeadDim + tid : kh * kHeadDim + (tid - kHeadDim);
-    float kq_r[kScanChunk], x_r = 0.0f;
+    float kq_r[kScanChunk], v_r = 0.0f, ab_r = 0.0f;
     const int nchunks = (rows + kScanChunk - 1) / kScanChunk;
     auto fetch = [&](int ch) {
         const int r0 = ch * kScanChunk;
@@ -267,36 +292,36 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
             const int t = r0 + i < rows ? r0 + i : rows - 1;
             kq_r[i] = qkv[(long long)t * ld + kq_src];
         }
-        if (tid < 10 * kScanChunk) {
-            const int i = tid < 8 * kScanChunk ? tid >> 3 : (tid - 8 * kScanChunk) >> 1;
+        {
+            const int i = tid >> 4;
             const int t = r0 + i < rows ? r0 + i : rows - 1;
-            const float *row = qkv + (long long)t * ld;
-            x_r = tid < 8 * kScanChunk ? row[2 * kQKDim + h * kHeadDim + c0 + (tid & 7)]
-                                       : row[(tid & 1) ? beta_off + h : alpha_off + h];
+            v_r = qkv[(long long)t * ld + 2 * kQKDim + h * kHeadDim + c0 + (tid & 15)];
+        }
+        if (tid < 2 * kScanChunk) {
+            const int i = tid >> 1;
+            const int t = r0 + i < rows ? r0 + i : rows - 1;
+            ab_r = qkv[(long long)t * ld + ((tid & 1) ? beta_off + h : alpha_off + h)];
         }
     };
-    /* the chunk's inputs into LDS; the decay expf(alpha) of each row is
-     * computed here, in parallel, off the scan's dependent chain */
     auto stage = [&](int par) {
 #pragma unroll
         for (int i = 0; i < kScanChunk; ++i) kq_s[par][i][tid] = kq_r[i];
-        if (tid < 8 * kScanChunk) v_s[par][tid >> 3][tid & 7] = x_r;
-        else if (tid < 10 * kScanChunk)
-            ab_s[par][(tid - 8 * kScanChunk) >> 1][tid & 1] = (tid & 1) ? x_r : q38_expf(x_r);
+        v_s[par][tid >> 4][tid & 15] = v_r;
+        if (tid < 2 * kScanChunk) ab_s[par][tid >> 1][tid & 1] = (tid & 1) ? ab_r : q38_expf(ab_r);
     };
-    /* a row's inputs from LDS, its decay computed there too, so that the
-     * next row's reads and expf overlap the current row's dependent chain */
     struct RowIn {
-        float k[4], q[4], v, beta, decay;
+        float k[8], q[8], v, beta, decay;
     };
     auto read_row = [&](int par, int i) {
         RowIn in;
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
             in.k[a] = kq_s[par][i][32 * a + l];
+            in.k[4 + a] = kq_s[par][i][32 * a + l + 16];
             in.q[a] = kq_s[par][i][kHeadDim + 32 * a + l];
+            in.q[4 + a] = kq_s[par][i][kHeadDim + 32 * a + l + 16];
         }
-        in.v = v_s[par][i][(tid >> 5) & 7];
+        in.v = v_s[par][i][cl];
         in.beta = ab_s[par][i][1];
         in.decay = ab_s[par][i][0];
         return in;
@@ -313,20 +338,31 @@ __global__ __launch_bounds__(256) void deltanet_state_kernel(float *__restrict__
         for (int i = 0; i < n; ++i) {
             const int t = r0 + i;
             const RowIn nxt = read_row(par, i + 1 < n ? i + 1 : i);
-            for (int a = 0; a < 4; ++a) sv[a] = __fmul_rn(sv[a], cur.decay);
-            float p = 0.0f;
-            for (int a = 0; a < 4; ++a) p = __builtin_fmaf(sv[a], cur.k[a], p);
-            const float pred = avx2_tree32(p);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sv[e] = __fmul_rn(sv[e], cur.decay);
+            float pa = 0.0f, pb = 0.0f;
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                pa = __builtin_fmaf(sv[a], cur.k[a], pa);
+                pb = __builtin_fmaf(sv[4 + a], cur.k[4 + a], pb);
+            }
+            const float pred = avx2_tree16(pa, pb);
             const float delta = __fmul_rn(__fsub_rn(cur.v, pred), cur.beta);
             float *s_out = state + (size_t)((slot0 + t + 1) % kStateSlots) * slot_stride + col_off;
             const bool store = !last_only || t == rows - 1;
-            float r = 0.0f;
+            float ra = 0.0f, rb = 0.0f;
+#pragma unroll
             for (int a = 0; a < 4; ++a) {
                 sv[a] = __builtin_fmaf(cur.k[a], delta, sv[a]);
-                if (store) s_out[32 * a + l] = sv[a];
-                r = __builtin_fmaf(sv[a], cur.q[a], r);
+                sv[4 + a] = __builtin_fmaf(cur.k[4 + a], delta, sv[4 + a]);
+                if (store) {
+                    s_out[32 * a + l] = sv[a];
+                    s_out[32 * a + l + 16] = sv[4 + a];
+                }
+                ra = __builtin_fmaf(sv[a], cur.q[a], ra);
+                rb = __builtin_fmaf(sv[4 + a], cur.q[4 + a], rb);
             }
-            const float result = avx2_tree32(r);
+            const float result = avx2_tree16(ra, rb);
             if (l == 0) out[(size_t)t * kLinV + h * kHeadDim + c] = __fmul_rn(result, query_scale);
             cur = nxt;
         }
@@ -425,8 +461,9 @@ __global__ __launch_bounds__(128) void deltanet_prep_rows_kernel(float *__restri
 
 /* deltanet_prep_kernel and deltanet_state_kernel in one launch, for up to
  * kFusedRows rows.  Block (h, cg) = (blockIdx.x / 16, blockIdx.x % 16) owns
- * the state columns 8cg..8cg+7 of value head h as in deltanet_state_kernel,
- * and first redoes, into LDS, the prep arithmetic of what those columns
+ * the state columns 8cg..8cg+7 of value head h, 32 lanes per column (lane l
+ * owns elements l + 32a, the reference's accumulator P[l], and the column's
+ * dots end in avx2_tree32), and first redoes, into LDS, the prep arithmetic of what those columns
  * read: the conv + SiLU + L2 norm of q and k head kh = h % 16 (thread i:
  * q channel i, k channel i - 128), conv + SiLU of its eight v channels, and
  * beta / alpha of head h.  Each conv channel's next state slots are written
@@ -1272,9 +1309,8 @@ void launch_deltanet_state(float *attn, float *delta_state, long long slot_strid
                            const float *qkv, long long ld, int beta_off, int alpha_off, float query_scale,
                            bool last_only, hipStream_t stream)
 {
-    deltanet_state_kernel<<<kVHeads * kHeadDim / 8, 256, 0, stream>>>(attn, delta_state, slot_stride, slot, rows,
-                                                                     qkv, ld, beta_off, alpha_off, query_scale,
-                                                                     last_only ? 1 : 0);
+    deltanet_state_kernel<<<kVHeads * kHeadDim / kScan16Cols, 256, 0, stream>>>(
+        attn, delta_state, slot_stride, slot, rows, qkv, ld, beta_off, alpha_off, query_scale, last_only ? 1 : 0);
 }
 
 bool launch_deltanet_fused(float *attn, float *delta_state, long long slot_stride, const uint32_t *slot, int rows,
