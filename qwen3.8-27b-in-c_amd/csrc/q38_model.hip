@@ -177,11 +177,6 @@ __global__ __launch_bounds__(128) void deltanet_prep_kernel(float *__restrict__ 
     }
 }
 
-/* Sum of 32 per-lane values in the reference's AVX2 reduction order
- * (q38_dot_f32_128, qwen38_model.c:616-637): lane l = 8*a + j holds the
- * accumulator of vector a, element j; result = ((H0+H1)+(H2+H3)) with
- * H[j] = Q[j] + Q[j+4], Q[j] = (P0[j]+P2[j]) + (P1[j]+P3[j]).
- * Operates on 32-lane halves of the wavefront; every lane gets the result. */
 /* lane l of each 16-lane row gets lane (l - N) mod 16 of the row (DPP row_ror:N) */
 template <int N>
 __device__ __forceinline__ float dpp_ror(float v)
@@ -194,40 +189,28 @@ __device__ __forceinline__ float dpp_quad(float v)
 {
     return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), CTRL, 0xf, 0xf, false));
 }
-/* As a butterfly, so that every lane of the half ends with the result and no
- * broadcast follows: each step adds the partner lane that holds the other
- * operand of the reference's pair.  Lane 0 adds exactly the reference's
- * operand pairs in its order; every other lane adds the same pairs, some
- * with the operands swapped, which rounds to the same float. */
-__device__ __forceinline__ float avx2_tree32(float v)
-{
-    /* lane l's partner l ^ 16 (v_permlane16_swap of v with itself: the odd
-     * 16-lane rows of the first copy trade places with the even rows of the
-     * second, so an even row finds its partner in the second result and an
-     * odd row in the first) */
-    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    const float partner = __uint_as_float((threadIdx.x & 16) ? sw[0] : sw[1]);
-    v = __fadd_rn(v, partner);                  /* lane 8a + j (+ 16): P_a[j] + P_{a+2}[j], a = 0, 1 */
-    v = __fadd_rn(v, dpp_ror<8>(v));            /* lane l: Q[l % 8] (partner l ^ 8) */
-    v = __fadd_rn(v, dpp_ror<4>(v));            /* lane l: Q[j] + Q[j ^ 4], j = l % 8: H[l % 4] */
-    v = __fadd_rn(v, dpp_quad<0xb1>(v));        /* quad partner l ^ 1: H0 + H1 or H2 + H3 */
-    v = __fadd_rn(v, dpp_quad<0x4e>(v));        /* quad partner l ^ 2: (H0 + H1) + (H2 + H3) */
-    return v;
-}
 
 constexpr int kScanChunk = 16;
 
-/* avx2_tree32 for a 16-lane row whose lane l holds the accumulators P[l]
- * (a) and P[l + 16] (b) of the 32-lane form: the first pair is added inside
- * the lane, the other four steps are the same row shifts and quad
- * permutations, so the result is the same float. */
+/* Sum of a column's 32 accumulators in the reference's AVX2 reduction order
+ * (q38_dot_f32_128, qwen38_model.c:616-637): P_a[j] is the accumulator of
+ * vector a = 0..3, element j = 0..7, and the result is ((H0+H1)+(H2+H3))
+ * with H[j] = Q[j] + Q[j+4], Q[j] = (P0[j]+P2[j]) + (P1[j]+P3[j]).  A column
+ * runs on a 16-lane row: lane l = 8a + j (a = 0, 1) holds P_a[j] in `a` and
+ * P_{a+2}[j] in `b`, so the first pair is added inside the lane; each later
+ * step is a butterfly that adds the partner lane holding the other operand
+ * of the reference's pair (row_ror 8: lane l ^ 8, row_ror 4 and the quad
+ * permutations: l ^ 4, l ^ 1, l ^ 2).  Lane 0 adds exactly the reference's
+ * operand pairs in its order; every other lane adds the same pairs, some
+ * with the operands swapped, which rounds to the same float, so every lane
+ * of the row ends with the sum. */
 __device__ __forceinline__ float avx2_tree16(float a, float b)
 {
-    float v = __fadd_rn(a, b);
-    v = __fadd_rn(v, dpp_ror<8>(v));
-    v = __fadd_rn(v, dpp_ror<4>(v));
-    v = __fadd_rn(v, dpp_quad<0xb1>(v));
-    v = __fadd_rn(v, dpp_quad<0x4e>(v));
+    float v = __fadd_rn(a, b);                  /* lane 8a + j: P_a[j] + P_{a+2}[j] */
+    v = __fadd_rn(v, dpp_ror<8>(v));            /* Q[l % 8] */
+    v = __fadd_rn(v, dpp_ror<4>(v));            /* Q[j] + Q[j ^ 4], j = l % 8: H[l % 4] */
+    v = __fadd_rn(v, dpp_quad<0xb1>(v));        /* H0 + H1 or H2 + H3 */
+    v = __fadd_rn(v, dpp_quad<0x4e>(v));        /* (H0 + H1) + (H2 + H3) */
     return v;
 }
 
@@ -460,15 +443,16 @@ __global__ __launch_bounds__(128) void deltanet_prep_rows_kernel(float *__restri
 }
 
 /* deltanet_prep_kernel and deltanet_state_kernel in one launch, for up to
- * kFusedRows rows.  Block (h, cg) = (blockIdx.x / 16, blockIdx.x % 16) owns
- * the state columns 8cg..8cg+7 of value head h, 32 lanes per column (lane l
- * owns elements l + 32a, the reference's accumulator P[l], and the column's
- * dots end in avx2_tree32), and first redoes, into LDS, the prep arithmetic of what those columns
- * read: the conv + SiLU + L2 norm of q and k head kh = h % 16 (thread i:
- * q channel i, k channel i - 128), conv + SiLU of its eight v channels, and
+ * kFusedRows rows.  Block (h, cg) = (blockIdx.x / 8, blockIdx.x % 8) owns
+ * the state columns 16cg..16cg+15 of value head h, 16 lanes per column as
+ * in deltanet_state_kernel, and first redoes, into LDS, the prep arithmetic
+ * of what those columns read: the conv + SiLU + L2 norm of q and k head
+ * kh = h % 16 (thread i: q channel i, k channel i - 128), conv + SiLU of its
+ * sixteen v channels, and
  * beta / alpha of head h.  Each conv channel's next state slots are written
  * by one block: q/k channels by block (kh, 0), v channels by their owner. */
 constexpr int kFusedRows = 8;
+constexpr int kFusedCols = 16;   /* state columns per block, 16 lanes each */
 
 __device__ __forceinline__ void conv_silu_rows(float *y_out, int y_stride, const float *qkv, long long ld, int ch,
                                                const float *conv_state, float *conv_out, long long conv_stride,
@@ -513,26 +497,31 @@ __global__ __launch_bounds__(256) void deltanet_fused_kernel(float *__restrict__
                                                              const float *__restrict__ ssm_dt)
 {
     __shared__ float qk_s[kFusedRows][256];   /* SiLU outputs: q of head kh (0..127), k (128..255) */
-    __shared__ float v_s[kFusedRows][8];
+    __shared__ float v_s[kFusedRows][kFusedCols];
     __shared__ float beta_s[kFusedRows], alpha_s[kFusedRows];   /* beta and decay = expf(alpha) */
     __shared__ double part_s[kFusedRows][4];
     __shared__ float scale_s[kFusedRows][2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int h = blockIdx.x >> 4, cg = blockIdx.x & 15, kh = h % 16;
-    const int c = cg * 8 + (tid >> 5), l = tid & 31;
+    constexpr int kGroups = kHeadDim / kFusedCols;   /* column groups per head */
+    const int h = blockIdx.x / kGroups, cg = blockIdx.x % kGroups, kh = h % 16;
+    const int c = cg * kFusedCols + (tid >> 4), l = tid & 15;
     const uint32_t slot0 = *slot_ptr;
     const size_t col_off = ((size_t)h * kHeadDim + c) * kHeadDim;
     const float *s = state + (size_t)(slot0 % kStateSlots) * slot_stride + col_off;
-    float sv[4];
-    for (int a = 0; a < 4; ++a) sv[a] = s[32 * a + l];
+    float sv[8];   /* elements 32a + l (a = 0..3), then 32a + l + 16 */
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        sv[a] = s[32 * a + l];
+        sv[4 + a] = s[32 * a + l + 16];
+    }
 
     /* prep (deltanet_prep_kernel, qwen38_model.c:720-757) */
     const int ch = tid < 128 ? kh * kHeadDim + tid : kQKDim + kh * kHeadDim + (tid - 128);
     conv_silu_rows(&qk_s[0][tid], 256, qkv, ld, ch, conv_state, h < 16 && cg == 0 ? conv_state : nullptr,
                    conv_stride, slot0, rows, conv_w);
-    if (tid < 8)
-        conv_silu_rows(&v_s[0][tid], 8, qkv, ld, 2 * kQKDim + h * kHeadDim + cg * 8 + tid, conv_state, conv_state,
-                       conv_stride, slot0, rows, conv_w);
+    if (tid < kFusedCols)
+        conv_silu_rows(&v_s[0][tid], kFusedCols, qkv, ld, 2 * kQKDim + h * kHeadDim + cg * kFusedCols + tid,
+                       conv_state, conv_state, conv_stride, slot0, rows, conv_w);
     if (tid >= 64 && tid < 64 + rows) {
         const float *row = qkv + (long long)(tid - 64) * ld;
         beta_s[tid - 64] = sigmoidf_exact(row[beta_off + h]);
@@ -564,28 +553,38 @@ __global__ __launch_bounds__(256) void deltanet_fused_kernel(float *__restrict__
     }
     __syncthreads();
 
-    /* state update (deltanet_state_kernel) */
+    /* state update (deltanet_state_kernel's arithmetic and lane layout) */
     for (int t = 0; t < rows; ++t) {
         const float decay = alpha_s[t];
         const float qs = scale_s[t][0], ks = scale_s[t][1];
-        float kv[4], qv[4];
-        for (int a = 0; a < 4; ++a) {
-            sv[a] = __fmul_rn(sv[a], decay);
-            kv[a] = __fmul_rn(qk_s[t][128 + 32 * a + l], ks);
-            qv[a] = __fmul_rn(qk_s[t][32 * a + l], qs);
+        float kv[8], qv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int i = 32 * (e & 3) + l + 16 * (e >> 2);
+            sv[e] = __fmul_rn(sv[e], decay);
+            kv[e] = __fmul_rn(qk_s[t][128 + i], ks);
+            qv[e] = __fmul_rn(qk_s[t][i], qs);
         }
-        float p = 0.0f;
-        for (int a = 0; a < 4; ++a) p = __builtin_fmaf(sv[a], kv[a], p);
-        const float pred = avx2_tree32(p);
-        const float delta = __fmul_rn(__fsub_rn(v_s[t][tid >> 5], pred), beta_s[t]);
+        float pa = 0.0f, pb = 0.0f;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            pa = __builtin_fmaf(sv[a], kv[a], pa);
+            pb = __builtin_fmaf(sv[4 + a], kv[4 + a], pb);
+        }
+        const float pred = avx2_tree16(pa, pb);
+        const float delta = __fmul_rn(__fsub_rn(v_s[t][tid >> 4], pred), beta_s[t]);
         float *s_out = state + (size_t)((slot0 + t + 1) % kStateSlots) * slot_stride + col_off;
-        float r = 0.0f;
+        float ra = 0.0f, rb = 0.0f;
+#pragma unroll
         for (int a = 0; a < 4; ++a) {
             sv[a] = __builtin_fmaf(kv[a], delta, sv[a]);
+            sv[4 + a] = __builtin_fmaf(kv[4 + a], delta, sv[4 + a]);
             s_out[32 * a + l] = sv[a];
-            r = __builtin_fmaf(sv[a], qv[a], r);
+            s_out[32 * a + l + 16] = sv[4 + a];
+            ra = __builtin_fmaf(sv[a], qv[a], ra);
+            rb = __builtin_fmaf(sv[4 + a], qv[4 + a], rb);
         }
-        const float result = avx2_tree32(r);
+        const float result = avx2_tree16(ra, rb);
         if (l == 0) out[(size_t)t * kLinV + h * kHeadDim + c] = __fmul_rn(result, query_scale);
     }
 }
@@ -1319,7 +1318,7 @@ bool launch_deltanet_fused(float *attn, float *delta_state, long long slot_strid
                            const float *ssm_dt, hipStream_t stream)
 {
     if (rows < 1 || rows > kFusedRows) return false;
-    deltanet_fused_kernel<<<kVHeads * kHeadDim / 8, 256, 0, stream>>>(attn, delta_state, slot_stride, slot, rows, qkv,
+    deltanet_fused_kernel<<<kVHeads * kHeadDim / kFusedCols, 256, 0, stream>>>(attn, delta_state, slot_stride, slot, rows, qkv,
                                                                      ld, beta_off, alpha_off, query_scale, conv_state,
                                                                      conv_stride, conv_w, ssm_a, ssm_dt);
     return true;
