@@ -68,12 +68,18 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(
     float bv = __builtin_nanf("");
     uint32_t bi = 0xffffffffu;
     const uint32_t base = chunk * kArgmaxChunk;
+    /* every load first (an element past the row re-reads the last one and
+     * is not compared), so the thread waits for memory once */
+    float x[kArgmaxPerThread];
+#pragma unroll
     for (int i = 0; i < kArgmaxPerThread; ++i) {
         const uint32_t e = base + i * kArgmaxThreads + threadIdx.x;
-        if (e < count) {
-            const float x = v[e];
-            if (better(x, e, bv, bi)) { bv = x; bi = e; }
-        }
+        x[i] = v[e < count ? e : count - 1];
+    }
+#pragma unroll
+    for (int i = 0; i < kArgmaxPerThread; ++i) {
+        const uint32_t e = base + i * kArgmaxThreads + threadIdx.x;
+        if (e < count && better(x[i], e, bv, bi)) { bv = x[i]; bi = e; }
     }
     block_best(bv, bi);
     if (threadIdx.x == 0) {
