@@ -605,6 +605,10 @@ __global__ __launch_bounds__(256) void deltanet_out_quant_kernel(float *__restri
     const int head = 2 * pair + half;
     float *x = attn + (size_t)t * kLinV + head * kHeadDim;
     const float v = x[i];
+    /* the gate and the norm weight do not depend on the sum: loaded (and
+     * the gate's SiLU computed) before it, so one memory wait covers all */
+    const float w = norm_w[i];
+    const float gz = siluf_exact(z[(size_t)t * z_stride + head * kHeadDim + i]);
     double s = (double)__fmul_rn(v, v);
     for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
     if ((tid & 63) == 0) partial[tid >> 6] = s;
@@ -623,8 +627,7 @@ __global__ __launch_bounds__(256) void deltanet_out_quant_kernel(float *__restri
     }
     __syncthreads();
     const float scale = rms_scale(mean_s[half]);
-    const float y = __fmul_rn(__fmul_rn(__fmul_rn(v, scale), norm_w[i]),
-                              siluf_exact(z[(size_t)t * z_stride + head * kHeadDim + i]));
+    const float y = __fmul_rn(__fmul_rn(__fmul_rn(v, scale), w), gz);
     x[i] = y;
     ybuf[tid] = y;
     __syncthreads();
@@ -680,16 +683,19 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float *__restrict__ q_ou
                             : key + (size_t)t * in_stride + h * kAttnDim;
     const float *w = is_q ? q_norm : k_norm;
     const float x = src[i];
+    /* the norm weight and the RoPE pair do not depend on the sum: loaded
+     * before it, so one memory wait covers all */
+    const float wi = w[i];
+    const int pair = i & 31;
+    const float c = i < 64 ? rope[(size_t)pos * 64 + pair] : 0.0f;
+    const float s = i < 64 ? rope[(size_t)pos * 64 + 32 + pair] : 0.0f;
     const float mean = block_sum_finish<256>((double)__fmul_rn(x, x), src, kAttnDim, MeanPost{256.0});
     const float scale = rms_scale(mean);
     __shared__ float v[kAttnDim];
-    v[i] = __fmul_rn(__fmul_rn(x, scale), w[i]);
+    v[i] = __fmul_rn(__fmul_rn(x, scale), wi);
     __syncthreads();
     float y = v[i];
     if (i < 64) {
-        const int pair = i & 31;
-        const float c = rope[(size_t)pos * 64 + pair];
-        const float s = rope[(size_t)pos * 64 + 32 + pair];
         const float x0 = v[pair], x1 = v[pair + 32];
         y = i < 32 ? __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s))
                    : __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
