@@ -94,6 +94,8 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(
     const uint32_t *__restrict__ pi, uint32_t nchunks, uint32_t *__restrict__ out)
 {
     const uint32_t row = blockIdx.x;
+    /* the row's first element (the NaN rule) is read with the partials */
+    const float first = values[static_cast<size_t>(row) * count];
     float bv = __builtin_nanf("");
     uint32_t bi = 0xffffffffu;
     for (uint32_t c = threadIdx.x; c < nchunks; c += kArgmaxThreads) {
@@ -102,10 +104,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(
         if (better(x, i, bv, bi)) { bv = x; bi = i; }
     }
     block_best(bv, bi);
-    if (threadIdx.x == 0) {
-        const float first = values[static_cast<size_t>(row) * count];
-        out[row] = (first != first || bi == 0xffffffffu) ? 0u : bi;
-    }
+    if (threadIdx.x == 0) out[row] = (first != first || bi == 0xffffffffu) ? 0u : bi;
 }
 
 /* Greedy acceptance (src/qwen38/qwen38_model.c:1662-1702): the leading
@@ -211,6 +210,7 @@ __global__ __launch_bounds__(256) void verify_tail_kernel(const float *__restric
     __shared__ uint32_t tgt[kTailMaxRows];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (uint32_t r = wave; r < rows; r += 4) {
+        const float first = values[(size_t)r * count];   /* read with the partials */
         float bv = __builtin_nanf("");
         uint32_t bi = 0xffffffffu;
         for (uint32_t c = lane; c < nchunks; c += 64) {
@@ -223,10 +223,7 @@ __global__ __launch_bounds__(256) void verify_tail_kernel(const float *__restric
             const uint32_t oi = __shfl_xor(bi, off, 64);
             if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
         }
-        if (lane == 0) {
-            const float first = values[(size_t)r * count];
-            tgt[r] = (first != first || bi == 0xffffffffu) ? 0u : bi;
-        }
+        if (lane == 0) tgt[r] = (first != first || bi == 0xffffffffu) ? 0u : bi;
     }
     __syncthreads();
     /* acceptance (src/qwen38/qwen38_model.c:1640-1702), as accept_kernel */

@@ -1176,10 +1176,12 @@ __global__ __launch_bounds__(128) void attn_mix_kernel(float *__restrict__ out, 
         mix_wait_vmcnt<0>();
         return;
     }
-    /* chain wavefront: one barrier per chunk, as the streaming wavefront */
+    /* chain wavefront: one barrier per chunk, as the streaming wavefront;
+     * the gate is read before the chain so that its load is not waited
+     * for after it */
+    const float g = q_and_gate[(size_t)t * qg_stride + h * 2 * kAttnDim + kAttnDim + 64 * slice + lane];
     const float o = mix_chain(ring, kMixSlotBytes, n, lane, 0);
     const int dim = h * kAttnDim + 64 * slice + lane;
-    const float g = q_and_gate[(size_t)t * qg_stride + h * 2 * kAttnDim + kAttnDim + 64 * slice + lane];
     out[(size_t)t * kQDim + dim] = __fmul_rn(o, sigmoidf_exact(g));
 }
 
