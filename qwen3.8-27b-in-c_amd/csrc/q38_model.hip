@@ -514,6 +514,12 @@ __global__ __launch_bounds__(256) void deltanet_fused_kernel(float *__restrict__
         sv[a] = s[32 * a + l];
         sv[4 + a] = s[32 * a + l + 16];
     }
+    /* beta / alpha inputs of row tid - 64 (threads 64 .. 64 + rows - 1 use
+     * them; the others read a row of the batch too), requested with the
+     * state, ahead of the conv */
+    const float *brow = qkv + (long long)(tid < 64 ? 0 : (tid - 64 < rows ? tid - 64 : rows - 1)) * ld;
+    const float beta_in = brow[beta_off + h], alpha_in = brow[alpha_off + h];
+    const float a_h = ssm_a[h], dt_h = ssm_dt[h];
 
     /* prep (deltanet_prep_kernel, qwen38_model.c:720-757) */
     const int ch = tid < 128 ? kh * kHeadDim + tid : kQKDim + kh * kHeadDim + (tid - 128);
@@ -523,12 +529,10 @@ __global__ __launch_bounds__(256) void deltanet_fused_kernel(float *__restrict__
         conv_silu_rows(&v_s[0][tid], kFusedCols, qkv, ld, 2 * kQKDim + h * kHeadDim + cg * kFusedCols + tid,
                        conv_state, conv_state, conv_stride, slot0, rows, conv_w);
     if (tid >= 64 && tid < 64 + rows) {
-        const float *row = qkv + (long long)(tid - 64) * ld;
-        beta_s[tid - 64] = sigmoidf_exact(row[beta_off + h]);
+        beta_s[tid - 64] = sigmoidf_exact(beta_in);
         /* the row's decay expf(alpha), here in parallel rather than on the
          * state update's dependent chain */
-        alpha_s[tid - 64] =
-            q38_expf(__fmul_rn(ssm_a[h], softplusf_exact(__fadd_rn(row[alpha_off + h], ssm_dt[h]))));
+        alpha_s[tid - 64] = q38_expf(__fmul_rn(a_h, softplusf_exact(__fadd_rn(alpha_in, dt_h))));
     }
     /* L2 norms of q and k per row: the double sum of squares of each
      * 128-vector as block_sum_finish (two wavefronts each) */
