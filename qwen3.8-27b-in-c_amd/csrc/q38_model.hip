@@ -198,9 +198,9 @@ constexpr int kScanChunk = 16;
  * with H[j] = Q[j] + Q[j+4], Q[j] = (P0[j]+P2[j]) + (P1[j]+P3[j]).  A column
  * runs on a 16-lane row: lane l = 8a + j (a = 0, 1) holds P_a[j] in `a` and
  * P_{a+2}[j] in `b`, so the first pair is added inside the lane; each later
- * step is a butterfly that adds the partner lane holding the other operand
- * of the reference's pair (row_ror 8: lane l ^ 8, row_ror 4 and the quad
- * permutations: l ^ 4, l ^ 1, l ^ 2).  Lane 0 adds exactly the reference's
+ * step adds a lane holding the other operand of the reference's pair (row_ror
+ * 8: lane l ^ 8; row_ror 4: lane (l - 4) mod 16, which then holds the value
+ * of j ^ 4; the quad permutations: lanes l ^ 1 and l ^ 2).  Lane 0 adds exactly the reference's
  * operand pairs in its order; every other lane adds the same pairs, some
  * with the operands swapped, which rounds to the same float, so every lane
  * of the row ends with the sum. */
